@@ -1,0 +1,207 @@
+/*
+ * ds355 — MI355X (gfx950) DiffSpec draft-context retrieval: C ABI.
+ *
+ * One shared library, libds355.so, built from hand-written HIP kernels.
+ * Every entry point:
+ *   - takes plain device pointers, element strides and sizes (no torch types);
+ *   - launches asynchronously on the caller's HIP stream and never
+ *     synchronises the host, never reads device values back and never
+ *     allocates device memory (all buffers are owned by the caller);
+ *   - returns 0 on success or a DS_ERR_* code; ds_last_error() then holds a
+ *     message (thread-local, valid until the next call on that thread).
+ * Strides are in elements, not bytes.  Reference citations are relative to
+ * the vllm-ascend-hust-diffspec repository root.
+ */
+#ifndef DS355_H
+#define DS355_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* ds_stream_t; /* == hipStream_t */
+
+enum ds_dtype { DS_BF16 = 0, DS_FP16 = 1, DS_FP32 = 2 };
+
+enum ds_status {
+  DS_OK = 0,
+  DS_ERR_INVALID = 1,     /* argument / shape check failed            */
+  DS_ERR_UNSUPPORTED = 2, /* valid but outside what the kernels cover */
+  DS_ERR_HIP = 3          /* a HIP runtime call failed                */
+};
+
+enum ds_head_reduce { DS_HEAD_MEAN = 0, DS_HEAD_MAX = 1 };
+
+/* Message for the last failed call on this thread ("" after success). */
+const char* ds_last_error(void);
+
+/* ABI version, bumped on any signature change. */
+int ds_abi_version(void);
+
+/*
+ * Paged chunk scores.
+ * Replaces paged_chunk_attention_scores (diffspec/kernels.py:95-150) and its
+ * Triton kernel (diffspec/kernels.py:11-92).
+ *
+ *   out[b, c] = reduce_h( sum_{t in chunk c, t < seq_lens[b]}
+ *                           exp(scale * q[b,h] . k[t, h / (Hq/Hkv)] - lse[b,h]) )
+ *               / max(n_valid(b, c), 1)
+ * with reduce_h = mean over the Hq query heads (the reference) or max over
+ * heads per token (DS_HEAD_MAX).  Keys are read through
+ * block_table[b * bt_stride + t / block_size].  out is [batch, max_chunks]
+ * fp32 with row stride out_stride; chunks at or beyond ceil(seq_lens[b] /
+ * chunk) are written as 0, as the reference does.
+ *
+ * query   : [batch, Hq, head_dim], token stride q_stride, head stride head_dim.
+ * lse     : fp32, element (b, h) at lse[b * lse_row_stride + h * lse_head_stride].
+ * key_cache: element (block, i, kvh, d) at
+ *            k[block * k_block_stride + i * k_token_stride + kvh * k_head_stride + d].
+ * dtype   : DS_BF16 or DS_FP16 (query and key_cache share it).
+ * Limits  : head_dim % 32 == 0 and <= 256, Hq % Hkv == 0, Hq / Hkv <= 16,
+ *           batch <= 1024.
+ */
+int ds_chunk_scores(ds_stream_t stream, int dtype,
+                    const void* query, int64_t q_stride,
+                    const void* key_cache, int64_t k_block_stride,
+                    int64_t k_token_stride, int64_t k_head_stride,
+                    const float* lse, int64_t lse_row_stride, int64_t lse_head_stride,
+                    const int32_t* block_table, int64_t bt_stride,
+                    const int32_t* seq_lens,
+                    int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                    int block_size, int chunk_size, int max_chunks, float scale,
+                    int head_reduce, float* out, int64_t out_stride);
+
+/*
+ * Batched top-k chunk selection.
+ * Replaces select_context_chunks (diffspec/runtime.py:348-414), called per
+ * row from runtime.py:1298-1308, as one launch over all rows.
+ *
+ * For row b with C = ceil(seq_lens[b] / chunk) and K = history_budget / chunk:
+ * C <= K selects 0..C-1; otherwise the newest chunk C-1 plus the K-1 highest
+ * scores of chunks 0..C-2 (equal scores: the lower chunk index wins), all in
+ * ascending order.  Writes ids[b * ids_stride + j] for j < counts[b] and
+ * counts[b].  ids_stride >= K.  seq_lens[b] is clamped to score_cols * chunk
+ * (the columns the score buffer holds).  Limits: K <= 2048, batch <= 65535.
+ */
+int ds_select_chunks(ds_stream_t stream,
+                     const float* scores, int64_t score_stride, int score_cols,
+                     const int32_t* seq_lens, int batch,
+                     int chunk_size, int history_budget,
+                     int32_t* ids, int64_t ids_stride, int32_t* counts);
+
+/*
+ * History plans from per-slot selections.
+ * Replaces _history_plan_host + the plan tensor build
+ * (diffspec/runtime.py:1713-1757) without host round trips.
+ *
+ * Row r uses slot = slots[r] and history_end = max(0, committed_lens[r] - 1).
+ * sel_count[slot] < 0 means "no selection" (window of the last
+ * history_budget tokens), 0 an empty selection, > 0 the number of sorted
+ * chunk ids at sel_ids[slot * sel_stride].  The rolling tail is
+ * min(history_end, recent_window, history_budget) tokens (recent_window ==
+ * chunk_size is the reference).  plan is [rows, plan_width] int64:
+ * [slot, history_len, tail_start, prefix_len, prefix_drop, chunk_ids..., 0...]
+ * (diffspec/compact_kv.py:197-205); plan_width = 5 + token_budget / chunk.
+ * working_lens[slot] = history_len when working_lens is not NULL.
+ * Rows with slots[r] outside [0, num_slots) are padding: plan row of zeros,
+ * no other write.
+ */
+int ds_build_plan(ds_stream_t stream,
+                  const int32_t* sel_ids, int64_t sel_stride, const int32_t* sel_count,
+                  int num_slots, const int32_t* slots, const int32_t* committed_lens, int rows,
+                  int chunk_size, int history_budget, int recent_window,
+                  int64_t* plan, int plan_width, int32_t* working_lens);
+
+/*
+ * Gather + local-position RoPE + working-cache write from plans.
+ * Replaces rebuild_compact_kv_from_plan (diffspec/compact_kv.py:184-242) and
+ * its Triton kernel (diffspec/compact_kv.py:8-133).
+ *
+ * raw  : [num_slots, max_model_len, heads, head_dim] (contiguous).
+ * work : [num_slots, heads, token_budget, head_dim] (contiguous).
+ * plan : [rows, plan_width] int64 (format above), contiguous.
+ * cos_sin: [cs_rows, >= rotary_dim], row stride cs_stride; cos at [p, i],
+ *          sin at [p, rotary_dim/2 + i].
+ * For each row and local position p < min(history_len, roundup16(max_width)):
+ * K[:rotary_dim] rotated at position p in fp32 (neox halves or GPT-J pairs),
+ * K[rotary_dim:] and V copied.  Nothing else is written.  row_active, if not
+ * NULL, skips rows with row_active[r] == 0.  dtype: DS_BF16/FP16/FP32.
+ */
+int ds_rebuild_compact_kv(ds_stream_t stream, int dtype,
+                          const void* raw_key, const void* raw_value,
+                          void* working_key, void* working_value,
+                          const int64_t* plan, int rows, int plan_width,
+                          const void* cos_sin, int64_t cs_stride, int cs_rows,
+                          int num_slots, int max_model_len, int heads, int head_dim,
+                          int token_budget, int chunk_size, int rotary_dim,
+                          int is_neox_style, int max_width, const int32_t* row_active);
+
+/*
+ * One fused retrieval step (no reference counterpart as a single call; it is
+ * runtime.py:1211-1308 + 1737-1765 + compact_kv.py as one launch chain):
+ *   DS_STAGE_SCORE : score rows with counts > 0 (committed query, rejected
+ *                    suffix cut; rows >= batch_size are padding)
+ *   DS_STAGE_SELECT: select into the per-slot state (rows with counts > 0)
+ *   DS_STAGE_PLAN  : plan row for every row from the slot state, then
+ *                    gather / RoPE / write
+ * `stages` is a bit mask; all three = one retrieval step.  SELECT and PLAN
+ * share one kernel launch.  At most three kernels on `stream`, no host
+ * synchronisation, launch shapes fixed by the descriptor's upper bounds
+ * (graph-capturable).
+ */
+enum ds_stage { DS_STAGE_SCORE = 1, DS_STAGE_SELECT = 2, DS_STAGE_PLAN = 4, DS_STAGE_ALL = 7 };
+
+typedef struct ds_step_desc {
+  /* verifier snapshot (scoring) */
+  int dtype;                         /* DS_BF16 / DS_FP16                     */
+  const void* query;                 /* [num_query_tokens, Hq, D]             */
+  int64_t q_stride;                  /* elements between query tokens         */
+  const float* lse;                  /* (token, h) at lse[t*lse_token_stride + h*lse_head_stride] */
+  int64_t lse_token_stride, lse_head_stride;
+  const void* key_cache;             /* paged target keys                     */
+  int64_t k_block_stride, k_token_stride, k_head_stride;
+  int block_size;
+  const int32_t* block_table;        /* [batch_rows, *] row stride bt_stride  */
+  int64_t bt_stride;
+  const int32_t* counts;             /* [batch_rows] committed tokens (0 = none) */
+  const int32_t* query_start;        /* [batch_rows] first query token of row */
+  const int32_t* query_len;          /* [batch_rows] query tokens of row      */
+  const int32_t* target_len;         /* [batch_rows] verifier KV length       */
+  int batch_rows;                    /* rows in the (padded) batch            */
+  int batch_size;                    /* real rows; rows >= batch_size are padding */
+  int num_q_heads, num_kv_heads, head_dim;
+  float scale;
+  int max_chunks;                    /* >= ceil(max scored length / chunk)    */
+  float* scores;                     /* [batch_rows, max_chunks] scratch out  */
+  int stages;                        /* DS_STAGE_* bit mask                   */
+  /* selection state, per slot */
+  int32_t* sel_ids;                  /* [num_slots, sel_stride]               */
+  int64_t sel_stride;                /* >= token_budget / chunk               */
+  int32_t* sel_count;                /* [num_slots]  -1 none / 0 empty / n    */
+  const int32_t* slots;              /* [batch_rows] canonical slot per row, -1 padding */
+  /* plan */
+  const int32_t* committed_lens;     /* [batch_rows] root position + 1        */
+  int64_t* plan;                     /* [batch_rows, plan_width]              */
+  int plan_width;
+  int32_t* working_lens;             /* [num_slots] or NULL                   */
+  /* draft raw / working caches */
+  int kv_dtype;                      /* DS_BF16 / DS_FP16 / DS_FP32           */
+  const void* raw_key; const void* raw_value;
+  void* working_key; void* working_value;
+  int num_slots, max_model_len, draft_heads, draft_head_dim, token_budget;
+  const void* cos_sin; int64_t cs_stride; int cs_rows;
+  int rotary_dim, is_neox_style;
+  const int32_t* row_active;         /* [batch_rows] or NULL: rows to re-gather */
+  /* policy */
+  int chunk_size, history_budget, recent_window;
+} ds_step_desc;
+
+int ds_retrieval_step(ds_stream_t stream, const ds_step_desc* desc);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DS355_H */

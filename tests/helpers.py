@@ -1,0 +1,76 @@
+"""Shared input generators for the parity tests (seeded, CPU-side)."""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from oracle import diffspec_oracle as O
+
+
+def gen(seed: int) -> torch.Generator:
+    return torch.Generator().manual_seed(seed)
+
+
+def randn(shape, dtype, g) -> torch.Tensor:
+    return torch.randn(shape, generator=g, dtype=torch.float32).to(dtype)
+
+
+def rope_table_recipe(rotary_dim: int, rows: int = 128, dtype=torch.bfloat16) -> torch.Tensor:
+    """cos/sin recipe of the reference's batched-rebuild device test
+    (tests/test_linear_attention_batch_npu.py:32-33): phases = p * (1..rot/2) / 1000."""
+    phases = torch.arange(rows, dtype=torch.float32)[:, None] * torch.arange(1, rotary_dim // 2 + 1)[None, :] / 1000
+    return torch.cat((phases.cos(), phases.sin()), -1).to(dtype)
+
+
+def paged_keys(lengths, num_kv_heads, head_dim, block_size, dtype, g, extra_blocks=3):
+    """Paged K with a shuffled page order: returns (key_cache, block_table int32)."""
+    pages = [(n + block_size - 1) // block_size for n in lengths]
+    total = sum(pages) + extra_blocks
+    key_cache = randn((total, block_size, num_kv_heads, head_dim), dtype, g)
+    perm = torch.randperm(total, generator=g)
+    width = max(max(pages), 1)
+    table = torch.zeros((len(lengths), width), dtype=torch.int32)
+    k = 0
+    for b, p in enumerate(pages):
+        table[b, :p] = perm[k:k + p].to(torch.int32)
+        k += p
+    return key_cache, table
+
+
+def lse_for(query, key_cache, table, lengths, scale):
+    """Exact per-head logsumexp over each row's keys, fp32 ``[B, Hq]``."""
+    batch, hq, d = query.shape
+    _, bs, hkv, _ = key_cache.shape
+    out = torch.zeros((batch, hq), dtype=torch.float32)
+    for b, n in enumerate(lengths):
+        if n <= 0:
+            continue
+        pages = (n + bs - 1) // bs
+        dense = key_cache[table[b, :pages].long()].reshape(-1, hkv, d)[:n].float()
+        grouped = query[b].float().reshape(hkv, hq // hkv, d)
+        logits = torch.einsum("hgd,thd->hgt", grouped, dense).reshape(hq, n) * scale
+        out[b] = torch.logsumexp(logits, dim=-1)
+    return out
+
+
+def uniform_lengths(n, lo, hi, g):
+    return [int(x) for x in torch.randint(lo, hi + 1, (n,), generator=g)]
+
+
+def max_ulp_bf16(a: torch.Tensor, b: torch.Tensor) -> int:
+    """Largest distance in bf16 units in the last place (same-sign values)."""
+    ai = a.contiguous().view(torch.int16).to(torch.int32)
+    bi = b.contiguous().view(torch.int16).to(torch.int32)
+    ai = torch.where(ai < 0, -(ai & 0x7FFF), ai)
+    bi = torch.where(bi < 0, -(bi & 0x7FFF), bi)
+    return int((ai - bi).abs().max()) if a.numel() else 0
+
+
+def default_scale(head_dim: int) -> float:
+    return 1.0 / math.sqrt(head_dim)
+
+
+__all__ = ["O", "gen", "randn", "rope_table_recipe", "paged_keys", "lse_for", "uniform_lengths",
+           "max_ulp_bf16", "default_scale"]

@@ -1,0 +1,234 @@
+"""GPU parity: one retrieval step through ds_retrieval_step (score -> select -> plan -> gather).
+
+Each case builds a verifier batch the way the plugin sees it (query tokens
+per row, committed counts, graph-padding rows, paged target K, permuted
+canonical slots) and checks every stage against the oracle:
+  scores      within rtol 1e-3 (atol 1e-6);
+  selection   bit-exact, judged on identical score inputs (the GPU's scores);
+  plans       bit-exact;
+  working KV  bit-exact (RoPE'd K within 1 bf16 ulp is the contract), and
+              untouched (NaN) outside each row's history.
+"""
+
+import pytest
+import torch
+
+from helpers import O, default_scale, gen, max_ulp_bf16, paged_keys, randn
+
+pytestmark = pytest.mark.gpu
+
+
+def build_case(seed, *, real_rows, pad_rows, target_lens, query_len, counts, hq, hkv, head_dim, chunk,
+               token_budget, block_size, lmax, slots, num_slots, depth=4, prev_counts=None):
+    g = gen(seed)
+    rows = real_rows + pad_rows
+    qlens = [query_len] * real_rows + [1] * pad_rows
+    tlens = list(target_lens) + [1] * pad_rows
+    ends = [sum(qlens[: i + 1]) for i in range(rows)]
+    starts = [0, *ends[:-1]]
+    tokens = ends[-1]
+    query = randn((tokens, hq, head_dim), torch.bfloat16, g)
+    lse = torch.randn((tokens, hq), generator=g)
+    key_cache, table = paged_keys(tlens, hkv, head_dim, block_size, torch.bfloat16, g)
+    scale = default_scale(head_dim)
+    # Exact LSE for each committed query over its causal prefix.
+    _, q_index, lengths = O.retrieval_rows(counts, ends, tlens, real_rows)
+    scored_rows = [i for i in range(real_rows) if counts[i] > 0]
+    from helpers import lse_for
+    exact = lse_for(query[q_index], key_cache, table[scored_rows], lengths, scale)
+    for j, qi in enumerate(q_index):
+        lse[qi] = exact[j]
+    raw_k = randn((num_slots, lmax, hkv, head_dim), torch.bfloat16, g)
+    raw_v = randn((num_slots, lmax, hkv, head_dim), torch.bfloat16, g)
+    budget = O.history_budget(token_budget, depth, chunk)
+    return dict(
+        query=query, lse=lse, key_cache=key_cache, table=table, scale=scale, counts=counts + [0] * pad_rows,
+        starts=starts, qlens=qlens, tlens=tlens, ends=ends, rows=rows, real_rows=real_rows,
+        slots=slots + [-1] * pad_rows, num_slots=num_slots, raw_k=raw_k, raw_v=raw_v, chunk=chunk,
+        token_budget=token_budget, budget=budget, hq=hq, hkv=hkv, head_dim=head_dim, lmax=lmax,
+        committed=[tl - ql + min(max(c, 1), ql) for tl, ql, c in zip(tlens, qlens, counts + [0] * pad_rows)],
+        cos_sin=O.rope_cos_sin_cache(head_dim, token_budget),
+    )
+
+
+def run_gpu(case, device, *, stages=None, state=None, row_active=None):
+    from ds355 import step
+
+    i32 = lambda xs: torch.tensor(xs, dtype=torch.int32, device=device)  # noqa: E731
+    rows = case["rows"]
+    max_chunks = (max(case["tlens"]) + case["chunk"] - 1) // case["chunk"]
+    if state is None:
+        state = dict(
+            scores=torch.zeros((rows, max_chunks), dtype=torch.float32, device=device),
+            sel_ids=torch.zeros((case["num_slots"], case["token_budget"] // case["chunk"]), dtype=torch.int32,
+                                device=device),
+            sel_count=torch.full((case["num_slots"],), -1, dtype=torch.int32, device=device),
+            plan=torch.zeros((rows, 5 + case["token_budget"] // case["chunk"]), dtype=torch.int64, device=device),
+            working_lens=torch.zeros((case["num_slots"],), dtype=torch.int32, device=device),
+            work_k=torch.full((case["num_slots"], case["hkv"], case["token_budget"], case["head_dim"]),
+                              float("nan"), dtype=torch.bfloat16, device=device),
+            raw_k=case["raw_k"].to(device), raw_v=case["raw_v"].to(device),
+            query=case["query"].to(device), lse=case["lse"].to(device), key_cache=case["key_cache"].to(device),
+            table=case["table"].to(device), cos_sin=case["cos_sin"].to(device),
+        )
+        state["work_v"] = torch.full_like(state["work_k"], float("nan"))
+    step.retrieval_step(
+        stages=step.ALL if stages is None else stages,
+        snapshot=step.VerifierSnapshot(state["query"], state["lse"], state["key_cache"], state["table"],
+                                       case["scale"]),
+        rows=step.VerifierRows(i32(case["counts"]), i32(case["starts"]), i32(case["qlens"]), i32(case["tlens"]),
+                               case["real_rows"]),
+        scores=state["scores"], sel_ids=state["sel_ids"], sel_count=state["sel_count"], slots=i32(case["slots"]),
+        committed_lens=i32(case["committed"]), plan=state["plan"], working_lens=state["working_lens"],
+        raw_key=state["raw_k"], raw_value=state["raw_v"], working_key=state["work_k"],
+        working_value=state["work_v"], cos_sin_cache=state["cos_sin"], rotary_dim=case["head_dim"],
+        is_neox_style=True, chunk_size=case["chunk"], history_budget=case["budget"],
+        row_active=None if row_active is None else i32(row_active),
+    )
+    torch.cuda.synchronize()
+    return state
+
+
+def check_step(case, state, *, previous=None, row_active=None):
+    chunk, budget = case["chunk"], case["budget"]
+    real = case["real_rows"]
+    rows_idx, q_index, lengths = O.retrieval_rows(case["counts"], case["ends"], case["tlens"], real)
+    gpu_scores = state["scores"].cpu()
+    expected_scores = O.paged_chunk_attention_scores(
+        case["query"][q_index], case["key_cache"], case["lse"][q_index], case["table"][rows_idx],
+        torch.tensor(lengths), chunk_size=chunk, max_seq_len=max(lengths), scale=case["scale"])
+    for j, b in enumerate(rows_idx):
+        c = (lengths[j] + chunk - 1) // chunk
+        torch.testing.assert_close(gpu_scores[b, :c], expected_scores[j, :c], rtol=1e-3, atol=1e-6)
+    # Selection on identical (GPU) scores: bit-exact.
+    selections = dict(previous or {})
+    for j, b in enumerate(rows_idx):
+        c = (lengths[j] + chunk - 1) // chunk
+        sel = O.select_context_chunks(gpu_scores[b, :c].contiguous(), lengths[j], chunk, budget)
+        selections[case["slots"][b]] = sel.chunk_indices.tolist()
+    sel_count = state["sel_count"].cpu()
+    sel_ids = state["sel_ids"].cpu()
+    for slot, chunks in selections.items():
+        assert int(sel_count[slot]) == len(chunks), slot
+        assert sel_ids[slot, : len(chunks)].tolist() == chunks, slot
+    # Plans, bit-exact; padding rows are all zero.
+    plans = []
+    for b in range(case["rows"]):
+        slot = case["slots"][b]
+        if slot < 0:
+            assert state["plan"][b].abs().sum().item() == 0
+            plans.append([0, 0, 0, 0, 0])
+            continue
+        plans.append(O.history_plan(slot, selections.get(slot), max(0, case["committed"][b] - 1), chunk, budget))
+    expected_plan = O.pad_plan(plans, case["token_budget"], chunk)
+    assert torch.equal(state["plan"].cpu(), expected_plan)
+    # Working cache.
+    exp_k = torch.full(tuple(state["work_k"].shape), float("nan"), dtype=torch.bfloat16)
+    exp_v = exp_k.clone()
+    width = max(p[1] for p in plans)
+    O.rebuild_compact_kv_from_plan(case["raw_k"], case["raw_v"], exp_k, exp_v, expected_plan, case["cos_sin"],
+                                   chunk_size=chunk, max_width=width, rotary_dim=case["head_dim"],
+                                   is_neox_style=True, row_active=row_active)
+    got_k, got_v = state["work_k"].cpu(), state["work_v"].cpu()
+    assert torch.equal(got_k.isnan(), exp_k.isnan())
+    assert torch.equal(torch.nan_to_num(got_v), torch.nan_to_num(exp_v))
+    assert max_ulp_bf16(torch.nan_to_num(got_k), torch.nan_to_num(exp_k)) <= 1
+    assert torch.equal(torch.nan_to_num(got_k), torch.nan_to_num(exp_k))
+    return selections
+
+
+def test_single_request_8k(cuda):
+    """One request, 8192 tokens, chunk 64, budget 2048 (K = 4 gives 1984 history tokens)."""
+    case = build_case(0, real_rows=1, pad_rows=0, target_lens=[8192], query_len=1, counts=[1], hq=32, hkv=4,
+                      head_dim=128, chunk=64, token_budget=2048, block_size=128, lmax=8192, slots=[0], num_slots=1)
+    state = run_gpu(case, cuda)
+    check_step(case, state)
+
+
+def test_ragged_16_requests_40k(cuda):
+    """16 requests, L ~ U[4096, 40960], contiguous slots in request order."""
+    g = gen(1)
+    lens = [int(x) for x in torch.randint(4096, 40961, (16,), generator=g)]
+    case = build_case(1, real_rows=16, pad_rows=0, target_lens=lens, query_len=1, counts=[1] * 16, hq=32, hkv=4,
+                      head_dim=128, chunk=64, token_budget=2048, block_size=128, lmax=40960,
+                      slots=list(range(16)), num_slots=16)
+    state = run_gpu(case, cuda)
+    check_step(case, state)
+
+
+def test_spec_decode_mask_padding_and_permuted_slots(cuda):
+    """Batch 16 + 16 graph-padding rows, K = 4 draft tail with accepted 0..4, random slot permutation."""
+    g = gen(4)
+    lens = [int(x) for x in torch.randint(8192, 40961, (16,), generator=g)]
+    accepted = [int(x) for x in torch.randint(0, 5, (16,), generator=g)]
+    counts = [a + 1 for a in accepted]
+    slots = [int(x) for x in torch.randperm(16, generator=g)]
+    case = build_case(4, real_rows=16, pad_rows=16, target_lens=lens, query_len=5, counts=counts, hq=32, hkv=4,
+                      head_dim=128, chunk=64, token_budget=2048, block_size=128, lmax=40960, slots=slots,
+                      num_slots=16)
+    state = run_gpu(case, cuda)
+    check_step(case, state)
+
+
+def test_zero_count_rows_keep_previous_selection(cuda):
+    """Rows that committed nothing are not scored and keep their last selection (runtime.py:1254)."""
+    g = gen(6)
+    lens = [int(x) for x in torch.randint(3000, 9000, (6,), generator=g)]
+    case = build_case(6, real_rows=6, pad_rows=2, target_lens=lens, query_len=5, counts=[1, 2, 3, 4, 5, 1],
+                      hq=16, hkv=2, head_dim=64, chunk=32, token_budget=1024, block_size=64, lmax=9000,
+                      slots=[5, 3, 1, 0, 2, 4], num_slots=6)
+    state = run_gpu(case, cuda)
+    first = check_step(case, state)
+    # Next cycle: rows 1 and 4 commit nothing; the others advance by their count.
+    case2 = dict(case)
+    case2["counts"] = [2, 0, 1, 3, 0, 5, 0, 0]
+    case2["committed"] = [tl - ql + min(max(c, 1), ql) for tl, ql, c in
+                          zip(case["tlens"], case["qlens"], case2["counts"])]
+    state = run_gpu(case2, cuda, state=state)
+    check_step(case2, state, previous=first)
+
+
+def test_stress_64_rows_reuse_half(cuda):
+    """64 rows, 8 KV heads / 64 q heads, chunk 128, budget 4096; half the rows keep their working rows."""
+    g = gen(5)
+    lens = [int(x) for x in torch.randint(2048, 6145, (64,), generator=g)]
+    case = build_case(5, real_rows=64, pad_rows=0, target_lens=lens, query_len=1, counts=[1] * 64, hq=64, hkv=8,
+                      head_dim=128, chunk=128, token_budget=4096, block_size=256, lmax=6144,
+                      slots=list(range(64)), num_slots=64)
+    state = run_gpu(case, cuda)
+    check_step(case, state)
+    full_k, full_v = state["work_k"].clone(), state["work_v"].clone()
+    # Same step again with a random half flagged for reuse: the result must not change.
+    active = [int(x) for x in (torch.rand(64, generator=g) < 0.5)]
+    state["work_k"][torch.tensor([i for i in range(64) if not active[i]], dtype=torch.long)] = full_k[
+        torch.tensor([i for i in range(64) if not active[i]], dtype=torch.long)]
+    run_gpu(case, cuda, state=state, row_active=active)
+    assert torch.equal(state["work_k"], full_k)
+    assert torch.equal(state["work_v"], full_v)
+    # Re-gathered rows really are rewritten; reused rows are not touched.
+    state["work_k"].fill_(float("nan"))
+    state["work_v"].fill_(float("nan"))
+    run_gpu(case, cuda, state=state, row_active=active)
+    for b in range(64):
+        n = int(state["plan"][b, 1])
+        if active[b]:
+            assert torch.equal(state["work_k"][b, :, :n], full_k[b, :, :n])
+        else:
+            assert torch.isnan(state["work_k"][b]).all()
+
+
+def test_stage_split_equals_full_chain(cuda):
+    """SCORE | SELECT then PLAN (the runtime's two call sites) equals the one-call chain."""
+    from ds355 import step
+
+    g = gen(7)
+    lens = [int(x) for x in torch.randint(1000, 20000, (8,), generator=g)]
+    case = build_case(7, real_rows=8, pad_rows=0, target_lens=lens, query_len=5, counts=[5, 1, 2, 3, 4, 5, 1, 2],
+                      hq=32, hkv=4, head_dim=128, chunk=64, token_budget=2048, block_size=128, lmax=20000,
+                      slots=[7, 6, 5, 4, 3, 2, 1, 0], num_slots=8)
+    full = run_gpu(case, cuda)
+    split = run_gpu(case, cuda, stages=step.SCORE | step.SELECT)
+    assert torch.isnan(split["work_k"]).all()
+    run_gpu(case, cuda, stages=step.PLAN, state=split)
+    for key in ("scores", "sel_ids", "sel_count", "plan", "working_lens", "work_k", "work_v"):
+        assert torch.equal(torch.nan_to_num(split[key]), torch.nan_to_num(full[key])), key

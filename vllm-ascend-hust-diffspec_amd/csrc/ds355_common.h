@@ -1,0 +1,153 @@
+// Shared device helpers and host-side error plumbing for libds355.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+#include <climits>
+
+#include "../../include/ds355.h"
+
+namespace ds355 {
+
+// ---------------------------------------------------------------------------
+// Host: thread-local error message and argument checks.
+// ---------------------------------------------------------------------------
+int set_error(int code, const char* fmt, ...);
+int clear_error();
+int check_launch(const char* what);
+
+#define DS_REQUIRE(cond, ...)                              \
+  do {                                                     \
+    if (!(cond)) return ::ds355::set_error(DS_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+#define DS_SUPPORTED(cond, ...)                            \
+  do {                                                     \
+    if (!(cond)) return ::ds355::set_error(DS_ERR_UNSUPPORTED, __VA_ARGS__); \
+  } while (0)
+
+// Compute units of the current device (cached per device).
+int device_cu_count();
+
+// Upper bound on rows handled by one launch (LDS prefix arrays).
+constexpr int kMaxRows = 1024;
+
+// ---------------------------------------------------------------------------
+// Device: element conversions.  bf16 / fp16 are carried as raw 16-bit words.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// fp32 -> bf16, round to nearest even; NaN -> 0x7fc0 (the CPU oracle's rule).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// fp32 -> fp16, IEEE round to nearest even.
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Element traits: storage word, widening to fp32 and rounding back.
+template <int DT> struct Elem;
+template <> struct Elem<DS_BF16> {
+  using T = uint16_t;
+  static __device__ __forceinline__ float load(T v) { return bf16_to_f32(v); }
+  static __device__ __forceinline__ T store(float f) { return f32_to_bf16(f); }
+};
+template <> struct Elem<DS_FP16> {
+  using T = uint16_t;
+  static __device__ __forceinline__ float load(T v) { return f16_to_f32(v); }
+  static __device__ __forceinline__ T store(float f) { return f32_to_f16(f); }
+};
+template <> struct Elem<DS_FP32> {
+  using T = float;
+  static __device__ __forceinline__ float load(T v) { return v; }
+  static __device__ __forceinline__ T store(float f) { return f; }
+};
+
+// ---------------------------------------------------------------------------
+// Device: wave64 reductions and block-wide exclusive scan over 256 threads.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Inclusive scan within the wave (lane order).
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    int n = __shfl_up(v, off, 64);
+    if (lane >= off) v += n;
+  }
+  return v;
+}
+
+// Exclusive scan over a 256-thread block; `total` receives the block sum.
+// Uses scratch[4]; contains two barriers.
+__device__ __forceinline__ int block_exclusive_scan(int v, int* scratch, int& total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int inc = wave_inclusive_scan(v);
+  if (lane == 63) scratch[wave] = inc;
+  __syncthreads();
+  int base = 0;
+  total = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    int s = scratch[w];
+    if (w < wave) base += s;
+    total += s;
+  }
+  __syncthreads();
+  return base + inc - v;
+}
+
+// Row prefix table in LDS: prefix[i] = sum_{j<i} count(j), for i <= rows.
+// Built by a 256-thread block in chunks of 256 rows.  Ends with a barrier.
+template <typename CountFn>
+__device__ __forceinline__ void build_row_prefix(int rows, int* prefix, int* scratch, CountFn count) {
+  int carry = 0;
+  for (int base = 0; base < rows; base += 256) {
+    const int r = base + static_cast<int>(threadIdx.x);
+    const int c = r < rows ? count(r) : 0;
+    int total;
+    const int ex = block_exclusive_scan(c, scratch, total);
+    if (r < rows) prefix[r] = carry + ex;
+    carry += total;
+  }
+  if (threadIdx.x == 0) prefix[rows] = carry;
+  __syncthreads();
+}
+
+// Largest i in [0, rows) with prefix[i] <= unit (prefix is non-decreasing,
+// prefix[0] == 0 and unit < prefix[rows]).
+__device__ __forceinline__ int find_row(const int* prefix, int rows, int unit) {
+  int lo = 0, hi = rows - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (prefix[mid] <= unit) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+}  // namespace ds355

@@ -1,0 +1,81 @@
+// One retrieval step as a launch chain on one stream:
+//   chunk_score_kernel (rows with committed tokens; committed query; rejected
+//   suffix cut) -> select_plan_kernel (selection into the per-slot state,
+//   then a plan row for every real row) -> gather kernel over the plan.
+// No host synchronisation; launch shapes depend only on the descriptor's
+// upper bounds, so the chain can be captured into a HIP graph.
+#include "rowdesc.h"
+
+namespace ds355 {
+
+int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_t q_stride, const void* key_cache,
+                        int64_t k_block_stride, int64_t k_token_stride, int64_t k_head_stride, const float* lse,
+                        int64_t lse_row_stride, int64_t lse_head_stride, const int32_t* block_table,
+                        int64_t bt_stride, const RowSource& src, int batch, int num_q_heads, int num_kv_heads,
+                        int head_dim, int block_size, int chunk_size, int max_chunks, float scale, int head_reduce,
+                        float* out, int64_t out_stride, int write_tail);
+
+int launch_select_plan(hipStream_t stream, const float* scores, int64_t score_stride, const RowSource& src,
+                       int batch, int chunk, int budget, int do_select, int do_plan, int32_t* ids,
+                       int64_t ids_stride, int32_t* counts, const int32_t* slots, int num_slots,
+                       const int32_t* committed_lens, int64_t* plan, int plan_width, int32_t* working_lens,
+                       int recent_window);
+
+int rebuild_compact_kv_impl(hipStream_t stream, int dtype, const void* raw_key, const void* raw_value,
+                            void* working_key, void* working_value, const int64_t* plan, int rows,
+                            int plan_width, const void* cos_sin, int64_t cs_stride, int cs_rows, int num_slots,
+                            int max_model_len, int heads, int head_dim, int token_budget, int chunk_size,
+                            int rotary_dim, int is_neox_style, int max_width, const int32_t* row_active);
+
+}  // namespace ds355
+
+extern "C" int ds_retrieval_step(ds_stream_t stream_handle, const ds_step_desc* d) {
+  using namespace ds355;
+  DS_REQUIRE(d != nullptr, "null step descriptor");
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);
+  const bool score = (d->stages & DS_STAGE_SCORE) != 0;
+  const bool select = (d->stages & DS_STAGE_SELECT) != 0;
+  const bool rebuild = (d->stages & DS_STAGE_PLAN) != 0;
+  DS_REQUIRE((d->stages & ~DS_STAGE_ALL) == 0, "unknown stage bits 0x%x", d->stages);
+  DS_REQUIRE(d->batch_rows >= 0 && d->batch_size >= 0 && d->batch_size <= d->batch_rows,
+             "batch_size must be between zero and batch_rows");
+  DS_REQUIRE(d->chunk_size > 0 && d->history_budget >= d->chunk_size && d->history_budget % d->chunk_size == 0,
+             "history_budget must be a positive chunk-size multiple");
+  DS_REQUIRE(d->history_budget < d->token_budget, "history_budget must be smaller than token_budget");
+  DS_REQUIRE(d->plan_width == 5 + d->token_budget / d->chunk_size, "plan width must be 5 + working_budget // chunk_size");
+  DS_REQUIRE(d->sel_stride >= d->token_budget / d->chunk_size, "selection row stride is smaller than the plan capacity");
+  if (d->batch_rows == 0 || d->stages == 0) return clear_error();
+
+  RowSource src{};
+  src.counts = d->counts;
+  src.q_start = d->query_start;
+  src.q_len = d->query_len;
+  src.target_len = d->target_len;
+  src.batch_size = d->batch_size;
+  if (score || select) {
+    DS_REQUIRE(d->counts && d->query_start && d->query_len && d->target_len, "null verifier row pointer");
+    DS_REQUIRE(d->max_chunks > 0 && d->scores != nullptr, "a score buffer is required");
+  }
+  int rc;
+  if (score) {
+    rc = launch_chunk_scores(stream, d->dtype, d->query, d->q_stride, d->key_cache, d->k_block_stride,
+                             d->k_token_stride, d->k_head_stride, d->lse, d->lse_token_stride, d->lse_head_stride,
+                             d->block_table, d->bt_stride, src, d->batch_rows, d->num_q_heads, d->num_kv_heads,
+                             d->head_dim, d->block_size, d->chunk_size, d->max_chunks, d->scale, DS_HEAD_MEAN,
+                             d->scores, d->max_chunks, 0);
+    if (rc != DS_OK) return rc;
+  }
+  if (select || rebuild) {
+    src.max_len = static_cast<int>(std::min<int64_t>(static_cast<int64_t>(d->max_chunks) * d->chunk_size, INT32_MAX));
+    rc = launch_select_plan(stream, d->scores, d->max_chunks, src, d->batch_rows, d->chunk_size, d->history_budget,
+                            select ? 1 : 0, rebuild ? 1 : 0, d->sel_ids, d->sel_stride, d->sel_count, d->slots,
+                            d->num_slots, d->committed_lens, d->plan, d->plan_width, d->working_lens,
+                            d->recent_window);
+    if (rc != DS_OK) return rc;
+  }
+  if (!rebuild) return clear_error();
+  return rebuild_compact_kv_impl(stream, d->kv_dtype, d->raw_key, d->raw_value, d->working_key, d->working_value,
+                                 d->plan, d->batch_rows, d->plan_width, d->cos_sin, d->cs_stride, d->cs_rows,
+                                 d->num_slots, d->max_model_len, d->draft_heads, d->draft_head_dim, d->token_budget,
+                                 d->chunk_size, d->rotary_dim, d->is_neox_style, d->history_budget, d->row_active);
+}

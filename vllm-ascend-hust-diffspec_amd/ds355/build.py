@@ -1,0 +1,74 @@
+"""Build libds355.so in-tree with hipcc for gfx950.
+
+``python -m ds355.build`` (or ``build()``) compiles every ``csrc/*.hip`` into
+``ds355/libds355.so``.  The GPU code is built for gfx950 only, with fp
+contraction off (the RoPE rotate must round each product separately) and
+packed-fp32 instructions disabled.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+SOURCE_DIR = PACKAGE_DIR.parent / "csrc"
+LIBRARY = PACKAGE_DIR / "libds355.so"
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    for candidate in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if candidate and Path(candidate).exists():
+            return candidate
+    raise RuntimeError("hipcc not found: the ds355 HIP library cannot be built")
+
+
+def sources() -> list[Path]:
+    return sorted(SOURCE_DIR.glob("*.hip"))
+
+
+def command(output: Path) -> list[str]:
+    return [
+        hipcc(),
+        f"--offload-arch={ARCH}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        "-ffp-contract=off",
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-Wall",
+        "-Wno-unused-function",
+        "-o", str(output),
+        *[str(s) for s in sources()],
+    ]
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile the library; raises CalledProcessError with hipcc's output on failure."""
+    tmp = LIBRARY.with_suffix(".so.tmp")
+    cmd = command(tmp)
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    stderr = "\n".join(line for line in result.stderr.splitlines() if noise not in line)
+    if result.returncode != 0:
+        raise subprocess.CalledProcessError(result.returncode, cmd, result.stdout, stderr)
+    if verbose and stderr.strip():
+        print(stderr, file=sys.stderr)
+    os.replace(tmp, LIBRARY)
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    try:
+        path = build(verbose=True)
+    except subprocess.CalledProcessError as error:
+        print(error.stderr, file=sys.stderr)
+        sys.exit(error.returncode)
+    print(path)

@@ -1,0 +1,381 @@
+"""Host orchestration of DiffSpec retrieval and rebuild over the HIP chain.
+
+``DiffSpecDraftCache`` mirrors the hot-path part of the reference's cache
+(diffspec/runtime.py:596-1765): canonical slots, the verifier snapshot, the
+retrieval cadence and skip rules, and the working-cache rebuild.  The
+per-row Python loops, the ``counts.to("cpu")`` synchronisation and the
+host-built plan of the reference are replaced by device state
+(``sel_ids`` / ``sel_count`` / ``working_lens``) and the stage-split launch
+chain of ``ds355.step``; host metadata that the reference already holds as
+Python lists (query ends, verifier lengths, slots) is uploaded through a
+small ring of pinned staging buffers with non-blocking copies.
+
+Tree drafting, draft attention, raw-KV capture and the adaptive controller
+are outside this module.
+"""
+
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+
+from . import step as _step
+from .plan import history_budget as _history_budget
+from .plan import plan_width as _plan_width
+
+
+@dataclass(frozen=True)
+class DiffSpecSettings:
+    """Field order and meaning of diffspec/runtime.py:18-41."""
+
+    chunk_size: int
+    token_budget: int
+    retrieval_interval: int
+    max_tree_nodes: int
+    max_tree_depth: int
+    tree_threshold: float
+    adaptive_profile: bool
+    recent_window: int | None = None  # None: one chunk, the reference's tail
+
+
+@dataclass
+class DiffSpecRuntimeMetrics:
+    """Retrieval counters of diffspec/runtime.py:65-116."""
+
+    retrieval_count: int = 0
+    retrieval_seconds: float = 0.0
+    retrieval_attempts: int = 0
+    retrieval_skipped_prefill: int = 0
+    retrieval_skipped_no_snapshot: int = 0
+    retrieval_skipped_interval: int = 0
+    retrieval_skipped_no_committed_tokens: int = 0
+
+    def observe_retrieval(self, elapsed_seconds: float) -> None:
+        self.retrieval_count += 1
+        self.retrieval_seconds += elapsed_seconds
+
+    def snapshot(self) -> dict[str, float | int]:
+        return {
+            "retrieval_count": self.retrieval_count,
+            "retrieval_attempts": self.retrieval_attempts,
+            "retrieval_skipped_prefill": self.retrieval_skipped_prefill,
+            "retrieval_skipped_no_snapshot": self.retrieval_skipped_no_snapshot,
+            "retrieval_skipped_interval": self.retrieval_skipped_interval,
+            "retrieval_skipped_no_committed_tokens": self.retrieval_skipped_no_committed_tokens,
+            "retrieval_ms": self.retrieval_seconds / max(self.retrieval_count, 1) * 1.0e3,
+        }
+
+
+class _Staging:
+    """Ring of pinned host buffers for small int32 row arrays (non-blocking H2D)."""
+
+    def __init__(self, fields: int, rows: int, device: torch.device, depth: int = 4) -> None:
+        pin = device.type == "cuda"
+        self.host = [torch.zeros((fields, rows), dtype=torch.int32, pin_memory=pin) for _ in range(depth)]
+        self.events: list[torch.cuda.Event | None] = [None] * depth
+        self.device = torch.zeros((fields, rows), dtype=torch.int32, device=device)
+        self.index = 0
+
+    def upload(self, columns: list[list[int]]) -> torch.Tensor:
+        i = self.index
+        self.index = (i + 1) % len(self.host)
+        if self.events[i] is not None:
+            self.events[i].synchronize()  # only waits if the GPU is a full ring behind
+        buf = self.host[i]
+        for f, values in enumerate(columns):
+            if values:
+                buf[f, : len(values)] = torch.tensor(values, dtype=torch.int32)
+        self.device.copy_(buf, non_blocking=True)
+        if self.device.device.type == "cuda":
+            event = torch.cuda.Event()
+            event.record()
+            self.events[i] = event
+        return self.device
+
+
+class DiffSpecDraftCache:
+    """Canonical raw KV, bounded working cache and retrieval state.
+
+    Constructor arguments follow diffspec/runtime.py:599-613.
+    ``rotary_embedding`` supplies ``rotary_dim``, ``is_neox_style`` and
+    either ``cos_sin_cache`` or ``_match_cos_sin_cache_dtype(x)``.
+    """
+
+    def __init__(
+        self,
+        settings: DiffSpecSettings,
+        *,
+        max_num_reqs: int,
+        max_model_len: int,
+        num_kv_heads: int,
+        head_dim: int,
+        target_num_layers: int,
+        dtype: torch.dtype,
+        device: torch.device,
+        rotary_embedding: Any,
+        target_cos_sin_cache: torch.Tensor | None = None,
+        target_tensor_parallel_size: int = 1,
+        max_batch_rows: int | None = None,
+    ) -> None:
+        if target_tensor_parallel_size < 1:
+            raise ValueError("Target tensor parallel size must be positive")
+        self.settings = settings
+        self.max_num_reqs = max_num_reqs
+        self.max_model_len = max_model_len
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+        self.target_last_layer = target_num_layers - 1
+        self.target_tensor_parallel_size = target_tensor_parallel_size
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.rotary_embedding = rotary_embedding
+        self.target_cos_sin_cache = target_cos_sin_cache
+        self.history_budget = _history_budget(settings.token_budget, settings.max_tree_depth, settings.chunk_size)
+        self.recent_window = settings.chunk_size if settings.recent_window is None else settings.recent_window
+
+        cache_shape = (max_num_reqs, max_model_len, num_kv_heads, head_dim)
+        self.raw_key = torch.empty(cache_shape, dtype=dtype, device=self.device)
+        self.raw_value = torch.empty_like(self.raw_key)
+        working_shape = (max_num_reqs, num_kv_heads, settings.token_budget, head_dim)
+        self.working_key = torch.empty(working_shape, dtype=dtype, device=self.device)
+        self.working_value = torch.empty_like(self.working_key)
+
+        # Per-slot selection state: sorted chunk ids and their count
+        # (-1 = no selection yet, 0 = empty selection).
+        capacity = settings.token_budget // settings.chunk_size
+        self.sel_ids = torch.zeros((max_num_reqs, capacity), dtype=torch.int32, device=self.device)
+        self.sel_count = torch.full((max_num_reqs,), -1, dtype=torch.int32, device=self.device)
+        self.working_lens = torch.zeros((max_num_reqs,), dtype=torch.int32, device=self.device)
+
+        self.max_batch_rows = max_batch_rows or max_num_reqs
+        self.max_chunks = (max_model_len + settings.chunk_size - 1) // settings.chunk_size
+        rows = self.max_batch_rows
+        self.scores = torch.zeros((rows, self.max_chunks), dtype=torch.float32, device=self.device)
+        self.plan = torch.zeros((rows, _plan_width(settings.token_budget, settings.chunk_size)),
+                                dtype=torch.int64, device=self.device)
+        self._rows_staging = _Staging(5, rows, self.device)
+        self._plan_staging = _Staging(2, rows, self.device)
+
+        self.retrieval_interval = settings.retrieval_interval
+        self.metrics = DiffSpecRuntimeMetrics()
+        self._request_slots: dict[str, int] = {}
+        self._active_slots: list[int] = []
+        self._retrieval_cycle = 0
+        self._target_query: torch.Tensor | None = None
+        self._target_lse: torch.Tensor | None = None
+        self._target_key_cache: torch.Tensor | None = None
+        self._target_block_tables: torch.Tensor | None = None
+        self._target_query_ends: list[int] = []
+        self._target_seq_lens: list[int] = []
+        self._target_scale = 0.0
+        self.target_is_prefill = True
+        self.local_positions: torch.Tensor | None = None  # root positions of the last rebuild (device)
+
+    # -- slots (runtime.py:755-793) --------------------------------------------------------------
+    def set_active_requests(self, request_ids: list[str]) -> None:
+        """Keep canonical rows stable across batch reorder and cancellation."""
+        active = set(request_ids)
+        freed = []
+        for request_id in list(self._request_slots):
+            if request_id not in active:
+                freed.append(self._request_slots.pop(request_id))
+        if freed:
+            index = torch.tensor(freed, dtype=torch.long)
+            self.sel_count[index.to(self.device)] = -1
+            self.working_lens[index.to(self.device)] = 0
+        used = set(self._request_slots.values())
+        free = iter(sorted(set(range(self.max_num_reqs)) - used))
+        for request_id in request_ids:
+            if request_id not in self._request_slots:
+                try:
+                    self._request_slots[request_id] = next(free)
+                except StopIteration as error:
+                    raise RuntimeError("DiffSpec canonical request slots are exhausted") from error
+        self._active_slots = [self._request_slots[r] for r in request_ids]
+
+    def begin_target_forward(self, request_ids: list[str]) -> None:
+        """Discard a stale verifier snapshot before a new verifier pass."""
+        self.set_active_requests(request_ids)
+        self._target_query = None
+        self._target_lse = None
+        self._target_key_cache = None
+        self._target_block_tables = None
+        self._target_query_ends = []
+        self._target_seq_lens = []
+        self.target_is_prefill = True
+
+    # -- verifier snapshot (runtime.py:841-894) ---------------------------------------------------
+    @staticmethod
+    def _reshape_target_lse(query: torch.Tensor, softmax_lse: torch.Tensor) -> torch.Tensor:
+        num_tokens, num_heads, _ = query.shape
+        lse = softmax_lse.squeeze()
+        if lse.ndim == 1 and num_tokens * num_heads == lse.numel():
+            return lse.reshape(num_tokens, num_heads)
+        if lse.shape == (num_tokens, num_heads):
+            return lse
+        if lse.shape == (num_heads, num_tokens):
+            return lse.transpose(0, 1)  # a strided view: the kernel takes both strides
+        if lse.numel() != num_tokens * num_heads:
+            raise ValueError("target softmax LSE does not match target query shape")
+        return lse.reshape(num_tokens, num_heads)
+
+    def capture_target_attention(
+        self,
+        query: torch.Tensor,
+        softmax_lse: torch.Tensor | None,
+        key_cache: torch.Tensor | None,
+        metadata: Any,
+        scale: float,
+    ) -> None:
+        """Keep the last verifier layer's query, LSE and paged K (no copies of K)."""
+        if softmax_lse is None or key_cache is None:
+            return
+        query_ends = list(getattr(metadata, "actual_seq_lengths_q", ()))
+        seq_lens = list(getattr(metadata, "seq_lens_list", ()))
+        block_tables = getattr(metadata, "block_tables", None)
+        if not query_ends or not seq_lens or block_tables is None:
+            return
+        is_prefill = bool(getattr(metadata, "num_prefills", 1))
+        lse = self._reshape_target_lse(query, softmax_lse)
+        if is_prefill:
+            index = torch.tensor([end - 1 for end in query_ends], dtype=torch.long, device=query.device)
+            lse = lse.index_select(0, index)
+            query = query.index_select(0, index)
+            query_ends = list(range(1, len(query_ends) + 1))
+        self._target_query = query.detach()
+        self._target_lse = lse.detach()
+        self._target_key_cache = key_cache
+        self._target_block_tables = block_tables[: len(seq_lens)]
+        self._target_query_ends = query_ends
+        self._target_seq_lens = seq_lens
+        self._target_scale = scale
+        self.target_is_prefill = is_prefill
+
+    # -- retrieval (runtime.py:1170-1334) ---------------------------------------------------------
+    def accept_target_queries(self, valid_sampled_token_count: torch.Tensor, *, is_prefill: bool) -> None:
+        """Retrieve context using the last committed verifier query per request."""
+        self.metrics.retrieval_attempts += 1
+        self._accept_target_queries(valid_sampled_token_count, is_prefill=is_prefill)
+
+    def retrieval_status(self) -> dict[str, float | int]:
+        """Counters plus slots holding a selection (reads the device state)."""
+        return dict(
+            self.metrics.snapshot(),
+            retrieval_cycle=self._retrieval_cycle,
+            selected_slots=int((self.sel_count >= 0).sum().item()),
+            target_tensor_parallel_size=self.target_tensor_parallel_size,
+        )
+
+    def _accept_target_queries(self, valid_sampled_token_count: torch.Tensor, *, is_prefill: bool) -> None:
+        if self._target_query is None or self._target_key_cache is None or self._target_block_tables is None:
+            self.metrics.retrieval_skipped_no_snapshot += 1
+            return
+        if is_prefill:
+            self.metrics.retrieval_skipped_prefill += 1
+            return
+        self._retrieval_cycle += 1
+        if self._retrieval_cycle % self.retrieval_interval:
+            self.metrics.retrieval_skipped_interval += 1
+            return
+        # Graph padding beyond the scheduler's requests is excluded (runtime.py:1211-1222).
+        batch_size = len(self._active_slots)
+        if (
+            valid_sampled_token_count.numel() < batch_size
+            or len(self._target_query_ends) < batch_size
+            or len(self._target_seq_lens) < batch_size
+            or self._target_block_tables.shape[0] < batch_size
+        ):
+            self.metrics.retrieval_skipped_no_snapshot += 1
+            return
+        if batch_size > self.max_batch_rows:
+            raise RuntimeError("DiffSpec batch exceeds max_batch_rows")
+        if self.target_tensor_parallel_size > 1:
+            raise NotImplementedError("the chunk-score all-reduce across tensor-parallel ranks is not built")
+        ends = self._target_query_ends[:batch_size]
+        starts = [0, *ends[:-1]]
+        lens = [e - s for s, e in zip(starts, ends)]
+        if max(self._target_seq_lens[:batch_size]) > self.max_chunks * self.settings.chunk_size:
+            raise ValueError("verifier length exceeds the score buffer (max_model_len)")
+        staged = self._rows_staging.upload([
+            starts, lens, self._target_seq_lens[:batch_size], self._active_slots, [],
+        ])
+        counts = staged[4, :batch_size]
+        counts.copy_(valid_sampled_token_count.reshape(-1)[:batch_size])  # device-side cast, no sync
+        rows = _step.VerifierRows(
+            counts=staged[4, :batch_size], query_start=staged[0, :batch_size],
+            query_len=staged[1, :batch_size], target_len=staged[2, :batch_size], batch_size=batch_size,
+        )
+        snapshot = _step.VerifierSnapshot(
+            query=self._target_query, lse=self._target_lse, key_cache=self._target_key_cache,
+            block_table=self._target_block_tables, scale=self._target_scale,
+        )
+        started = time.perf_counter()
+        self._launch(_step.SCORE | _step.SELECT, batch_size, snapshot=snapshot, rows=rows,
+                     slots=staged[3, :batch_size], committed=staged[2, :batch_size])
+        self.metrics.observe_retrieval(time.perf_counter() - started)
+
+    # -- rebuild (runtime.py:1349-1371, 1683-1765) ------------------------------------------------
+    def prepare_compact_prefill(
+        self, metadata: Any, num_tokens: int, *, committed_seq_lens: list[int] | torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """Rebuild every active row's working cache at its committed root.
+
+        ``committed_seq_lens`` (root position + 1 per row) may be a host list
+        or an int32 device tensor.  Returns the rows' local root positions
+        (the history lengths) as a device tensor; nothing is read back.
+        """
+        seq_lens = committed_seq_lens
+        if seq_lens is None:
+            seq_lens = list(getattr(metadata, "seq_lens_list", ()))
+        if isinstance(seq_lens, list) and not seq_lens:
+            raise RuntimeError("DiffSpec compact prefill requires sequence lengths")
+        if not self._active_slots:
+            raise RuntimeError("DiffSpec request slots have not been initialized")
+        rows = num_tokens
+        if rows > len(self._active_slots) or rows > self.max_batch_rows:
+            raise RuntimeError("DiffSpec draft tensors omit active request rows")
+        slots = self._active_slots[:rows]
+        if isinstance(seq_lens, torch.Tensor):
+            staged = self._plan_staging.upload([slots, []])
+            staged[1, :rows].copy_(seq_lens.reshape(-1)[:rows])
+        else:
+            staged = self._plan_staging.upload([slots, list(seq_lens[:rows])])
+        self._launch(_step.PLAN, rows, slots=staged[0, :rows], committed=staged[1, :rows])
+        self.local_positions = self.plan[:rows, 1]
+        return self.local_positions
+
+    def _launch(
+        self,
+        stages: int,
+        batch_rows: int,
+        *,
+        slots: torch.Tensor,
+        committed: torch.Tensor,
+        snapshot: _step.VerifierSnapshot | None = None,
+        rows: _step.VerifierRows | None = None,
+    ) -> None:
+        rotary = self.rotary_embedding
+        cos_sin = self._cos_sin_cache()
+        _step.retrieval_step(
+            stages=stages, snapshot=snapshot, rows=rows,
+            scores=self.scores[:batch_rows] if stages & (_step.SCORE | _step.SELECT) else None,
+            sel_ids=self.sel_ids, sel_count=self.sel_count, slots=slots, committed_lens=committed,
+            plan=self.plan[:batch_rows], working_lens=self.working_lens,
+            raw_key=self.raw_key, raw_value=self.raw_value,
+            working_key=self.working_key, working_value=self.working_value,
+            cos_sin_cache=cos_sin, rotary_dim=rotary.rotary_dim, is_neox_style=rotary.is_neox_style,
+            chunk_size=self.settings.chunk_size, history_budget=self.history_budget,
+            recent_window=self.recent_window,
+        )
+
+    def _cos_sin_cache(self) -> torch.Tensor:
+        rotary = self.rotary_embedding
+        match = getattr(rotary, "_match_cos_sin_cache_dtype", None)
+        cache = match(self.raw_key) if match is not None else rotary.cos_sin_cache
+        if cache.dtype != self.dtype or cache.device != self.device:
+            cache = cache.to(device=self.device, dtype=self.dtype)
+            rotary.cos_sin_cache = cache
+        return cache

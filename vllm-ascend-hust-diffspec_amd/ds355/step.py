@@ -1,0 +1,186 @@
+"""One retrieval step as a single launch chain (``ds_retrieval_step``).
+
+score -> select (into per-slot state) -> plan -> gather/RoPE/write on the
+current stream, with no host synchronisation.  This is the device-side
+composition of diffspec/runtime.py:1211-1308 (row choice, committed query,
+rejected-suffix cut, per-row selection), runtime.py:1737-1765 (plans) and
+diffspec/compact_kv.py (gather).  Every argument is a device tensor or a host
+integer known before the step; launch shapes depend only on the buffers'
+sizes, so a step can be captured into a HIP graph.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+
+def _i32(name: str, t: torch.Tensor, n: int | None = None) -> torch.Tensor:
+    if t.dtype != torch.int32 or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous int32 tensor")
+    if n is not None and t.numel() < n:
+        raise ValueError(f"{name} has {t.numel()} entries, need {n}")
+    return t
+
+
+@dataclass
+class VerifierSnapshot:
+    """Target last-layer state used for scoring (runtime.py:841-878).
+
+    query ``[tokens, Hq, D]``; lse viewed as ``[tokens, Hq]`` (any strides);
+    key_cache ``[blocks, block_size, Hkv, D]``; block_table ``[rows, *]`` int32.
+    """
+
+    query: torch.Tensor
+    lse: torch.Tensor
+    key_cache: torch.Tensor
+    block_table: torch.Tensor
+    scale: float
+
+
+@dataclass
+class VerifierRows:
+    """Per-row verifier metadata, int32 device tensors of ``batch_rows`` entries.
+
+    ``counts`` = committed tokens (``valid_sampled_token_count``), ``query_start``
+    / ``query_len`` = the row's query tokens, ``target_len`` = verifier KV
+    length.  Rows at or beyond ``batch_size`` are graph padding.
+    """
+
+    counts: torch.Tensor
+    query_start: torch.Tensor
+    query_len: torch.Tensor
+    target_len: torch.Tensor
+    batch_size: int
+
+
+SCORE, SELECT, PLAN, ALL = _lib.DS_STAGE_SCORE, _lib.DS_STAGE_SELECT, _lib.DS_STAGE_PLAN, _lib.DS_STAGE_ALL
+
+
+def retrieval_step(
+    *,
+    stages: int = ALL,
+    snapshot: VerifierSnapshot | None,
+    rows: VerifierRows | None,
+    scores: torch.Tensor | None,
+    sel_ids: torch.Tensor,
+    sel_count: torch.Tensor,
+    slots: torch.Tensor,
+    committed_lens: torch.Tensor,
+    plan: torch.Tensor,
+    working_lens: torch.Tensor | None,
+    raw_key: torch.Tensor,
+    raw_value: torch.Tensor,
+    working_key: torch.Tensor,
+    working_value: torch.Tensor,
+    cos_sin_cache: torch.Tensor,
+    rotary_dim: int,
+    is_neox_style: bool,
+    chunk_size: int,
+    history_budget: int,
+    recent_window: int | None = None,
+    row_active: torch.Tensor | None = None,
+) -> None:
+    """Run the stages in ``stages`` (``SCORE | SELECT | PLAN``; ``ALL`` = one step).
+
+    SCORE needs ``snapshot``; SCORE and SELECT need ``rows`` and ``scores``, a
+    ``[batch_rows, max_chunks]`` fp32 buffer whose ``max_chunks`` covers
+    ``ceil(max target_len / chunk_size)``.  PLAN writes ``plan`` and gathers.
+    """
+    if stages & ~ALL:
+        raise ValueError(f"unknown stage bits {stages:#x}")
+    do_score = bool(stages & SCORE)
+    uses_rows = bool(stages & (SCORE | SELECT))
+    batch_rows = slots.numel()
+    num_slots, max_model_len, heads, head_dim = raw_key.shape
+    token_budget = working_key.shape[2]
+    if raw_value.shape != raw_key.shape or working_value.shape != working_key.shape:
+        raise ValueError("raw key/value must have matching 4-D shapes")
+    if working_key.shape[0] != num_slots or working_key.shape[1] != heads or working_key.shape[3] != head_dim:
+        raise ValueError("working cache slot, head and head dimensions must match raw KV")
+    if not all(t.is_contiguous() for t in (raw_key, raw_value, working_key, working_value, plan)):
+        raise ValueError("raw KV, working KV and plan must be contiguous")
+    if plan.dtype != torch.int64 or plan.shape[0] != batch_rows:
+        raise ValueError("plan must be int64 with one row per batch row")
+    if cos_sin_cache.dtype != raw_key.dtype or cos_sin_cache.stride(1) != 1:
+        raise ValueError("cos/sin cache must use the KV dtype with unit last stride")
+    if cos_sin_cache.shape[0] < history_budget:
+        raise ValueError("cos/sin cache must contain all local positions and rotary dimensions")
+    _i32("slots", slots)
+    _i32("committed_lens", committed_lens, batch_rows)
+    _i32("sel_ids", sel_ids)
+    _i32("sel_count", sel_count, num_slots)
+    if sel_ids.shape[0] < num_slots:
+        raise ValueError("sel_ids needs a row per slot")
+    if working_lens is not None:
+        _i32("working_lens", working_lens, num_slots)
+    if row_active is not None:
+        _i32("row_active", row_active, batch_rows)
+    tensors = [sel_ids, sel_count, slots, committed_lens, plan, raw_key, raw_value, working_key, working_value,
+               cos_sin_cache, working_lens, row_active]
+
+    desc = _lib.StepDesc()
+    desc.stages = stages
+    desc.batch_size = batch_rows
+    if uses_rows:
+        if rows is None or scores is None:
+            raise ValueError("scoring and selection need verifier rows and a score buffer")
+        if scores.dtype != torch.float32 or scores.ndim != 2 or scores.shape[0] != batch_rows or not scores.is_contiguous():
+            raise ValueError("scores must be a contiguous fp32 [batch_rows, max_chunks] buffer")
+        for name in ("counts", "query_start", "query_len", "target_len"):
+            _i32(name, getattr(rows, name), batch_rows)
+        if not 0 <= rows.batch_size <= batch_rows:
+            raise ValueError("batch_size must be between zero and batch_rows")
+        tensors += [scores, rows.counts, rows.query_start, rows.query_len, rows.target_len]
+        desc.counts, desc.query_start = rows.counts.data_ptr(), rows.query_start.data_ptr()
+        desc.query_len, desc.target_len = rows.query_len.data_ptr(), rows.target_len.data_ptr()
+        desc.batch_size = rows.batch_size
+        desc.max_chunks = scores.shape[1]
+        desc.scores = scores.data_ptr()
+    if do_score:
+        if snapshot is None:
+            raise ValueError("scoring needs a verifier snapshot")
+        q, lse, kc, bt = snapshot.query, snapshot.lse, snapshot.key_cache, snapshot.block_table
+        if q.ndim != 3 or kc.ndim != 4 or q.shape[2] != kc.shape[3]:
+            raise ValueError("query and key head dimensions must match")
+        if q.shape[1] % kc.shape[2] != 0:
+            raise ValueError("query heads must be divisible by KV heads")
+        if q.stride(2) != 1 or q.stride(1) != q.shape[2] or kc.stride(3) != 1:
+            raise ValueError("query and key cache rows must be contiguous")
+        if lse.dtype != torch.float32 or lse.ndim != 2 or lse.shape != q.shape[:2]:
+            raise ValueError("target softmax LSE does not match target query shape")
+        if bt.dtype != torch.int32 or bt.ndim != 2 or bt.stride(1) != 1 or bt.shape[0] < batch_rows:
+            raise ValueError("block_table must be int32 [rows, blocks] with unit last stride")
+        if q.dtype != kc.dtype:
+            raise ValueError("query and key cache must share a dtype")
+        tensors += [q, lse, kc, bt]
+        desc.dtype = _lib.dtype_code(q.dtype)
+        desc.query, desc.q_stride = q.data_ptr(), q.stride(0)
+        desc.lse, desc.lse_token_stride, desc.lse_head_stride = lse.data_ptr(), lse.stride(0), lse.stride(1)
+        desc.key_cache = kc.data_ptr()
+        desc.k_block_stride, desc.k_token_stride, desc.k_head_stride = kc.stride(0), kc.stride(1), kc.stride(2)
+        desc.block_size = kc.shape[1]
+        desc.block_table, desc.bt_stride = bt.data_ptr(), bt.stride(0)
+        desc.num_q_heads, desc.num_kv_heads, desc.head_dim = q.shape[1], kc.shape[2], q.shape[2]
+        desc.scale = float(snapshot.scale)
+    device = _lib.require_gpu(*tensors)
+    desc.batch_rows = batch_rows
+    desc.sel_ids, desc.sel_stride, desc.sel_count = sel_ids.data_ptr(), sel_ids.stride(0), sel_count.data_ptr()
+    desc.slots = slots.data_ptr()
+    desc.committed_lens, desc.plan, desc.plan_width = committed_lens.data_ptr(), plan.data_ptr(), plan.shape[1]
+    desc.working_lens = _lib.ptr(working_lens)
+    desc.kv_dtype = _lib.dtype_code(raw_key.dtype)
+    desc.raw_key, desc.raw_value = raw_key.data_ptr(), raw_value.data_ptr()
+    desc.working_key, desc.working_value = working_key.data_ptr(), working_value.data_ptr()
+    desc.num_slots, desc.max_model_len, desc.draft_heads, desc.draft_head_dim = num_slots, max_model_len, heads, head_dim
+    desc.token_budget = token_budget
+    desc.cos_sin, desc.cs_stride, desc.cs_rows = cos_sin_cache.data_ptr(), cos_sin_cache.stride(0), cos_sin_cache.shape[0]
+    desc.rotary_dim, desc.is_neox_style = rotary_dim, 1 if is_neox_style else 0
+    desc.row_active = _lib.ptr(row_active)
+    desc.chunk_size, desc.history_budget = chunk_size, history_budget
+    desc.recent_window = chunk_size if recent_window is None else recent_window
+    lib = _lib.load()
+    _lib.check(lib.ds_retrieval_step(_lib.stream_handle(device), desc))

@@ -1,0 +1,405 @@
+"""Benchmark: microseconds per DiffSpec retrieval step on one MI355X.
+
+A step is one launch chain over a ragged batch: chunk scores (paged target
+K, committed query, supplied LSE) -> per-request top-k selection -> history
+plans -> gather of the selected pre-RoPE KV + RoPE at local positions +
+working-cache write.  Inputs are synthetic (seeded N(0,1) bf16), resident in
+HBM before timing, and rotated over several copies so consecutive steps do
+not hit in the 256 MB Infinity Cache.
+
+Prints ONE JSON line.  The default workload is the 16-request ragged batch
+(context lengths uniform in [4096, 40960], 4 KV heads x 128, 32 query heads,
+chunk 64, token budget 2048, K = 4 draft tokens -> 1984 history tokens).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "vllm-ascend-hust-diffspec_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
+METRIC = "µs per retrieval step (16 req, 40k ctx) and achieved HBM GB/s vs peak, 1 GPU"
+
+WORKLOADS = {
+    # name: (rows, lengths spec, Hq, Hkv, D, chunk, token_budget, padding rows, qlen, permuted slots, reuse half)
+    "single-8k": dict(rows=1, lens=("fixed", 8192), hq=32, hkv=4, d=128, chunk=64, budget=2048),
+    "ragged16-40k": dict(rows=16, lens=("uniform", 4096, 40960), hq=32, hkv=4, d=128, chunk=64, budget=2048),
+    "fixed16-40k": dict(rows=16, lens=("fixed", 40960), hq=32, hkv=4, d=128, chunk=64, budget=2048),
+    "long4-128k": dict(rows=4, lens=("fixed", 131072), hq=32, hkv=4, d=128, chunk=32, budget=2048),
+    "specmask16-pad32": dict(rows=16, lens=("uniform", 8192, 40960), hq=32, hkv=4, d=128, chunk=64, budget=2048,
+                             pad=16, qlen=5, permute=True),
+    "stress64": dict(rows=64, lens=("uniform", 2048, 40960), hq=64, hkv=8, d=128, chunk=128, budget=4096,
+                     reuse_half=True),
+}
+DEFAULT_WORKLOAD = "ragged16-40k"
+DRAFT_TOKENS = 4
+BLOCK_SIZE = 128
+ROPE_THETA = 1.0e6
+
+
+def log(*args):
+    print(*args, file=sys.stderr, flush=True)
+
+
+def build_inputs(spec, seed, device):
+    """Seeded synthetic verifier batch + draft caches on `device`."""
+    import torch
+
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    rows = spec["rows"]
+    pad = spec.get("pad", 0)
+    qlen = spec.get("qlen", 1)
+    kind = spec["lens"][0]
+    if kind == "fixed":
+        tlens = [spec["lens"][1]] * rows
+    else:
+        lo, hi = spec["lens"][1], spec["lens"][2]
+        tlens = [int(x) for x in torch.randint(lo, hi + 1, (rows,), generator=g)]
+    if qlen > 1:
+        accepted = [int(x) for x in torch.randint(0, DRAFT_TOKENS + 1, (rows,), generator=g)]
+        counts = [a + 1 for a in accepted]
+    else:
+        counts = [1] * rows
+    slots = [int(x) for x in torch.randperm(rows, generator=g)] if spec.get("permute") else list(range(rows))
+    hq, hkv, d, chunk = spec["hq"], spec["hkv"], spec["d"], spec["chunk"]
+    total_rows = rows + pad
+    qlens = [qlen] * rows + [1] * pad
+    all_tlens = tlens + [1] * pad
+    ends = [sum(qlens[: i + 1]) for i in range(total_rows)]
+    starts = [0, *ends[:-1]]
+    committed = [tl - ql + min(max(c, 1), ql) for tl, ql, c in zip(all_tlens, qlens, counts + [0] * pad)]
+    pages = [(n + BLOCK_SIZE - 1) // BLOCK_SIZE for n in all_tlens]
+    num_blocks = sum(pages)
+    gd = torch.Generator(device=device).manual_seed(seed + 1)
+    query = torch.randn((ends[-1], hq, d), generator=gd, device=device, dtype=torch.float32).to(torch.bfloat16)
+    key_cache = torch.randn((num_blocks, BLOCK_SIZE, hkv, d), generator=gd, device=device,
+                            dtype=torch.float32).to(torch.bfloat16)
+    perm = torch.randperm(num_blocks, generator=g)
+    table = torch.zeros((total_rows, max(pages)), dtype=torch.int32)
+    k = 0
+    for b, p in enumerate(pages):
+        table[b, :p] = perm[k:k + p].to(torch.int32)
+        k += p
+    table = table.to(device)
+    lmax = max(tlens)
+    raw_k = torch.randn((rows, lmax, hkv, d), generator=gd, device=device, dtype=torch.float32).to(torch.bfloat16)
+    raw_v = torch.randn((rows, lmax, hkv, d), generator=gd, device=device, dtype=torch.float32).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(d)
+    # Exact LSE of each committed query over its scored prefix (fp32 matmul).
+    lse = torch.zeros((ends[-1], hq), dtype=torch.float32, device=device)
+    for b in range(rows):
+        if counts[b] <= 0:
+            continue
+        qi = starts[b] + min(max(counts[b] - 1, 0), qlens[b] - 1)
+        n = committed[b]
+        dense = key_cache[table[b, : (n + BLOCK_SIZE - 1) // BLOCK_SIZE].long()].reshape(-1, hkv, d)[:n].float()
+        qg = query[qi].float().reshape(hkv, hq // hkv, d)
+        logits = torch.matmul(qg, dense.permute(1, 2, 0).contiguous()).reshape(hq, n) * scale
+        lse[qi] = torch.logsumexp(logits, dim=-1)
+    return dict(query=query, lse=lse, key_cache=key_cache, table=table, raw_k=raw_k, raw_v=raw_v, tlens=all_tlens,
+                counts=counts + [0] * pad, starts=starts, qlens=qlens, committed=committed, slots=slots + [-1] * pad,
+                rows=rows, total_rows=total_rows, scale=scale, lmax=lmax)
+
+
+def algorithmic_bytes(spec, inp, plan_lens, active):
+    """Bytes a perfect kernel must move (K read once; q, LSE, scores; selected K/V read + written; cos/sin)."""
+    hq, hkv, d, chunk = spec["hq"], spec["hkv"], spec["d"], spec["chunk"]
+    scored = [n for n, c in zip(inp["committed"], inp["counts"]) if c > 0]
+    chunks = [(n + chunk - 1) // chunk for n in scored]
+    score_bytes = sum(scored) * hkv * d * 2 + len(scored) * hq * (d * 2 + 4) + sum(chunks) * 4
+    gathered = [h for h, a in zip(plan_lens, active) if a]
+    gather_bytes = sum(gathered) * hkv * d * 2 * 4 + (max(gathered, default=0) * d * 2)
+    chain_bytes = score_bytes + sum(chunks) * 4 + gather_bytes
+    return score_bytes, gather_bytes, chain_bytes
+
+
+def run(args):
+    import torch
+
+    from ds355 import _lib, step
+    from ds355.plan import history_budget
+
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1"}))
+        log("bench.py measures one MI355X; a multi-GPU run is not part of this build (sharding is described in "
+            "DESIGN.md)")
+        sys.exit(2)
+    spec = WORKLOADS[args.workload]
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    lib = _lib.load()
+    chunk, token_budget, d, hkv = spec["chunk"], spec["budget"], spec["d"], spec["hkv"]
+    hb = history_budget(token_budget, DRAFT_TOKENS, chunk)
+    t0 = time.time()
+    copies = [build_inputs(spec, args.seed, device)]
+    for _ in range(args.copies - 1):
+        copies.append({k: (v.clone() if isinstance(v, torch.Tensor) else v) for k, v in copies[0].items()})
+    log(f"inputs ready in {time.time() - t0:.1f}s ({args.copies} copies)")
+    inp0 = copies[0]
+    total_rows, rows, lmax = inp0["total_rows"], inp0["rows"], inp0["lmax"]
+    max_chunks = (max(inp0["tlens"]) + chunk - 1) // chunk
+    inv = 1.0 / (ROPE_THETA ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    freqs = torch.outer(torch.arange(token_budget, dtype=torch.float32), inv)
+    cos_sin = torch.cat((freqs.cos(), freqs.sin()), -1).to(torch.bfloat16).to(device)
+    i32 = lambda xs: torch.tensor(xs, dtype=torch.int32, device=device)  # noqa: E731
+    rows_t = dict(counts=i32(inp0["counts"]), starts=i32(inp0["starts"]), qlens=i32(inp0["qlens"]),
+                  tlens=i32(inp0["tlens"]), slots=i32(inp0["slots"]), committed=i32(inp0["committed"]))
+    g = torch.Generator().manual_seed(args.seed + 7)
+    reuse = spec.get("reuse_half", False)
+    active = [1] * total_rows
+    if reuse:
+        active = [int(x) for x in (torch.rand(total_rows, generator=g) >= 0.5)]
+    row_active = i32(active) if reuse else None
+
+    states = []
+    for inp in copies:
+        st = dict(
+            scores=torch.zeros((total_rows, max_chunks), dtype=torch.float32, device=device),
+            sel_ids=torch.zeros((rows, token_budget // chunk), dtype=torch.int32, device=device),
+            sel_count=torch.full((rows,), -1, dtype=torch.int32, device=device),
+            plan=torch.zeros((total_rows, 5 + token_budget // chunk), dtype=torch.int64, device=device),
+            working_lens=torch.zeros((rows,), dtype=torch.int32, device=device),
+            work_k=torch.zeros((rows, hkv, token_budget, d), dtype=torch.bfloat16, device=device),
+        )
+        st["work_v"] = torch.zeros_like(st["work_k"])
+        states.append(st)
+
+    descs = []
+    for inp, st in zip(copies, states):
+        desc, _ = step.build_step_desc(
+            snapshot=step.VerifierSnapshot(inp["query"], inp["lse"], inp["key_cache"], inp["table"], inp["scale"]),
+            rows=step.VerifierRows(rows_t["counts"], rows_t["starts"], rows_t["qlens"], rows_t["tlens"], rows),
+            scores=st["scores"], sel_ids=st["sel_ids"], sel_count=st["sel_count"], slots=rows_t["slots"],
+            committed_lens=rows_t["committed"], plan=st["plan"], working_lens=st["working_lens"],
+            raw_key=inp["raw_k"], raw_value=inp["raw_v"], working_key=st["work_k"], working_value=st["work_v"],
+            cos_sin_cache=cos_sin, rotary_dim=d, is_neox_style=True, chunk_size=chunk, history_budget=hb,
+            row_active=row_active,
+        )
+        descs.append(desc)
+    stream = torch.cuda.current_stream(device).cuda_stream
+
+    def launch(i, stages=None):
+        desc = descs[i % len(descs)]
+        if stages is not None:
+            desc.stages = stages
+        rc = lib.ds_retrieval_step(stream, desc)
+        desc.stages = step.ALL
+        if rc:
+            _lib.check(rc)
+
+    # A full step on every copy first: the plans the gather-only timing uses.
+    for i in range(len(descs)):
+        launch(i)
+    torch.cuda.synchronize()
+
+    # Untimed warmup, then exactly K timed steps bracketed by synchronisation.
+    for i in range(args.warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_wall = time.perf_counter()
+    start.record()
+    for i in range(args.steps):
+        launch(i)
+    stop.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t_wall) * 1e3
+    chain_ms = start.elapsed_time(stop) / args.steps
+
+    # Per-kernel durations with HIP events on the launch stream.
+    def time_stage(stages, reps):
+        for i in range(3):
+            launch(i, stages)
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for i in range(reps):
+            ev[i][0].record()
+            launch(i, stages)
+            ev[i][1].record()
+        torch.cuda.synchronize()
+        return statistics.mean(a.elapsed_time(b) for a, b in ev) * 1e3  # µs
+
+    reps = max(20, args.steps // 2)
+    score_us = time_stage(step.SCORE, reps)
+    select_us = time_stage(step.SELECT, reps)
+    plan_gather_us = time_stage(step.PLAN, reps)
+
+    # Gather alone through the drop-in entry point, on the plans the chain produced.
+    from ds355.compact_kv import rebuild_compact_kv_from_plan
+    gather_ev = []
+    for i in range(reps + 3):
+        inp, st = copies[i % len(copies)], states[i % len(copies)]
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        rebuild_compact_kv_from_plan(inp["raw_k"], inp["raw_v"], st["work_k"], st["work_v"], st["plan"][:rows],
+                                     cos_sin, chunk_size=chunk, max_width=hb, rotary_dim=d, is_neox_style=True,
+                                     row_active=None if row_active is None else row_active[:rows])
+        b.record()
+        gather_ev.append((a, b))
+    torch.cuda.synchronize()
+    gather_us = statistics.mean(a.elapsed_time(b) for a, b in gather_ev[3:]) * 1e3
+
+    plan_lens = states[0]["plan"][:, 1].tolist()
+    score_bytes, gather_bytes, chain_bytes = algorithmic_bytes(spec, inp0, plan_lens, active)
+    score_gbps = score_bytes / (score_us * 1e-6) / 1e9
+    gather_gbps = gather_bytes / (gather_us * 1e-6) / 1e9
+    chain_gbps = chain_bytes / (chain_ms * 1e-3) / 1e9
+
+    # Device copy bandwidth of a plain 1 GiB copy, for context.
+    src = torch.empty(1 << 29, dtype=torch.int16, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(10):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    copy_gbps = 2 * src.numel() * 2 * 10 / (a.elapsed_time(b) * 1e-3) / 1e9
+    del src, dst
+
+    traffic = None
+    traffic_file = ROOT / "profiles" / f"traffic_{args.workload}.json"
+    if traffic_file.exists():
+        traffic = json.loads(traffic_file.read_text()).get("score_kernel_hbm_bytes_per_launch")
+
+    cpu = None if args.no_cpu_baseline else cpu_baseline(spec, copies[0], cos_sin, hb, rows_t, active, reuse)
+    if cpu is not None:
+        cpu["gpu_speedup"] = round(cpu["value"] / (chain_ms * 1e3), 1)
+
+    result = {
+        "metric": METRIC,
+        "value": round(chain_ms * 1e3, 2),
+        "unit": "µs",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(chain_ms, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.workload}: {rows} requests"
+                        + (f" + {spec.get('pad')} padding rows" if spec.get("pad") else "")
+                        + f", context {spec['lens']}, Hq {spec['hq']} / Hkv {hkv} x {d} bf16, chunk {chunk}, "
+                          f"token budget {token_budget}, history {hb}, paged K block {BLOCK_SIZE}, "
+                          f"{len(copies)} rotated input copies",
+            "global_batch": rows,
+            "seq_len": max(inp0["tlens"]),
+            "parallelism": "single GPU",
+            "scored_tokens": sum(n for n, c in zip(inp0["committed"], inp0["counts"]) if c > 0),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "chunk_score_kernel",
+            "achieved": round(score_gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(score_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes": score_bytes,
+            "avg_us": round(score_us, 2),
+        },
+        "kernels_us": {"chunk_score": round(score_us, 2), "select": round(select_us, 2),
+                       "plan_and_gather": round(plan_gather_us, 2), "gather": round(gather_us, 2)},
+        "gather_roofline": {"achieved": round(gather_gbps, 1), "frac": round(gather_gbps / HBM_PEAK_GBPS, 4),
+                            "algorithmic_bytes": gather_bytes},
+        "chain": {"algorithmic_bytes": chain_bytes, "achieved_gbps": round(chain_gbps, 1),
+                  "frac": round(chain_gbps / HBM_PEAK_GBPS, 4), "wall_ms_total": round(wall_ms, 3)},
+        "copy_gbps": round(copy_gbps, 1),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result, ensure_ascii=False), flush=True)
+
+
+def cpu_baseline(spec, inp, cos_sin, hb, rows_t, active, reuse):
+    """The oracle's CPU restatement of the reference path, timed on this host."""
+    import torch
+
+    from oracle import diffspec_oracle as O
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    chunk, token_budget, d = spec["chunk"], spec["budget"], spec["d"]
+    rows = inp["rows"]
+    t0 = time.time()
+    real = [b for b in range(inp["total_rows"]) if inp["counts"][b] > 0]
+    _, q_index, lengths = O.retrieval_rows(inp["counts"], [s + q for s, q in zip(inp["starts"], inp["qlens"])],
+                                           inp["tlens"], rows)
+    query = inp["query"][q_index].cpu()
+    lse = inp["lse"][q_index].cpu()
+    key_cache = inp["key_cache"].cpu()
+    table = inp["table"][real].cpu()
+    raw_k, raw_v = inp["raw_k"].cpu(), inp["raw_v"].cpu()
+    work_k = torch.zeros((rows, spec["hkv"], token_budget, d), dtype=torch.bfloat16)
+    work_v = torch.zeros_like(work_k)
+    cs = cos_sin.cpu()
+    slots = [inp["slots"][b] for b in real]
+    ends = [max(0, inp["committed"][b] - 1) for b in real]
+    regather = [bool(active[b]) for b in real] if reuse else None
+    log(f"cpu baseline inputs copied in {time.time() - t0:.1f}s")
+
+    def one():
+        O.retrieval_step(query, lse, key_cache, table, lengths, raw_k, raw_v, work_k, work_v, slots, ends, cs,
+                         chunk_size=chunk, budget=hb, token_budget=token_budget, scale=inp["scale"], rotary_dim=d,
+                         is_neox_style=True, regather=regather)
+
+    t = time.perf_counter()
+    one()  # warm-up
+    first = time.perf_counter() - t
+    reps = max(1, min(5, int(20.0 / max(first, 1e-3))))
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t)
+    med = statistics.median(times)
+    cpu_model = platform.processor() or ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(med * 1e6, 1),
+        "unit": "µs",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"the full step ({len(real)} requests, same inputs), median of {reps} runs after 1 warm-up; "
+                  f"os.cpu_count()={os.cpu_count()}, cpu='{cpu_model}'",
+        "gpu_speedup": None,
+    }
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--workload", default=DEFAULT_WORKLOAD, choices=sorted(WORKLOADS))
+    parser.add_argument("--copies", type=int, default=3, help="rotated input copies (defeats the 256 MB MALL)")
+    parser.add_argument("--seed", type=int, default=0)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+    run(args)
+
+
+if __name__ == "__main__":
+    main()

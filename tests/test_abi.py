@@ -1,0 +1,154 @@
+"""C-ABI checks that need no GPU: exports, struct layout, validation, no CPU fallback."""
+
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "ds355.h"
+
+
+def _declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(ds_[a-z_0-9]+)\s*\(", text)))
+
+
+def _step_desc_fields():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    body = re.search(r"typedef struct ds_step_desc \{(.*?)\} ds_step_desc;", text, flags=re.S).group(1)
+    fields = []
+    for decl in body.split(";"):
+        decl = " ".join(decl.split())
+        if not decl:
+            continue
+        m = re.match(r"(const )?(int64_t|int32_t|int|float|void)\s*(\*?)\s*(.*)", decl)
+        assert m, decl
+        kind = "ptr" if m.group(3) else m.group(2)
+        for name in m.group(4).split(","):
+            fields.append((name.strip().lstrip("*").strip(), kind))
+    return fields
+
+
+def test_library_exports_every_declared_symbol():
+    from ds355 import _lib
+
+    lib = _lib.load()
+    declared = _declared_functions()
+    assert set(declared) == set(_lib.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.ds_abi_version() == _lib.ABI_VERSION
+    nm = shutil.which("nm")
+    if nm:
+        out = subprocess.run([nm, "-D", "--defined-only", str(_lib.LIBRARY_PATH)], capture_output=True, text=True)
+        exported = set(re.findall(r" T (ds_[a-z_0-9]+)", out.stdout))
+        assert exported == set(declared)
+
+
+def test_step_desc_matches_header_fields():
+    from ds355 import _lib
+
+    sizes = {"ptr": ctypes.c_void_p, "int": ctypes.c_int, "int64_t": ctypes.c_int64, "float": ctypes.c_float,
+             "int32_t": ctypes.c_int32}
+    header = _step_desc_fields()
+    py = [(name, t) for name, t in _lib.StepDesc._fields_]
+    assert [n for n, _ in header] == [n for n, _ in py]
+    for (name, kind), (_, ctype) in zip(header, py):
+        assert ctypes.sizeof(sizes[kind]) == ctypes.sizeof(ctype), name
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_step_desc_offsets_match_c_compiler(tmp_path):
+    from ds355 import _lib
+
+    names = [n for n, _ in _lib.StepDesc._fields_]
+    src = tmp_path / "layout.c"
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {",
+             '  printf("%zu\\n", sizeof(ds_step_desc));']
+    lines += [f'  printf("%zu\\n", offsetof(ds_step_desc, {n}));' for n in names]
+    lines += ["  return 0;", "}"]
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-O0", "-o", str(exe), str(src)], check=True)
+    values = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert values[0] == ctypes.sizeof(_lib.StepDesc)
+    for name, offset in zip(names, values[1:]):
+        assert getattr(_lib.StepDesc, name).offset == offset, name
+
+
+def test_c_side_validation_reports_reference_messages():
+    """Argument checks run before any HIP call, so they are exercised without a GPU."""
+    from ds355 import _lib
+
+    lib = _lib.load()
+    rc = lib.ds_rebuild_compact_kv(None, _lib.DS_BF16, None, None, None, None, None, 1, 9, None, 16, 8,
+                                   2, 8, 1, 16, 8, 2, 3, 1, 4, None)
+    assert rc == _lib.DS_ERR_INVALID
+    assert lib.ds_last_error().decode() == "rotary_dim must be even and between zero and head_dim"
+    rc = lib.ds_rebuild_compact_kv(None, _lib.DS_BF16, None, None, None, None, None, 1, 8, None, 16, 8,
+                                   2, 8, 1, 16, 8, 2, 16, 1, 4, None)
+    assert rc == _lib.DS_ERR_INVALID
+    assert lib.ds_last_error().decode() == "plan width must be 5 + working_budget // chunk_size"
+    rc = lib.ds_chunk_scores(None, _lib.DS_BF16, None, 0, None, 0, 0, 0, None, 0, 0, None, 0, None,
+                             1, 6, 4, 128, 16, 64, 1, 1.0, 0, None, 0)
+    assert rc == _lib.DS_ERR_INVALID
+    assert lib.ds_last_error().decode() == "query heads must be divisible by KV heads"
+    rc = lib.ds_chunk_scores(None, _lib.DS_BF16, None, 0, None, 0, 0, 0, None, 0, 0, None, 0, None,
+                             1, 64, 2, 128, 16, 64, 1, 1.0, 0, None, 0)
+    assert rc == _lib.DS_ERR_UNSUPPORTED
+    rc = lib.ds_select_chunks(None, None, 4, 4, None, 1, 4, 6, None, 4, None)
+    assert rc == _lib.DS_ERR_INVALID
+    assert lib.ds_last_error().decode() == "token_budget must be a positive chunk-size multiple"
+    desc = _lib.StepDesc()
+    desc.stages = 8
+    assert lib.ds_retrieval_step(None, desc) == _lib.DS_ERR_INVALID
+    assert "unknown stage bits" in lib.ds_last_error().decode()
+
+
+def test_no_cpu_fallback():
+    """Every product entry point refuses CPU tensors instead of computing on the host."""
+    from ds355.compact_kv import rebuild_compact_kv_from_plan
+    from ds355.kernels import paged_chunk_attention_scores
+    from ds355.selection import select_context_chunks
+
+    q = torch.zeros((1, 4, 32), dtype=torch.bfloat16)
+    k = torch.zeros((2, 16, 1, 32), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU only"):
+        paged_chunk_attention_scores(q, k, torch.zeros(4), torch.zeros((1, 2), dtype=torch.int32),
+                                     torch.ones(1, dtype=torch.int32), chunk_size=4, max_seq_len=4, scale=1.0)
+    with pytest.raises(ValueError, match="GPU only"):
+        select_context_chunks(torch.rand(4), 16, 4, 8)
+    raw = torch.zeros((2, 8, 1, 32), dtype=torch.bfloat16)
+    work = torch.zeros((2, 1, 8, 32), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU only"):
+        rebuild_compact_kv_from_plan(raw, raw, work, work, torch.zeros((1, 9), dtype=torch.int64),
+                                     torch.zeros((8, 32), dtype=torch.bfloat16), chunk_size=2, max_width=2,
+                                     rotary_dim=32, is_neox_style=True)
+
+
+def test_reference_validation_order_on_host():
+    """The drop-in wrappers raise the reference's messages before touching the device."""
+    from ds355.compact_kv import rebuild_compact_kv_from_plan
+    from ds355.kernels import paged_chunk_attention_scores
+
+    with pytest.raises(ValueError, match=r"query must have shape \[batch, query_heads, head_dim\]"):
+        paged_chunk_attention_scores(torch.zeros(4, 32), torch.zeros(1, 1, 1, 32), torch.zeros(4),
+                                     torch.zeros(1, 1), torch.zeros(1), chunk_size=4, max_seq_len=4, scale=1.0)
+    with pytest.raises(ValueError, match="key_cache must have shape"):
+        paged_chunk_attention_scores(torch.zeros(1, 4, 32), torch.zeros(1, 32), torch.zeros(4),
+                                     torch.zeros(1, 1), torch.zeros(1), chunk_size=4, max_seq_len=4, scale=1.0)
+    raw = torch.zeros((2, 8, 1, 32))
+    with pytest.raises(ValueError, match="raw key/value must have matching 4-D shapes"):
+        rebuild_compact_kv_from_plan(raw, raw[:1], raw, raw, torch.zeros((1, 9), dtype=torch.int64),
+                                     torch.zeros((8, 32)), chunk_size=2, max_width=2, rotary_dim=32,
+                                     is_neox_style=True)
+    with pytest.raises(ValueError, match="working cache slot, head and head dimensions must match raw KV"):
+        work = torch.zeros((3, 1, 8, 32))
+        rebuild_compact_kv_from_plan(raw, raw, work, work, torch.zeros((1, 9), dtype=torch.int64),
+                                     torch.zeros((8, 32)), chunk_size=2, max_width=2, rotary_dim=32,
+                                     is_neox_style=True)

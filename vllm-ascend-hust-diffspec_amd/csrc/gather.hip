@@ -346,11 +346,13 @@ int rebuild_compact_kv_impl(hipStream_t stream, int dtype, const void* raw_key, 
                             void* working_key, void* working_value, const int64_t* plan, int rows,
                             int plan_width, const void* cos_sin, int64_t cs_stride, int cs_rows, int num_slots,
                             int max_model_len, int heads, int head_dim, int token_budget, int chunk_size,
-                            int rotary_dim, int is_neox_style, int max_width, const int32_t* row_active) {
+                            int rotary_dim, int is_neox_style, int max_width, const int32_t* row_active,
+                            bool padded_rows) {
   DS_REQUIRE(dtype == DS_BF16 || dtype == DS_FP16 || dtype == DS_FP32, "KV caches must use BF16, FP16 or FP32");
   DS_REQUIRE(rows >= 0 && num_slots > 0 && max_model_len > 0 && heads > 0 && head_dim > 0,
              "raw sequence, head and head dimensions must be positive");
-  DS_REQUIRE(rows <= num_slots, "KV plan exceeds the working cache batch or token capacity");
+  // Plans of a padded batch may have more rows than slots (padding rows are empty).
+  DS_REQUIRE(padded_rows || rows <= num_slots, "KV plan exceeds the working cache batch or token capacity");
   DS_REQUIRE(max_width >= 0 && max_width <= token_budget,
              "KV plan exceeds the working cache batch or token capacity");
   DS_REQUIRE(rotary_dim >= 0 && rotary_dim <= head_dim && rotary_dim % 2 == 0,
@@ -410,5 +412,5 @@ extern "C" int ds_rebuild_compact_kv(ds_stream_t stream, int dtype, const void* 
   return ds355::rebuild_compact_kv_impl(reinterpret_cast<hipStream_t>(stream), dtype, raw_key, raw_value,
                                         working_key, working_value, plan, rows, plan_width, cos_sin, cs_stride,
                                         cs_rows, num_slots, max_model_len, heads, head_dim, token_budget,
-                                        chunk_size, rotary_dim, is_neox_style, max_width, row_active);
+                                        chunk_size, rotary_dim, is_neox_style, max_width, row_active, false);
 }

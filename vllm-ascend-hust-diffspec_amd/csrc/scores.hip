@@ -248,6 +248,7 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
              "query and key cache must be 16-byte aligned");
   if (batch == 0 || max_chunks == 0) return clear_error();
   DS_REQUIRE(query && key_cache && lse && block_table && out, "null tensor pointer");
+  DS_REQUIRE(src.seq_lens != nullptr || src.counts != nullptr, "null seq_lens pointer");
 
   ScoreArgs a{};
   a.q = static_cast<const uint16_t*>(query);
@@ -296,7 +297,6 @@ extern "C" int ds_chunk_scores(ds_stream_t stream, int dtype, const void* query,
                                const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                int block_size, int chunk_size, int max_chunks, float scale, int head_reduce,
                                float* out, int64_t out_stride) {
-  if (batch > 0) DS_REQUIRE(seq_lens != nullptr, "null seq_lens pointer");
   ds355::RowSource src{};
   src.seq_lens = seq_lens;
   return ds355::launch_chunk_scores(reinterpret_cast<hipStream_t>(stream), dtype, query, q_stride, key_cache,

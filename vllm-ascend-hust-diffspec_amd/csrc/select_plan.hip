@@ -224,7 +224,7 @@ int launch_select_plan(hipStream_t stream, const float* scores, int64_t score_st
     DS_REQUIRE(recent_window > 0, "recent_window must be positive");
   }
   if (batch == 0) return clear_error();
-  if (do_select) DS_REQUIRE(scores && ids && counts, "null selection pointer");
+  if (do_select) DS_REQUIRE(scores && ids && counts && (src.seq_lens || src.counts), "null selection pointer");
   if (do_plan) DS_REQUIRE(ids && counts && committed_lens && plan, "null plan pointer");
 
   SelectArgs a{};
@@ -255,7 +255,6 @@ int launch_select_plan(hipStream_t stream, const float* scores, int64_t score_st
 extern "C" int ds_select_chunks(ds_stream_t stream, const float* scores, int64_t score_stride, int score_cols,
                                 const int32_t* seq_lens, int batch, int chunk_size, int history_budget,
                                 int32_t* ids, int64_t ids_stride, int32_t* counts) {
-  if (batch > 0) DS_REQUIRE(seq_lens != nullptr, "null seq_lens pointer");
   DS_REQUIRE(chunk_size > 0, "chunk_size must be positive");
   DS_REQUIRE(score_cols >= 0 && score_cols <= score_stride, "score_cols must be between 0 and the row stride");
   ds355::RowSource src{};

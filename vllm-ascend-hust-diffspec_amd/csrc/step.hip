@@ -25,7 +25,8 @@ int rebuild_compact_kv_impl(hipStream_t stream, int dtype, const void* raw_key, 
                             void* working_key, void* working_value, const int64_t* plan, int rows,
                             int plan_width, const void* cos_sin, int64_t cs_stride, int cs_rows, int num_slots,
                             int max_model_len, int heads, int head_dim, int token_budget, int chunk_size,
-                            int rotary_dim, int is_neox_style, int max_width, const int32_t* row_active);
+                            int rotary_dim, int is_neox_style, int max_width, const int32_t* row_active,
+                            bool padded_rows);
 
 }  // namespace ds355
 
@@ -77,5 +78,6 @@ extern "C" int ds_retrieval_step(ds_stream_t stream_handle, const ds_step_desc* 
   return rebuild_compact_kv_impl(stream, d->kv_dtype, d->raw_key, d->raw_value, d->working_key, d->working_value,
                                  d->plan, d->batch_rows, d->plan_width, d->cos_sin, d->cs_stride, d->cs_rows,
                                  d->num_slots, d->max_model_len, d->draft_heads, d->draft_head_dim, d->token_budget,
-                                 d->chunk_size, d->rotary_dim, d->is_neox_style, d->history_budget, d->row_active);
+                                 d->chunk_size, d->rotary_dim, d->is_neox_style, d->history_budget, d->row_active,
+                                 true);
 }

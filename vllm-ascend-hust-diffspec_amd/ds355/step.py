@@ -60,7 +60,30 @@ class VerifierRows:
 SCORE, SELECT, PLAN, ALL = _lib.DS_STAGE_SCORE, _lib.DS_STAGE_SELECT, _lib.DS_STAGE_PLAN, _lib.DS_STAGE_ALL
 
 
-def retrieval_step(
+def retrieval_step(**kwargs) -> None:
+    """Run the stages of one step (see ``build_step_desc`` for the arguments)."""
+    desc, device = build_step_desc(**kwargs)
+    launch(desc, device)
+
+
+def launch(desc: _lib.StepDesc, device: torch.device, stages: int | None = None) -> None:
+    """Launch a prebuilt descriptor on the current stream of ``device``.
+
+    The descriptor holds raw device addresses: the tensors it was built from
+    must stay alive and keep their storage.  ``stages`` overrides the
+    descriptor's stage mask for this call.
+    """
+    if stages is not None:
+        saved = desc.stages
+        desc.stages = stages
+    try:
+        _lib.check(_lib.load().ds_retrieval_step(_lib.stream_handle(device), desc))
+    finally:
+        if stages is not None:
+            desc.stages = saved
+
+
+def build_step_desc(
     *,
     stages: int = ALL,
     snapshot: VerifierSnapshot | None,
@@ -83,8 +106,8 @@ def retrieval_step(
     history_budget: int,
     recent_window: int | None = None,
     row_active: torch.Tensor | None = None,
-) -> None:
-    """Run the stages in ``stages`` (``SCORE | SELECT | PLAN``; ``ALL`` = one step).
+) -> tuple[_lib.StepDesc, torch.device]:
+    """Validate and pack a step descriptor for ``stages`` (``SCORE | SELECT | PLAN``; ``ALL`` = one step).
 
     SCORE needs ``snapshot``; SCORE and SELECT need ``rows`` and ``scores``, a
     ``[batch_rows, max_chunks]`` fp32 buffer whose ``max_chunks`` covers
@@ -182,5 +205,4 @@ def retrieval_step(
     desc.row_active = _lib.ptr(row_active)
     desc.chunk_size, desc.history_budget = chunk_size, history_budget
     desc.recent_window = chunk_size if recent_window is None else recent_window
-    lib = _lib.load()
-    _lib.check(lib.ds_retrieval_step(_lib.stream_handle(device), desc))
+    return desc, device

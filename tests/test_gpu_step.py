@@ -184,6 +184,8 @@ def test_zero_count_rows_keep_previous_selection(cuda):
     case2["counts"] = [2, 0, 1, 3, 0, 5, 0, 0]
     case2["committed"] = [tl - ql + min(max(c, 1), ql) for tl, ql, c in
                           zip(case["tlens"], case["qlens"], case2["counts"])]
+    state["work_k"].fill_(float("nan"))  # fresh sentinel: only this cycle's writes are checked
+    state["work_v"].fill_(float("nan"))
     state = run_gpu(case2, cuda, state=state)
     check_step(case2, state, previous=first)
 
@@ -200,11 +202,9 @@ def test_stress_64_rows_reuse_half(cuda):
     full_k, full_v = state["work_k"].clone(), state["work_v"].clone()
     # Same step again with a random half flagged for reuse: the result must not change.
     active = [int(x) for x in (torch.rand(64, generator=g) < 0.5)]
-    state["work_k"][torch.tensor([i for i in range(64) if not active[i]], dtype=torch.long)] = full_k[
-        torch.tensor([i for i in range(64) if not active[i]], dtype=torch.long)]
     run_gpu(case, cuda, state=state, row_active=active)
-    assert torch.equal(state["work_k"], full_k)
-    assert torch.equal(state["work_v"], full_v)
+    assert torch.equal(torch.nan_to_num(state["work_k"]), torch.nan_to_num(full_k))
+    assert torch.equal(torch.nan_to_num(state["work_v"]), torch.nan_to_num(full_v))
     # Re-gathered rows really are rewritten; reused rows are not touched.
     state["work_k"].fill_(float("nan"))
     state["work_v"].fill_(float("nan"))

@@ -167,6 +167,7 @@ def run(args):
     for inp in copies:
         st = dict(
             scores=torch.zeros((total_rows, max_chunks), dtype=torch.float32, device=device),
+            partials=torch.zeros((total_rows, max_chunks, hkv), dtype=torch.float32, device=device),
             sel_ids=torch.zeros((rows, token_budget // chunk), dtype=torch.int32, device=device),
             sel_count=torch.full((rows,), -1, dtype=torch.int32, device=device),
             plan=torch.zeros((total_rows, 5 + token_budget // chunk), dtype=torch.int64, device=device),
@@ -181,7 +182,7 @@ def run(args):
         desc, _ = step.build_step_desc(
             snapshot=step.VerifierSnapshot(inp["query"], inp["lse"], inp["key_cache"], inp["table"], inp["scale"]),
             rows=step.VerifierRows(rows_t["counts"], rows_t["starts"], rows_t["qlens"], rows_t["tlens"], rows),
-            scores=st["scores"], sel_ids=st["sel_ids"], sel_count=st["sel_count"], slots=rows_t["slots"],
+            scores=st["scores"], score_partials=st["partials"], sel_ids=st["sel_ids"], sel_count=st["sel_count"], slots=rows_t["slots"],
             committed_lens=rows_t["committed"], plan=st["plan"], working_lens=st["working_lens"],
             raw_key=inp["raw_k"], raw_value=inp["raw_v"], working_key=st["work_k"], working_value=st["work_v"],
             cos_sin_cache=cos_sin, rotary_dim=d, is_neox_style=True, chunk_size=chunk, history_budget=hb,

@@ -60,8 +60,12 @@ int ds_abi_version(void);
  * key_cache: element (block, i, kvh, d) at
  *            k[block * k_block_stride + i * k_token_stride + kvh * k_head_stride + d].
  * dtype   : DS_BF16 or DS_FP16 (query and key_cache share it).
+ * workspace: caller-owned device scratch of batch * max_chunks * Hkv floats
+ *           (per-KV-head partial sums; unused with DS_HEAD_MAX).  Two
+ *           kernels: the streaming pass and a small finalize pass.
  * Limits  : head_dim % 32 == 0 and <= 256, Hq % Hkv == 0, Hq / Hkv <= 16,
- *           batch <= 1024.
+ *           batch <= 1024; DS_HEAD_MAX needs chunk <= 128 or a chunk that
+ *           divides 64.
  */
 int ds_chunk_scores(ds_stream_t stream, int dtype,
                     const void* query, int64_t q_stride,
@@ -72,7 +76,8 @@ int ds_chunk_scores(ds_stream_t stream, int dtype,
                     const int32_t* seq_lens,
                     int batch, int num_q_heads, int num_kv_heads, int head_dim,
                     int block_size, int chunk_size, int max_chunks, float scale,
-                    int head_reduce, float* out, int64_t out_stride);
+                    int head_reduce, float* out, int64_t out_stride,
+                    float* workspace, size_t workspace_bytes);
 
 /*
  * Batched top-k chunk selection.
@@ -175,7 +180,8 @@ typedef struct ds_step_desc {
   int num_q_heads, num_kv_heads, head_dim;
   float scale;
   int max_chunks;                    /* >= ceil(max scored length / chunk)    */
-  float* scores;                     /* [batch_rows, max_chunks] scratch out  */
+  float* scores;                     /* [batch_rows, max_chunks] final scores (written by SELECT) */
+  float* score_partials;             /* [batch_rows, max_chunks, Hkv] per-KV-head sums (SCORE -> SELECT) */
   int stages;                        /* DS_STAGE_* bit mask                   */
   /* selection state, per slot */
   int32_t* sel_ids;                  /* [num_slots, sel_stride]               */

@@ -95,11 +95,11 @@ def test_c_side_validation_reports_reference_messages():
     assert rc == _lib.DS_ERR_INVALID
     assert lib.ds_last_error().decode() == "plan width must be 5 + working_budget // chunk_size"
     rc = lib.ds_chunk_scores(None, _lib.DS_BF16, None, 0, None, 0, 0, 0, None, 0, 0, None, 0, None,
-                             1, 6, 4, 128, 16, 64, 1, 1.0, 0, None, 0)
+                             1, 6, 4, 128, 16, 64, 1, 1.0, 0, None, 0, None, 0)
     assert rc == _lib.DS_ERR_INVALID
     assert lib.ds_last_error().decode() == "query heads must be divisible by KV heads"
     rc = lib.ds_chunk_scores(None, _lib.DS_BF16, None, 0, None, 0, 0, 0, None, 0, 0, None, 0, None,
-                             1, 64, 2, 128, 16, 64, 1, 1.0, 0, None, 0)
+                             1, 64, 2, 128, 16, 64, 1, 1.0, 0, None, 0, None, 0)
     assert rc == _lib.DS_ERR_UNSUPPORTED
     rc = lib.ds_select_chunks(None, None, 4, 4, None, 1, 4, 6, None, 4, None)
     assert rc == _lib.DS_ERR_INVALID

@@ -60,6 +60,7 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None):
     if state is None:
         state = dict(
             scores=torch.zeros((rows, max_chunks), dtype=torch.float32, device=device),
+            partials=torch.zeros((rows, max_chunks, case["hkv"]), dtype=torch.float32, device=device),
             sel_ids=torch.zeros((case["num_slots"], case["token_budget"] // case["chunk"]), dtype=torch.int32,
                                 device=device),
             sel_count=torch.full((case["num_slots"],), -1, dtype=torch.int32, device=device),
@@ -78,7 +79,7 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None):
                                        case["scale"]),
         rows=step.VerifierRows(i32(case["counts"]), i32(case["starts"]), i32(case["qlens"]), i32(case["tlens"]),
                                case["real_rows"]),
-        scores=state["scores"], sel_ids=state["sel_ids"], sel_count=state["sel_count"], slots=i32(case["slots"]),
+        scores=state["scores"], score_partials=state["partials"], sel_ids=state["sel_ids"], sel_count=state["sel_count"], slots=i32(case["slots"]),
         committed_lens=i32(case["committed"]), plan=state["plan"], working_lens=state["working_lens"],
         raw_key=state["raw_k"], raw_value=state["raw_v"], working_key=state["work_k"],
         working_value=state["work_v"], cos_sin_cache=state["cos_sin"], rotary_dim=case["head_dim"],

@@ -2,26 +2,36 @@
 //
 // Counterpart of diffspec/kernels.py:11-150.  The reference launches one
 // program per (row, chunk, query head), so every key row is fetched once per
-// query head of its GQA group.  Here a workgroup owns one (row, chunk) unit
-// across all heads: each key row is loaded once, straight from HBM into the
-// B operand of v_mfma_f32_16x16x32_{bf16,f16} (16 tokens x 32 dims per
-// instruction, 16 bytes per lane), and multiplied by all query heads of its
-// KV head at once (A operand: up to 16 heads x 32 dims, kept in registers).
-// The 16x16 fp32 logits come back 4 per lane (rows = heads, column =
-// token), are turned into exp(scale*logit - lse) in registers, summed in the
-// lane, then across the wave with shuffles and across the 4 waves through
-// LDS.  The head mean (kernels.py:150) is fused: out = sum / (Hq * n_valid).
+// query head of its GQA group.  Here every key row is loaded once, straight
+// from HBM into the B operand of v_mfma_f32_16x16x32_{bf16,f16} (16 tokens x
+// 32 dims per instruction, 16 bytes per lane), and multiplied by all query
+// heads of its KV head at once (A operand: up to 16 heads x 32 dims).  The
+// 16x16 fp32 logits come back 4 per lane (rows = heads, column = token) and
+// are turned into exp(scale * logit - lse) in registers.
 //
-// Units (row, chunk) of a ragged batch are numbered by an exclusive prefix
-// sum over per-row chunk counts that each workgroup builds in LDS; the grid
-// is persistent over that list.
+// Work decomposition.  A unit is (row, span of U tokens, KV head), U = the
+// chunk size rounded up to 64 tokens when the chunk divides 64 (so a unit
+// holds 1..4 whole chunks).  Units are numbered through an exclusive prefix
+// sum over per-row unit counts built in LDS, and every wave of the persistent
+// grid walks its own strided unit list with no block barrier: the units are
+// small and uniform, so the static split leaves a short tail.  Each wave runs
+// a three-stage software pipeline over 16-token-group batches: block-table
+// lookups (uniform, scalar loads) two batches ahead, key / query / LSE loads
+// one batch ahead, MFMA + exp on the current batch.  A unit's per-chunk sums
+// are reduced across the wave with shuffles and stored as partials
+// [row, chunk, KV head]; the head sum and the 1 / (Hq * n_valid)
+// normalisation (kernels.py:80-82, 150) happen where the partials are read:
+// in the selection kernel for a retrieval step, or in finalize_kernel for
+// the drop-in entry point.  The per-token head max (head_reduce = max) keeps
+// all KV heads of a span in one wave and writes final scores directly.
 #include "rowdesc.h"
 
 namespace ds355 {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kMaxChunkForMax = 2048;  // LDS per-token maxima (head_reduce=max)
+constexpr int kWaves = 4;
+constexpr int kMaxNtu = 8;  // 16-token groups per unit with head_reduce = max (U <= 128)
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -41,9 +51,13 @@ struct ScoreArgs {
   const int32_t* bt;
   int64_t bt_stride;
   RowSource src;
-  int batch, Hq, Hkv, D, block_size, chunk, max_chunks;
+  int batch, Hq, Hkv, G, D, block_size, chunk, max_chunks;
+  int U;    // tokens per unit
+  int cpu;  // chunks per unit
+  int ntu;  // 16-token groups per unit
   float scale;
-  float* out;
+  float* partial;  // [batch, max_chunks, Hkv] (head mean) — per-KV-head sums
+  float* out;      // [batch, out_stride] final scores (head max; tail zeros)
   int64_t out_stride;
   int write_tail;
 };
@@ -59,175 +73,330 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(const Raw16& a, const Raw16& b, 
   }
 }
 
-__device__ __forceinline__ int row_units(const ScoreArgs& a, int b) {
-  const RowDesc d = row_desc(a.src, b);
-  return d.active ? (d.len + a.chunk - 1) / a.chunk : 0;
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Load through the constant address space: a wave-uniform address becomes a
+// scalar (SMEM) load, counted by lgkmcnt instead of the in-order vmcnt, so
+// waiting for it never drains the key loads in flight.  Only for memory the
+// kernel does not write.
+__device__ __forceinline__ int32_t scalar_load(const int32_t* p) {
+  typedef const __attribute__((address_space(4))) int32_t* const_ptr;
+  return *(const_ptr)(p);
 }
 
-// STEPS = head_dim / 32 (MFMA k-steps per key row).  HMAX selects the
-// per-token max over heads instead of the head mean.
-template <int DT, int STEPS, bool HMAX>
-__global__ __launch_bounds__(kThreads) void chunk_score_kernel(ScoreArgs a) {
-  constexpr int kBatch = STEPS >= 16 ? 1 : 16 / STEPS;  // items per load batch (64 VGPRs of keys)
-  __shared__ int s_prefix[kMaxRows + 1];
-  __shared__ int s_scratch[4];
-  __shared__ float s_red[2][4];
-  __shared__ unsigned s_tokmax[HMAX ? kMaxChunkForMax : 1];
+// Where a batch sits in the wave's stream.  All fields are wave-uniform.
+struct BatchCtx {
+  int valid;
+  int b;
+  int t0;    // first token of the unit
+  int len;   // row's scored length
+  int qrow;  // query / LSE row
+  int g;     // KV head
+  int tg0;   // first 16-token group of the batch within the unit
+  int last;  // last batch of the unit
+  int c0;    // first chunk of the unit
+  int64_t qbase;  // element offset of (qrow, first query head of g) in q
+  int64_t lbase;  // element offset of (qrow, first query head of g) in lse
+};
 
-  if (HMAX) {
-    for (int t = threadIdx.x; t < kMaxChunkForMax; t += kThreads) s_tokmax[t] = 0u;
+template <int KB, int STEPS>
+struct Batch {
+  Raw16 k[KB][STEPS];
+  Raw16 q[STEPS];
+  float lse[4];
+  BatchCtx c;
+};
+
+// STEPS = head_dim / 32.  KB = 16-token groups per batch.  HMAX = per-token
+// head max.  UNIFORM_PAGE = every 16-token group lies inside one block
+// (block_size and the unit start are multiples of 16), so its block-table
+// entry is one scalar load.
+template <int DT, int STEPS, int KB, bool HMAX, bool UNIFORM_PAGE>
+__global__ __launch_bounds__(kThreads, 2) void chunk_score_kernel(ScoreArgs a) {
+  __shared__ int s_prefix[kMaxRows + 1];
+  __shared__ int s_len[kMaxRows];
+  __shared__ int s_qrow[kMaxRows];
+  __shared__ int s_scratch[4];
+
+  const int units_per_span = HMAX ? 1 : a.Hkv;
+  for (int r = threadIdx.x; r < a.batch; r += kThreads) {
+    const RowDesc d = row_desc(a.src, r);
+    s_len[r] = d.active ? d.len : 0;
+    s_qrow[r] = static_cast<int>(d.qrow);
   }
-  build_row_prefix(a.batch, s_prefix, s_scratch, [&](int b) { return row_units(a, b); });
+  __syncthreads();
+  build_row_prefix(a.batch, s_prefix, s_scratch,
+                   [&](int r) { return (s_len[r] + a.U - 1) / a.U * units_per_span; });
   const int total = s_prefix[a.batch];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
   const int col = lane & 15;   // A row (query head in group) / B column (token in group)
-  const int kgrp = lane >> 4;  // which 8-element k slice of the 32-wide step
-  const int G = a.Hq / a.Hkv;
-  const int NT = (a.chunk + 15) / 16;
-  const int items = NT * a.Hkv;                    // (kv head, 16-token group) pairs per unit
-  const int per_wave = (items + 3) / 4;
-  const int item_begin = wave * per_wave;
-  const int item_end = min(items, item_begin + per_wave);
-  const float inv_heads = 1.0f / static_cast<float>(a.Hq);
+  const int kgrp = lane >> 4;  // 8-element k slice of the 32-wide MFMA step
+  const int gw = uniform(blockIdx.x * kWaves + (threadIdx.x >> 6));
+  const int tw = gridDim.x * kWaves;
+  const int bph = (a.ntu + KB - 1) / KB;     // batches per KV head of a unit
+  const int bpu = bph * (HMAX ? a.Hkv : 1);  // batches per unit
 
-  int parity = 0;
-  for (int unit = blockIdx.x; unit < total; unit += gridDim.x, parity ^= 1) {
-    const int b = find_row(s_prefix, a.batch, unit);
-    const int c = unit - s_prefix[b];
-    const RowDesc d = row_desc(a.src, b);
-    const int t_begin = c * a.chunk;
-    const int n_valid = min(a.chunk, d.len - t_begin);
-    const uint16_t* qrow = a.q + d.qrow * a.q_stride;
-    const int32_t* bt_row = a.bt + static_cast<int64_t>(b) * a.bt_stride;
+  int row_hint = 0;
+  auto ctx_of = [&](int n) -> BatchCtx {
+    BatchCtx c{};
+    const int k = n / bpu;
+    const int j = n - k * bpu;
+    const int unit = gw + k * tw;
+    if (unit >= total) return c;
+    int lo = row_hint, hi = a.batch - 1;  // unit positions grow along the stream
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_prefix[mid] <= unit) lo = mid; else hi = mid - 1;
+    }
+    row_hint = lo;
+    const int r = unit - s_prefix[lo];
+    const int span = HMAX ? r : r / a.Hkv;
+    const int head_in_unit = j / bph;
+    c.valid = 1;
+    c.b = lo;
+    c.t0 = span * a.U;
+    c.len = s_len[lo];
+    c.qrow = s_qrow[lo];
+    c.g = (HMAX ? 0 : r - span * a.Hkv) + head_in_unit;
+    c.tg0 = (j - head_in_unit * bph) * KB;
+    c.last = j == bpu - 1;
+    c.c0 = span * a.cpu;
+    c.qbase = static_cast<int64_t>(c.qrow) * a.q_stride + static_cast<int64_t>(c.g * a.G) * a.D;
+    c.lbase = static_cast<int64_t>(c.qrow) * a.lse_row_stride + static_cast<int64_t>(c.g * a.G) * a.lse_head_stride;
+    return c;
+  };
 
-    float acc = 0.f;
-    int cached_g = -1;
-    Raw16 qa[STEPS];
-    float lse4[4];
-
-    for (int i0 = item_begin; i0 < item_end; i0 += kBatch) {
-      Raw16 kb[kBatch][STEPS];
-      // Load phase: all key vectors of the batch are in flight together.
+  // Every load below is issued unconditionally, from wave-uniform bases plus
+  // small per-lane offsets: lanes and batches with nothing to read use a
+  // valid dummy address (row 0, or a clamped head / in-block row) and
+  // compute() masks them.  Each batch therefore adds a fixed number of loads,
+  // and the wait for the batch being computed never drains the next batch.
+  //
+  // kb[i] = element offset of token group i's first row for KV head g
+  // (uniform: the group lies inside one block).  Reading lanes past the row
+  // end stays inside that block.
+  auto pages_of = [&](const BatchCtx& c, int64_t (&kb)[KB]) {
 #pragma unroll
-      for (int ib = 0; ib < kBatch; ++ib) {
-        const int item = i0 + ib;
-        const int g = item / NT;
-        const int tg = item - g * NT;
-        const int tin = tg * 16 + col;
-        const int t = t_begin + tin;
-        const bool valid = item < item_end && tin < a.chunk && t < d.len;
-        if (valid) {
-          const int64_t page = bt_row[t / a.block_size];
-          const uint16_t* krow = a.k + page * a.k_block_stride + static_cast<int64_t>(t % a.block_size) * a.k_token_stride +
-                                 static_cast<int64_t>(g) * a.k_head_stride + kgrp * 8;
-#pragma unroll
-          for (int s = 0; s < STEPS; ++s) kb[ib][s] = *reinterpret_cast<const Raw16*>(krow + 32 * s);
-        } else {
-#pragma unroll
-          for (int s = 0; s < STEPS; ++s) kb[ib][s] = Raw16{{0u, 0u, 0u, 0u}};
-        }
+    for (int i = 0; i < KB; ++i) {
+      kb[i] = 0;
+      if (UNIFORM_PAGE) {
+        const int tg = c.tg0 + i;
+        const int tok0 = c.t0 + tg * 16;
+        const bool ok = c.valid && tg < a.ntu && tok0 < c.len;
+        const int64_t idx = ok ? static_cast<int64_t>(c.b) * a.bt_stride + uniform(tok0 / a.block_size) : 0;
+        const int64_t page = scalar_load(a.bt + idx);
+        kb[i] = ok ? page * a.k_block_stride + static_cast<int64_t>(tok0 % a.block_size) * a.k_token_stride +
+                         static_cast<int64_t>(c.g) * a.k_head_stride
+                   : 0;
       }
-      // Compute phase.
+    }
+  };
+
+  const int64_t lane_k = static_cast<int64_t>(col) * a.k_token_stride + kgrp * 8;
+  const int q_head = min(col, a.G - 1);  // rows >= G read a real head; masked later
+
+  auto load = [&](const BatchCtx& c, const int64_t (&kb)[KB], Batch<KB, STEPS>& out) {
+    out.c = c;
 #pragma unroll
-      for (int ib = 0; ib < kBatch; ++ib) {
-        const int item = i0 + ib;
-        if (item >= item_end) continue;  // wave-uniform
-        const int g = item / NT;
-        const int tg = item - g * NT;
-        if (g != cached_g) {
-          cached_g = g;
-          const bool head_ok = col < G;
-          const uint16_t* qh = qrow + static_cast<int64_t>(g * G + col) * a.D + kgrp * 8;
-#pragma unroll
-          for (int s = 0; s < STEPS; ++s) {
-            qa[s] = head_ok ? *reinterpret_cast<const Raw16*>(qh + 32 * s) : Raw16{{0u, 0u, 0u, 0u}};
-          }
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int m = 4 * kgrp + i;
-            lse4[i] = m < G ? a.lse[d.qrow * a.lse_row_stride + static_cast<int64_t>(g * G + m) * a.lse_head_stride]
-                            : 0.f;
-          }
-        }
-        f32x4_t logit = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < STEPS; ++s) logit = mfma16x16x32<DT>(qa[s], kb[ib][s], logit);
+    for (int i = 0; i < KB; ++i) {
+      const uint16_t* krow;
+      if (UNIFORM_PAGE) {
+        krow = a.k + kb[i] + lane_k;
+      } else {
+        const int tg = c.tg0 + i;
         const int tin = tg * 16 + col;
-        const bool tok_ok = tin < a.chunk && t_begin + tin < d.len;
-        if (HMAX) {
-          float m4 = 0.f;
+        const int tok = c.t0 + tin;
+        const bool ok = c.valid && tg < a.ntu && tin < a.U && tok < c.len;
+        const int64_t page = a.bt[ok ? static_cast<int64_t>(c.b) * a.bt_stride + tok / a.block_size : 0];
+        const int64_t off = ok ? page * a.k_block_stride + static_cast<int64_t>(tok % a.block_size) * a.k_token_stride +
+                                     static_cast<int64_t>(c.g) * a.k_head_stride
+                               : 0;
+        krow = a.k + off + kgrp * 8;
+      }
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int m = 4 * kgrp + i;
-            if (m < G && tok_ok) m4 = fmaxf(m4, __expf(logit[i] * a.scale - lse4[i]));
-          }
-          m4 = fmaxf(m4, __shfl_xor(m4, 16, 64));
-          m4 = fmaxf(m4, __shfl_xor(m4, 32, 64));
-          if (kgrp == 0 && tok_ok) atomicMax(&s_tokmax[tin], __float_as_uint(m4));
-        } else {
+      for (int s = 0; s < STEPS; ++s) out.k[i][s] = *reinterpret_cast<const Raw16*>(krow + 32 * s);
+    }
+    const uint16_t* qh = a.q + c.qbase + static_cast<int64_t>(q_head) * a.D + kgrp * 8;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int m = 4 * kgrp + i;
-            if (m < G && tok_ok) acc += __expf(logit[i] * a.scale - lse4[i]);
-          }
+    for (int s = 0; s < STEPS; ++s) out.q[s] = *reinterpret_cast<const Raw16*>(qh + 32 * s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = min(4 * kgrp + i, a.G - 1);
+      out.lse[i] = a.lse[c.lbase + static_cast<int64_t>(m) * a.lse_head_stride];
+    }
+  };
+
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};  // per chunk of the unit (head mean)
+  float tmax[kMaxNtu];                  // per 16-token group (head max)
+#pragma unroll
+  for (int t = 0; t < kMaxNtu; ++t) tmax[t] = 0.f;
+
+  auto compute = [&](const Batch<KB, STEPS>& bt) {
+    const BatchCtx& c = bt.c;
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+      const int tg = c.tg0 + i;
+      if (tg >= a.ntu) continue;  // wave-uniform
+      f32x4_t logit = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s) logit = mfma16x16x32<DT>(bt.q[s], bt.k[i][s], logit);
+      const int tin = tg * 16 + col;
+      const bool tok_ok = tin < a.U && c.t0 + tin < c.len;
+      if (HMAX) {
+        float m4 = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (4 * kgrp + e < a.G && tok_ok) m4 = fmaxf(m4, __expf(logit[e] * a.scale - bt.lse[e]));
+        }
+        m4 = fmaxf(m4, __shfl_xor(m4, 16, 64));
+        m4 = fmaxf(m4, __shfl_xor(m4, 32, 64));
+#pragma unroll
+        for (int t = 0; t < kMaxNtu; ++t) {
+          if (t == tg) tmax[t] = fmaxf(tmax[t], m4);
+        }
+      } else {
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (4 * kgrp + e < a.G && tok_ok) s += __expf(logit[e] * a.scale - bt.lse[e]);
+        }
+        const int ci = (tg * 16) / a.chunk;  // chunk of the unit (uniform; 0 when the unit is one chunk)
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+          if (cc == ci) acc[cc] += s;
         }
       }
     }
-
+    if (!c.last) return;
+    const int chunks_row = (c.len + a.chunk - 1) / a.chunk;
     if (HMAX) {
-      __syncthreads();
-      for (int t = threadIdx.x; t < a.chunk; t += kThreads) {
-        acc += __uint_as_float(s_tokmax[t]);
-        s_tokmax[t] = 0u;
+      for (int cc = 0; cc < a.cpu; ++cc) {
+        float s = 0.f;
+#pragma unroll
+        for (int t = 0; t < kMaxNtu; ++t) {
+          if (kgrp == 0 && t < a.ntu && (t * 16) / a.chunk == cc && t * 16 + col < a.U &&
+              c.t0 + t * 16 + col < c.len) {
+            s += tmax[t];
+          }
+        }
+        s = wave_sum(s);
+        const int ch = c.c0 + cc;
+        if (lane == 0 && ch < chunks_row) {
+          const int n_valid = min(a.chunk, c.len - ch * a.chunk);
+          a.out[static_cast<int64_t>(c.b) * a.out_stride + ch] = s / static_cast<float>(n_valid);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < kMaxNtu; ++t) tmax[t] = 0.f;
+    } else {
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        if (cc < a.cpu) {
+          const float s = wave_sum(acc[cc]);
+          const int ch = c.c0 + cc;
+          if (lane == 0 && ch < chunks_row) {
+            a.partial[(static_cast<int64_t>(c.b) * a.max_chunks + ch) * a.Hkv + c.g] = s;
+          }
+        }
+        acc[cc] = 0.f;
       }
     }
-    acc = wave_sum(acc);
-    if (lane == 0) s_red[parity][wave] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const float sum = s_red[parity][0] + s_red[parity][1] + s_red[parity][2] + s_red[parity][3];
-      const float denom = static_cast<float>(n_valid > 1 ? n_valid : 1);
-      a.out[static_cast<int64_t>(b) * a.out_stride + c] = HMAX ? sum / denom : (sum / denom) * inv_heads;
-    }
+  };
+
+  // Three-stage pipeline, unrolled by two so every buffer index is static.
+  // Per half: vector loads for batch n+1 (their block-table entries arrived
+  // a half earlier), then the block-table lookups for n+2, then the maths of
+  // batch n.  Scalar loads complete out of order, so the lookups are issued
+  // after the loads that consume the previous ones.
+  BatchCtx cx0 = ctx_of(0), cx1 = ctx_of(1);
+  int64_t pg0[KB], pg1[KB];
+  pages_of(cx0, pg0);
+  pages_of(cx1, pg1);
+  Batch<KB, STEPS> d0, d1;
+  load(cx0, pg0, d0);
+  for (int n = 0;; n += 2) {
+    if (!d0.c.valid) break;
+    load(cx1, pg1, d1);
+    cx0 = ctx_of(n + 2);
+    pages_of(cx0, pg0);
+    compute(d0);
+    if (!d1.c.valid) break;
+    load(cx0, pg0, d0);
+    cx1 = ctx_of(n + 3);
+    pages_of(cx1, pg1);
+    compute(d1);
   }
 
   if (a.write_tail) {
-    // Chunks at or beyond a row's length are 0, as in the reference output.
+    // Head max writes final scores; chunks at or beyond a row's length are 0.
     const int64_t n = static_cast<int64_t>(a.batch) * a.max_chunks;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
          i += static_cast<int64_t>(gridDim.x) * kThreads) {
       const int b = static_cast<int>(i / a.max_chunks);
       const int c = static_cast<int>(i - static_cast<int64_t>(b) * a.max_chunks);
-      if (c >= s_prefix[b + 1] - s_prefix[b]) a.out[static_cast<int64_t>(b) * a.out_stride + c] = 0.f;
+      if (c >= (s_len[b] + a.chunk - 1) / a.chunk) a.out[static_cast<int64_t>(b) * a.out_stride + c] = 0.f;
     }
   }
 }
 
+// Drop-in output: out[b, c] = sum_g partial[b, c, g] / n_valid / Hq, 0 past the row.
+__global__ __launch_bounds__(kThreads) void finalize_kernel(const float* __restrict__ partial,
+                                                            const int32_t* __restrict__ seq_lens, int batch,
+                                                            int max_chunks, int hkv, int hq, int chunk, int max_len,
+                                                            float* __restrict__ out, int64_t out_stride) {
+  const int64_t n = static_cast<int64_t>(batch) * max_chunks;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * kThreads) {
+    const int b = static_cast<int>(i / max_chunks);
+    const int c = static_cast<int>(i - static_cast<int64_t>(b) * max_chunks);
+    const int len = min(max(seq_lens[b], 0), max_len);
+    float v = 0.f;
+    if (c * chunk < len) {
+      float s = 0.f;
+      for (int g = 0; g < hkv; ++g) s += partial[i * hkv + g];
+      const int n_valid = min(chunk, len - c * chunk);
+      v = (s / static_cast<float>(n_valid)) / static_cast<float>(hq);
+    }
+    out[static_cast<int64_t>(b) * out_stride + c] = v;
+  }
+}
+
+template <int DT, int STEPS, bool HMAX>
+void launch_kb(hipStream_t stream, const ScoreArgs& a, int grid, bool uniform_page) {
+  constexpr int KB = (16 / STEPS) >= 4 ? 4 : ((16 / STEPS) >= 2 ? 2 : 1);
+  if (uniform_page) {
+    chunk_score_kernel<DT, STEPS, KB, HMAX, true><<<grid, kThreads, 0, stream>>>(a);
+  } else {
+    chunk_score_kernel<DT, STEPS, KB, HMAX, false><<<grid, kThreads, 0, stream>>>(a);
+  }
+}
+
 template <int DT, bool HMAX>
-void launch_steps(hipStream_t stream, const ScoreArgs& a, int grid) {
+void launch_steps(hipStream_t stream, const ScoreArgs& a, int grid, bool uniform_page) {
   switch (a.D / 32) {
-    case 1: chunk_score_kernel<DT, 1, HMAX><<<grid, kThreads, 0, stream>>>(a); break;
-    case 2: chunk_score_kernel<DT, 2, HMAX><<<grid, kThreads, 0, stream>>>(a); break;
-    case 3: chunk_score_kernel<DT, 3, HMAX><<<grid, kThreads, 0, stream>>>(a); break;
-    case 4: chunk_score_kernel<DT, 4, HMAX><<<grid, kThreads, 0, stream>>>(a); break;
-    case 5: chunk_score_kernel<DT, 5, HMAX><<<grid, kThreads, 0, stream>>>(a); break;
-    case 6: chunk_score_kernel<DT, 6, HMAX><<<grid, kThreads, 0, stream>>>(a); break;
-    case 7: chunk_score_kernel<DT, 7, HMAX><<<grid, kThreads, 0, stream>>>(a); break;
-    default: chunk_score_kernel<DT, 8, HMAX><<<grid, kThreads, 0, stream>>>(a); break;
+    case 1: launch_kb<DT, 1, HMAX>(stream, a, grid, uniform_page); break;
+    case 2: launch_kb<DT, 2, HMAX>(stream, a, grid, uniform_page); break;
+    case 3: launch_kb<DT, 3, HMAX>(stream, a, grid, uniform_page); break;
+    case 4: launch_kb<DT, 4, HMAX>(stream, a, grid, uniform_page); break;
+    case 5: launch_kb<DT, 5, HMAX>(stream, a, grid, uniform_page); break;
+    case 6: launch_kb<DT, 6, HMAX>(stream, a, grid, uniform_page); break;
+    case 7: launch_kb<DT, 7, HMAX>(stream, a, grid, uniform_page); break;
+    default: launch_kb<DT, 8, HMAX>(stream, a, grid, uniform_page); break;
   }
 }
 
 }  // namespace
 
-// Shared by ds_chunk_scores and the fused step.
+// Shared by ds_chunk_scores and the fused step.  With head_reduce = mean the
+// kernel writes per-KV-head partials ([batch, max_chunks, Hkv] in `partial`);
+// with max it writes final scores to `out` (and zero tails if write_tail).
 int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_t q_stride, const void* key_cache,
                         int64_t k_block_stride, int64_t k_token_stride, int64_t k_head_stride, const float* lse,
                         int64_t lse_row_stride, int64_t lse_head_stride, const int32_t* block_table,
                         int64_t bt_stride, const RowSource& src, int batch, int num_q_heads, int num_kv_heads,
                         int head_dim, int block_size, int chunk_size, int max_chunks, float scale, int head_reduce,
-                        float* out, int64_t out_stride, int write_tail) {
+                        float* partial, float* out, int64_t out_stride, int write_tail, size_t partial_bytes) {
   DS_REQUIRE(dtype == DS_BF16 || dtype == DS_FP16, "chunk scores support BF16 or FP16 query/key caches");
   DS_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0,
              "query heads must be divisible by KV heads");
@@ -235,19 +404,30 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
   DS_REQUIRE(block_size > 0, "block_size must be positive");
   DS_REQUIRE(batch >= 0 && max_chunks >= 0, "batch and max_chunks must be non-negative");
   DS_REQUIRE(head_reduce == DS_HEAD_MEAN || head_reduce == DS_HEAD_MAX, "head_reduce must be mean or max");
-  DS_SUPPORTED(head_dim > 0 && head_dim % 32 == 0 && head_dim <= 256, "head_dim must be a multiple of 32 up to 256 (got %d)",
-               head_dim);
+  DS_SUPPORTED(head_dim > 0 && head_dim % 32 == 0 && head_dim <= 256,
+               "head_dim must be a multiple of 32 up to 256 (got %d)", head_dim);
   DS_SUPPORTED(num_q_heads / num_kv_heads <= 16, "at most 16 query heads per KV head (got %d)",
                num_q_heads / num_kv_heads);
   DS_SUPPORTED(batch <= kMaxRows, "at most %d rows per launch (got %d)", kMaxRows, batch);
-  DS_SUPPORTED(head_reduce == DS_HEAD_MEAN || chunk_size <= kMaxChunkForMax,
-               "head_reduce=max supports chunks of at most %d tokens", kMaxChunkForMax);
   DS_REQUIRE(q_stride % 8 == 0 && k_block_stride % 8 == 0 && k_token_stride % 8 == 0 && k_head_stride % 8 == 0,
              "query and key strides must be multiples of 8 elements (16-byte rows)");
   DS_REQUIRE((reinterpret_cast<uintptr_t>(query) & 15u) == 0 && (reinterpret_cast<uintptr_t>(key_cache) & 15u) == 0,
              "query and key cache must be 16-byte aligned");
+  const bool hmax = head_reduce == DS_HEAD_MAX;
+  // Unit span: whole chunks, at least 64 tokens when the chunk divides 64.
+  int cpu = 1;
+  if (chunk_size % 16 == 0 && chunk_size < 64 && 64 % chunk_size == 0) cpu = 64 / chunk_size;
+  const int U = cpu * chunk_size;
+  const int ntu = (U + 15) / 16;
+  DS_SUPPORTED(!hmax || ntu <= kMaxNtu, "head_reduce=max supports chunks of at most %d tokens", kMaxNtu * 16);
   if (batch == 0 || max_chunks == 0) return clear_error();
-  DS_REQUIRE(query && key_cache && lse && block_table && out, "null tensor pointer");
+  DS_REQUIRE(query && key_cache && lse && block_table, "null tensor pointer");
+  if (!hmax) {
+    const size_t need = static_cast<size_t>(batch) * max_chunks * num_kv_heads * sizeof(float);
+    DS_REQUIRE(partial != nullptr && partial_bytes >= need,
+               "workspace too small: need %zu bytes (batch * max_chunks * kv_heads * 4)", need);
+  }
+  DS_REQUIRE(!hmax || out != nullptr, "null score output pointer");
   DS_REQUIRE(src.seq_lens != nullptr || src.counts != nullptr, "null seq_lens pointer");
 
   ScoreArgs a{};
@@ -267,23 +447,32 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
   a.batch = batch;
   a.Hq = num_q_heads;
   a.Hkv = num_kv_heads;
+  a.G = num_q_heads / num_kv_heads;
   a.D = head_dim;
   a.block_size = block_size;
   a.chunk = chunk_size;
   a.max_chunks = max_chunks;
+  a.U = U;
+  a.cpu = cpu;
+  a.ntu = ntu;
   a.scale = scale;
+  a.partial = partial;
   a.out = out;
   a.out_stride = out_stride;
-  a.write_tail = write_tail;
+  a.write_tail = hmax ? write_tail : 0;
 
-  const int64_t upper = static_cast<int64_t>(batch) * max_chunks;
-  const int64_t cap = static_cast<int64_t>(device_cu_count()) * 8;
-  const int grid = static_cast<int>(upper < cap ? upper : cap);
-  const bool hmax = head_reduce == DS_HEAD_MAX;
+  const int64_t spans = (static_cast<int64_t>(max_chunks) * chunk_size + U - 1) / U;
+  const int64_t upper_units = static_cast<int64_t>(batch) * spans * (hmax ? 1 : num_kv_heads);
+  const int64_t upper_blocks = (upper_units + kWaves - 1) / kWaves;
+  const int64_t cap = static_cast<int64_t>(device_cu_count()) * 2;
+  const int grid = static_cast<int>(std::max<int64_t>(1, std::min(upper_blocks, cap)));
+  const bool uniform_page = (block_size % 16 == 0) && (U % 16 == 0);
   if (dtype == DS_BF16) {
-    if (hmax) launch_steps<DS_BF16, true>(stream, a, grid); else launch_steps<DS_BF16, false>(stream, a, grid);
+    if (hmax) launch_steps<DS_BF16, true>(stream, a, grid, uniform_page);
+    else launch_steps<DS_BF16, false>(stream, a, grid, uniform_page);
   } else {
-    if (hmax) launch_steps<DS_FP16, true>(stream, a, grid); else launch_steps<DS_FP16, false>(stream, a, grid);
+    if (hmax) launch_steps<DS_FP16, true>(stream, a, grid, uniform_page);
+    else launch_steps<DS_FP16, false>(stream, a, grid, uniform_page);
   }
   return check_launch("ds_chunk_scores");
 }
@@ -296,12 +485,22 @@ extern "C" int ds_chunk_scores(ds_stream_t stream, int dtype, const void* query,
                                int64_t lse_head_stride, const int32_t* block_table, int64_t bt_stride,
                                const int32_t* seq_lens, int batch, int num_q_heads, int num_kv_heads, int head_dim,
                                int block_size, int chunk_size, int max_chunks, float scale, int head_reduce,
-                               float* out, int64_t out_stride) {
-  ds355::RowSource src{};
+                               float* out, int64_t out_stride, float* workspace, size_t workspace_bytes) {
+  using namespace ds355;
+  RowSource src{};
   src.seq_lens = seq_lens;
-  return ds355::launch_chunk_scores(reinterpret_cast<hipStream_t>(stream), dtype, query, q_stride, key_cache,
-                                    k_block_stride, k_token_stride, k_head_stride, lse, lse_row_stride,
-                                    lse_head_stride, block_table, bt_stride, src, batch, num_q_heads, num_kv_heads,
-                                    head_dim, block_size, chunk_size, max_chunks, scale, head_reduce, out,
-                                    out_stride, 1);
+  const bool hmax = head_reduce == DS_HEAD_MAX;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int rc = launch_chunk_scores(s, dtype, query, q_stride, key_cache, k_block_stride, k_token_stride, k_head_stride,
+                               lse, lse_row_stride, lse_head_stride, block_table, bt_stride, src, batch, num_q_heads,
+                               num_kv_heads, head_dim, block_size, chunk_size, max_chunks, scale, head_reduce,
+                               workspace, out, out_stride, 1, workspace_bytes);
+  if (rc != DS_OK || hmax || batch == 0 || max_chunks == 0) return rc;
+  DS_REQUIRE(out != nullptr, "null score output pointer");
+  const int64_t n = static_cast<int64_t>(batch) * max_chunks;
+  const int grid = static_cast<int>(std::min<int64_t>((n + kThreads - 1) / kThreads, 4096));
+  const int max_len = static_cast<int>(std::min<int64_t>(static_cast<int64_t>(max_chunks) * chunk_size, INT32_MAX));
+  finalize_kernel<<<grid, kThreads, 0, s>>>(workspace, seq_lens, batch, max_chunks, num_kv_heads, num_q_heads,
+                                            chunk_size, max_len, out, out_stride);
+  return check_launch("ds_chunk_scores finalize");
 }

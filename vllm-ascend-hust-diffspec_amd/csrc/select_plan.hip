@@ -23,8 +23,10 @@ constexpr int kLdsKeys = 12288;  // candidates kept in LDS; larger rows read key
 constexpr int kMaxSel = 2048;    // chunk ids per selection
 
 struct SelectArgs {
-  const float* scores;
+  float* scores;           // final scores [batch, score_stride]; written here when partials are given
   int64_t score_stride;
+  const float* partials;   // per-KV-head sums [batch, max_chunks, hkv] from the score pass, or nullptr
+  int max_chunks, hkv, hq;
   RowSource src;
   int batch;
   int chunk;
@@ -82,15 +84,28 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
     if (C <= K) {
       for (int i = tid; i < C; i += kThreads) s_ids[i] = i;
       n_sel = C;
-    } else {
-      const int N = C - 1;  // candidates (newest chunk excluded from the ranking)
-      int need = K - 1;
-      const float* row_scores = a.scores + static_cast<int64_t>(b) * a.score_stride;
-      const bool in_lds = N <= kLdsKeys;
-      if (in_lds) {
-        for (int i = tid; i < N; i += kThreads) s_keys[i] = order_key(row_scores[i]);
+    }
+    float* row_scores = a.scores + static_cast<int64_t>(b) * a.score_stride;
+    const int N = C - 1;  // candidates (newest chunk excluded from the ranking)
+    const bool in_lds = C > K && N <= kLdsKeys;
+    if (a.partials != nullptr) {
+      // Final scores from the per-KV-head partials (fixed head order):
+      // sum_g / n_valid / Hq, the same rounding steps as the drop-in finalize.
+      const float* part = a.partials + static_cast<int64_t>(b) * a.max_chunks * a.hkv;
+      for (int i = tid; i < C; i += kThreads) {
+        float sum = 0.f;
+        for (int g = 0; g < a.hkv; ++g) sum += part[static_cast<int64_t>(i) * a.hkv + g];
+        const int n_valid = min(a.chunk, d.len - i * a.chunk);
+        const float v = (sum / static_cast<float>(n_valid)) / static_cast<float>(a.hq);
+        row_scores[i] = v;
+        if (in_lds && i < N) s_keys[i] = order_key(v);
       }
-      __syncthreads();
+    } else if (in_lds) {
+      for (int i = tid; i < N; i += kThreads) s_keys[i] = order_key(row_scores[i]);
+    }
+    __syncthreads();
+    if (C > K) {
+      int need = K - 1;
       auto key_at = [&](int i) -> uint32_t { return in_lds ? s_keys[i] : order_key(row_scores[i]); };
 
       uint32_t prefix = 0u, pmask = 0u;
@@ -208,7 +223,8 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
 
 }  // namespace
 
-int launch_select_plan(hipStream_t stream, const float* scores, int64_t score_stride, const RowSource& src,
+int launch_select_plan(hipStream_t stream, float* scores, int64_t score_stride, const float* partials,
+                       int max_chunks, int hkv, int hq, const RowSource& src,
                        int batch, int chunk, int budget, int do_select, int do_plan, int32_t* ids,
                        int64_t ids_stride, int32_t* counts, const int32_t* slots, int num_slots,
                        const int32_t* committed_lens, int64_t* plan, int plan_width, int32_t* working_lens,
@@ -227,9 +243,14 @@ int launch_select_plan(hipStream_t stream, const float* scores, int64_t score_st
   if (do_select) DS_REQUIRE(scores && ids && counts && (src.seq_lens || src.counts), "null selection pointer");
   if (do_plan) DS_REQUIRE(ids && counts && committed_lens && plan, "null plan pointer");
 
+  if (do_select && partials != nullptr) DS_REQUIRE(hkv > 0 && hq > 0 && max_chunks > 0, "bad score partial shape");
   SelectArgs a{};
   a.scores = scores;
   a.score_stride = score_stride;
+  a.partials = partials;
+  a.max_chunks = max_chunks;
+  a.hkv = hkv;
+  a.hq = hq;
   a.src = src;
   a.batch = batch;
   a.chunk = chunk;
@@ -260,7 +281,8 @@ extern "C" int ds_select_chunks(ds_stream_t stream, const float* scores, int64_t
   ds355::RowSource src{};
   src.seq_lens = seq_lens;
   src.max_len = static_cast<int>(std::min<int64_t>(static_cast<int64_t>(score_cols) * chunk_size, INT32_MAX));
-  return ds355::launch_select_plan(reinterpret_cast<hipStream_t>(stream), scores, score_stride, src, batch,
+  return ds355::launch_select_plan(reinterpret_cast<hipStream_t>(stream), const_cast<float*>(scores), score_stride,
+                                   nullptr, 0, 0, 0, src, batch,
                                    chunk_size, history_budget, 1, 0, ids, ids_stride, counts, nullptr, batch,
                                    nullptr, nullptr, 0, nullptr, chunk_size);
 }
@@ -274,7 +296,8 @@ extern "C" int ds_build_plan(ds_stream_t stream, const int32_t* sel_ids, int64_t
   DS_REQUIRE(num_slots > 0, "num_slots must be positive");
   ds355::RowSource src{};
   src.max_len = 0;
-  return ds355::launch_select_plan(reinterpret_cast<hipStream_t>(stream), nullptr, 0, src, rows, chunk_size,
+  return ds355::launch_select_plan(reinterpret_cast<hipStream_t>(stream), nullptr, 0, nullptr, 0, 0, 0, src, rows,
+                                   chunk_size,
                                    history_budget, 0, 1, const_cast<int32_t*>(sel_ids), sel_stride,
                                    const_cast<int32_t*>(sel_count), slots, num_slots, committed_lens, plan,
                                    plan_width, working_lens, recent_window);

@@ -13,9 +13,10 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
                         int64_t lse_row_stride, int64_t lse_head_stride, const int32_t* block_table,
                         int64_t bt_stride, const RowSource& src, int batch, int num_q_heads, int num_kv_heads,
                         int head_dim, int block_size, int chunk_size, int max_chunks, float scale, int head_reduce,
-                        float* out, int64_t out_stride, int write_tail);
+                        float* partial, float* out, int64_t out_stride, int write_tail, size_t partial_bytes);
 
-int launch_select_plan(hipStream_t stream, const float* scores, int64_t score_stride, const RowSource& src,
+int launch_select_plan(hipStream_t stream, float* scores, int64_t score_stride, const float* partials,
+                       int max_chunks, int hkv, int hq, const RowSource& src,
                        int batch, int chunk, int budget, int do_select, int do_plan, int32_t* ids,
                        int64_t ids_stride, int32_t* counts, const int32_t* slots, int num_slots,
                        const int32_t* committed_lens, int64_t* plan, int plan_width, int32_t* working_lens,
@@ -55,7 +56,9 @@ extern "C" int ds_retrieval_step(ds_stream_t stream_handle, const ds_step_desc* 
   src.batch_size = d->batch_size;
   if (score || select) {
     DS_REQUIRE(d->counts && d->query_start && d->query_len && d->target_len, "null verifier row pointer");
-    DS_REQUIRE(d->max_chunks > 0 && d->scores != nullptr, "a score buffer is required");
+    DS_REQUIRE(d->max_chunks > 0 && d->scores != nullptr && d->score_partials != nullptr,
+               "score and score-partial buffers are required");
+    DS_REQUIRE(d->num_kv_heads > 0 && d->num_q_heads > 0, "head counts must be positive");
   }
   int rc;
   if (score) {
@@ -63,12 +66,13 @@ extern "C" int ds_retrieval_step(ds_stream_t stream_handle, const ds_step_desc* 
                              d->k_token_stride, d->k_head_stride, d->lse, d->lse_token_stride, d->lse_head_stride,
                              d->block_table, d->bt_stride, src, d->batch_rows, d->num_q_heads, d->num_kv_heads,
                              d->head_dim, d->block_size, d->chunk_size, d->max_chunks, d->scale, DS_HEAD_MEAN,
-                             d->scores, d->max_chunks, 0);
+                             d->score_partials, nullptr, 0, 0, SIZE_MAX);
     if (rc != DS_OK) return rc;
   }
   if (select || rebuild) {
     src.max_len = static_cast<int>(std::min<int64_t>(static_cast<int64_t>(d->max_chunks) * d->chunk_size, INT32_MAX));
-    rc = launch_select_plan(stream, d->scores, d->max_chunks, src, d->batch_rows, d->chunk_size, d->history_budget,
+    rc = launch_select_plan(stream, d->scores, d->max_chunks, d->score_partials, d->max_chunks, d->num_kv_heads,
+                            d->num_q_heads, src, d->batch_rows, d->chunk_size, d->history_budget,
                             select ? 1 : 0, rebuild ? 1 : 0, d->sel_ids, d->sel_stride, d->sel_count, d->slots,
                             d->num_slots, d->committed_lens, d->plan, d->plan_width, d->working_lens,
                             d->recent_window);

@@ -58,6 +58,7 @@ class StepDesc(ctypes.Structure):
         ("scale", _f32),
         ("max_chunks", _i32),
         ("scores", _p),
+        ("score_partials", _p),
         ("stages", _i32),
         ("sel_ids", _p), ("sel_stride", _i64), ("sel_count", _p), ("slots", _p),
         ("committed_lens", _p), ("plan", _p), ("plan_width", _i32), ("working_lens", _p),
@@ -77,7 +78,7 @@ _SIGNATURES = {
     "ds_abi_version": (_i32, []),
     "ds_chunk_scores": (_i32, [
         _p, _i32, _p, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _p,
-        _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p, _i64,
+        _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _i32, _p, _i64, _p, ctypes.c_size_t,
     ]),
     "ds_select_chunks": (_i32, [_p, _p, _i64, _i32, _p, _i32, _i32, _i32, _p, _i64, _p]),
     "ds_build_plan": (_i32, [_p, _p, _i64, _p, _i32, _p, _p, _i32, _i32, _i32, _i32, _p, _i32, _p]),

@@ -69,6 +69,9 @@ def paged_chunk_attention_scores(
     lens = seq_lens if seq_lens.dtype == torch.int32 else seq_lens.to(torch.int32)
     lens = lens.contiguous()
     mode = _lib.DS_HEAD_MAX if head_reduce == "max" else _lib.DS_HEAD_MEAN
+    workspace = None
+    if mode == _lib.DS_HEAD_MEAN:
+        workspace = torch.empty((batch_size, max_chunks, num_kv_heads), dtype=torch.float32, device=device)
     _lib.check(lib.ds_chunk_scores(
         _lib.stream_handle(device), _lib.dtype_code(query.dtype),
         query.data_ptr(), query.stride(0),
@@ -78,5 +81,6 @@ def paged_chunk_attention_scores(
         lens.data_ptr(),
         batch_size, num_query_heads, num_kv_heads, head_dim, block_size, chunk_size, max_chunks,
         float(scale), mode, out.data_ptr(), out.stride(0),
+        _lib.ptr(workspace), 0 if workspace is None else workspace.numel() * 4,
     ))
     return out

@@ -154,6 +154,7 @@ class DiffSpecDraftCache:
         self.max_chunks = (max_model_len + settings.chunk_size - 1) // settings.chunk_size
         rows = self.max_batch_rows
         self.scores = torch.zeros((rows, self.max_chunks), dtype=torch.float32, device=self.device)
+        self._score_partials: torch.Tensor | None = None  # [rows, max_chunks, target KV heads], on first use
         self.plan = torch.zeros((rows, _plan_width(settings.token_budget, settings.chunk_size)),
                                 dtype=torch.int64, device=self.device)
         self._rows_staging = _Staging(5, rows, self.device)
@@ -359,9 +360,17 @@ class DiffSpecDraftCache:
     ) -> None:
         rotary = self.rotary_embedding
         cos_sin = self._cos_sin_cache()
+        partials = None
+        if stages & (_step.SCORE | _step.SELECT):
+            kv_heads = snapshot.key_cache.shape[2]
+            if self._score_partials is None or self._score_partials.shape[2] != kv_heads:
+                self._score_partials = torch.zeros((self.max_batch_rows, self.max_chunks, kv_heads),
+                                                   dtype=torch.float32, device=self.device)
+            partials = self._score_partials[:batch_rows]
         _step.retrieval_step(
             stages=stages, snapshot=snapshot, rows=rows,
             scores=self.scores[:batch_rows] if stages & (_step.SCORE | _step.SELECT) else None,
+            score_partials=partials,
             sel_ids=self.sel_ids, sel_count=self.sel_count, slots=slots, committed_lens=committed,
             plan=self.plan[:batch_rows], working_lens=self.working_lens,
             raw_key=self.raw_key, raw_value=self.raw_value,

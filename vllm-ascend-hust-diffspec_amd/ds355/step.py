@@ -89,6 +89,7 @@ def build_step_desc(
     snapshot: VerifierSnapshot | None,
     rows: VerifierRows | None,
     scores: torch.Tensor | None,
+    score_partials: torch.Tensor | None = None,
     sel_ids: torch.Tensor,
     sel_count: torch.Tensor,
     slots: torch.Tensor,
@@ -109,13 +110,15 @@ def build_step_desc(
 ) -> tuple[_lib.StepDesc, torch.device]:
     """Validate and pack a step descriptor for ``stages`` (``SCORE | SELECT | PLAN``; ``ALL`` = one step).
 
-    SCORE needs ``snapshot``; SCORE and SELECT need ``rows`` and ``scores``, a
+    SCORE needs ``snapshot``; SCORE and SELECT need ``rows``, ``scores`` (a
     ``[batch_rows, max_chunks]`` fp32 buffer whose ``max_chunks`` covers
-    ``ceil(max target_len / chunk_size)``.  PLAN writes ``plan`` and gathers.
+    ``ceil(max target_len / chunk_size)``; SELECT writes the final scores
+    there) and ``score_partials`` (``[batch_rows, max_chunks, Hkv]`` fp32, the
+    per-KV-head sums SCORE writes and SELECT reads).  PLAN writes ``plan`` and
+    gathers.
     """
     if stages & ~ALL:
         raise ValueError(f"unknown stage bits {stages:#x}")
-    do_score = bool(stages & SCORE)
     uses_rows = bool(stages & (SCORE | SELECT))
     batch_rows = slots.numel()
     num_slots, max_model_len, heads, head_dim = raw_key.shape
@@ -157,15 +160,20 @@ def build_step_desc(
             _i32(name, getattr(rows, name), batch_rows)
         if not 0 <= rows.batch_size <= batch_rows:
             raise ValueError("batch_size must be between zero and batch_rows")
-        tensors += [scores, rows.counts, rows.query_start, rows.query_len, rows.target_len]
+        if (score_partials is None or score_partials.dtype != torch.float32 or score_partials.ndim != 3
+                or score_partials.shape[:2] != scores.shape or not score_partials.is_contiguous()):
+            raise ValueError("score_partials must be a contiguous fp32 [batch_rows, max_chunks, kv_heads] buffer")
+        tensors += [scores, score_partials, rows.counts, rows.query_start, rows.query_len, rows.target_len]
+        desc.score_partials = score_partials.data_ptr()
+        desc.num_kv_heads = score_partials.shape[2]
         desc.counts, desc.query_start = rows.counts.data_ptr(), rows.query_start.data_ptr()
         desc.query_len, desc.target_len = rows.query_len.data_ptr(), rows.target_len.data_ptr()
         desc.batch_size = rows.batch_size
         desc.max_chunks = scores.shape[1]
         desc.scores = scores.data_ptr()
-    if do_score:
+    if uses_rows:
         if snapshot is None:
-            raise ValueError("scoring needs a verifier snapshot")
+            raise ValueError("scoring and selection need the verifier snapshot (heads, scale)")
         q, lse, kc, bt = snapshot.query, snapshot.lse, snapshot.key_cache, snapshot.block_table
         if q.ndim != 3 or kc.ndim != 4 or q.shape[2] != kc.shape[3]:
             raise ValueError("query and key head dimensions must match")
@@ -179,6 +187,8 @@ def build_step_desc(
             raise ValueError("block_table must be int32 [rows, blocks] with unit last stride")
         if q.dtype != kc.dtype:
             raise ValueError("query and key cache must share a dtype")
+        if score_partials.shape[2] != kc.shape[2]:
+            raise ValueError("score_partials must have one column per KV head")
         tensors += [q, lse, kc, bt]
         desc.dtype = _lib.dtype_code(q.dtype)
         desc.query, desc.q_stride = q.data_ptr(), q.stride(0)

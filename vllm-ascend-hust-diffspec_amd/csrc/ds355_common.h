@@ -91,6 +91,25 @@ __device__ __forceinline__ int wave_sum_int(int v) {
   return v;
 }
 
+// Sum over the 64 lanes with DPP lane permutes only (no LDS instruction, so
+// it never waits on outstanding scalar or LDS loads).  The total lands in
+// lane 63.  Steps: quad xor 1, quad xor 2, half-row mirror, row mirror (each
+// 16-lane row now holds its row sum), then row broadcasts 15 and 31 fold the
+// four rows into row 3.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xf, true));
+}
+__device__ __forceinline__ float wave_sum_to_lane63(float v) {
+  v = dpp_add<0xB1, 0xf>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E, 0xf>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141, 0xf>(v);  // row_half_mirror
+  v = dpp_add<0x140, 0xf>(v);  // row_mirror
+  v = dpp_add<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v = dpp_add<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
 // Inclusive scan within the wave (lane order).
 __device__ __forceinline__ int wave_inclusive_scan(int v) {
   const int lane = threadIdx.x & 63;

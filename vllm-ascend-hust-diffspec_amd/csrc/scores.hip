@@ -55,6 +55,8 @@ struct ScoreArgs {
   int U;    // tokens per unit
   int cpu;  // chunks per unit
   int ntu;  // 16-token groups per unit
+  int hkv_log2, bs_log2;  // log2 when a power of two, else -1
+  int ci_shift;  // chunk of a unit's token t = t >> ci_shift (31 when a unit is one chunk)
   float scale;
   float* partial;  // [batch, max_chunks, Hkv] (head mean) — per-KV-head sums
   float* out;      // [batch, out_stride] final scores (head max; tail zeros)
@@ -74,6 +76,10 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(const Raw16& a, const Raw16& b, 
 }
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// x / d and x % d for x >= 0, by shifts when d is a power of two (lg >= 0).
+__device__ __forceinline__ int udiv(int x, int d, int lg) { return lg >= 0 ? (x >> lg) : x / d; }
+__device__ __forceinline__ int umod(int x, int d, int lg) { return lg >= 0 ? (x & (d - 1)) : x % d; }
 
 // Load through the constant address space: a wave-uniform address becomes a
 // scalar (SMEM) load, counted by lgkmcnt instead of the in-order vmcnt, so
@@ -140,7 +146,7 @@ __global__ __launch_bounds__(kThreads, 2) void chunk_score_kernel(ScoreArgs a) {
   int row_hint = 0;
   auto ctx_of = [&](int n) -> BatchCtx {
     BatchCtx c{};
-    const int k = n / bpu;
+    const int k = bpu == 1 ? n : n / bpu;
     const int j = n - k * bpu;
     const int unit = gw + k * tw;
     if (unit >= total) return c;
@@ -151,8 +157,8 @@ __global__ __launch_bounds__(kThreads, 2) void chunk_score_kernel(ScoreArgs a) {
     }
     row_hint = lo;
     const int r = unit - s_prefix[lo];
-    const int span = HMAX ? r : r / a.Hkv;
-    const int head_in_unit = j / bph;
+    const int span = HMAX ? r : udiv(r, a.Hkv, a.hkv_log2);
+    const int head_in_unit = bph == 1 ? j : j / bph;
     c.valid = 1;
     c.b = lo;
     c.t0 = span * a.U;
@@ -184,9 +190,9 @@ __global__ __launch_bounds__(kThreads, 2) void chunk_score_kernel(ScoreArgs a) {
         const int tg = c.tg0 + i;
         const int tok0 = c.t0 + tg * 16;
         const bool ok = c.valid && tg < a.ntu && tok0 < c.len;
-        const int64_t idx = ok ? static_cast<int64_t>(c.b) * a.bt_stride + uniform(tok0 / a.block_size) : 0;
+        const int64_t idx = ok ? static_cast<int64_t>(c.b) * a.bt_stride + uniform(udiv(tok0, a.block_size, a.bs_log2)) : 0;
         const int64_t page = scalar_load(a.bt + idx);
-        kb[i] = ok ? page * a.k_block_stride + static_cast<int64_t>(tok0 % a.block_size) * a.k_token_stride +
+        kb[i] = ok ? page * a.k_block_stride + static_cast<int64_t>(umod(tok0, a.block_size, a.bs_log2)) * a.k_token_stride +
                          static_cast<int64_t>(c.g) * a.k_head_stride
                    : 0;
       }
@@ -238,6 +244,9 @@ __global__ __launch_bounds__(kThreads, 2) void chunk_score_kernel(ScoreArgs a) {
     for (int i = 0; i < KB; ++i) {
       const int tg = c.tg0 + i;
       if (tg >= a.ntu) continue;  // wave-uniform
+      // Everything between the MFMA chain and the first read of its result
+      // stays branch-free: the chunk index is one shift, computed up front.
+      const int ci = (tg * 16) >> a.ci_shift;
       f32x4_t logit = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < STEPS; ++s) logit = mfma16x16x32<DT>(bt.q[s], bt.k[i][s], logit);
@@ -261,11 +270,8 @@ __global__ __launch_bounds__(kThreads, 2) void chunk_score_kernel(ScoreArgs a) {
         for (int e = 0; e < 4; ++e) {
           if (4 * kgrp + e < a.G && tok_ok) s += __expf(logit[e] * a.scale - bt.lse[e]);
         }
-        const int ci = (tg * 16) / a.chunk;  // chunk of the unit (uniform; 0 when the unit is one chunk)
 #pragma unroll
-        for (int cc = 0; cc < 4; ++cc) {
-          if (cc == ci) acc[cc] += s;
-        }
+        for (int cc = 0; cc < 4; ++cc) acc[cc] += cc == ci ? s : 0.f;
       }
     }
     if (!c.last) return;
@@ -293,9 +299,9 @@ __global__ __launch_bounds__(kThreads, 2) void chunk_score_kernel(ScoreArgs a) {
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc) {
         if (cc < a.cpu) {
-          const float s = wave_sum(acc[cc]);
+          const float s = wave_sum_to_lane63(acc[cc]);
           const int ch = c.c0 + cc;
-          if (lane == 0 && ch < chunks_row) {
+          if (lane == 63 && ch < chunks_row) {
             a.partial[(static_cast<int64_t>(c.b) * a.max_chunks + ch) * a.Hkv + c.g] = s;
           }
         }
@@ -455,6 +461,16 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
   a.U = U;
   a.cpu = cpu;
   a.ntu = ntu;
+  auto log2_or_neg = [](int v) {
+    if (v <= 0 || (v & (v - 1)) != 0) return -1;
+    int l = 0;
+    while ((1 << l) < v) ++l;
+    return l;
+  };
+  a.hkv_log2 = log2_or_neg(num_kv_heads);
+  a.bs_log2 = log2_or_neg(block_size);
+  // cpu > 1 only for chunks of 16 or 32 tokens (powers of two).
+  a.ci_shift = cpu > 1 ? log2_or_neg(chunk_size) : 31;
   a.scale = scale;
   a.partial = partial;
   a.out = out;

@@ -133,8 +133,7 @@ def run(args):
 
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1"}))
-        log("bench.py measures one MI355X; a multi-GPU run is not part of this build (sharding is described in "
-            "DESIGN.md)")
+        log("bench.py measures one MI355X; runs over several GPUs are not supported")
         sys.exit(2)
     spec = WORKLOADS[args.workload]
     device = torch.device("cuda:0")

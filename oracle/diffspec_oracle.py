@@ -12,8 +12,18 @@ reference file and lines it follows (paths are relative to the reference
 repository root).
 
 How each function is pinned (checked against something other than itself) is
-listed in ``PINNING`` at the bottom of this file; the tests in
-``tests/test_oracle_*.py`` carry those checks.
+listed in ``PINNING`` at the bottom of this file; ``tests/test_oracle.py``
+carries those checks, and ``tests/golden/`` holds the fixtures they write.
+
+Parity unpinned (no fixture or known-answer test of the reference covers it):
+  * the reference's CPU rotate goes through vLLM's external
+    ``RotaryEmbedding.forward_native`` (diffspec/runtime.py:1629-1647), which
+    every reference CPU test replaces with an identity rotary; this oracle
+    rotates by the textbook neox / GPT-J formula in fp32 instead, pinned by a
+    float64 recomputation, not by vLLM's code;
+  * softmax LSE values come from torch_npu's fused attention in the reference
+    (ascend_patch.py:205-239); here LSE is an input, built by the closed form
+    ``logsumexp`` as the reference's own device test does.
 """
 
 from __future__ import annotations
@@ -541,4 +551,5 @@ PINNING = {
                                     "value KAT test_runtime.py:800-803",
     "retrieval_rows": "committed-query matrix test_runtime.py:72-142 and 532-605",
     "to_bf16_rne": "equals torch's fp32->bf16 cast on random and tie-heavy inputs",
+    "retrieval_step": "composition of the pinned functions above; checked against them row by row",
 }

@@ -41,8 +41,9 @@ WORKLOADS = {
     "specmask16-pad32": dict(rows=16, lens=("uniform", 8192, 40960), hq=32, hkv=4, d=128, chunk=64, budget=2048,
                              pad=16, qlen=5, permute=True),
     "stress64": dict(rows=64, lens=("uniform", 2048, 40960), hq=64, hkv=8, d=128, chunk=128, budget=4096,
-                     reuse_half=True),
+                     reuse_half=True, window=512),
 }
+RECENT_WINDOW = 256  # rolling recent-window tokens (stress64: 512)
 DEFAULT_WORKLOAD = "ragged16-40k"
 DRAFT_TOKENS = 4
 BLOCK_SIZE = 128
@@ -185,6 +186,7 @@ def run(args):
             committed_lens=rows_t["committed"], plan=st["plan"], working_lens=st["working_lens"],
             raw_key=inp["raw_k"], raw_value=inp["raw_v"], working_key=st["work_k"], working_value=st["work_v"],
             cos_sin_cache=cos_sin, rotary_dim=d, is_neox_style=True, chunk_size=chunk, history_budget=hb,
+            recent_window=spec.get("window", RECENT_WINDOW),
             row_active=row_active,
         )
         descs.append(desc)
@@ -236,16 +238,21 @@ def run(args):
     select_us = time_stage(step.SELECT, reps)
     plan_gather_us = time_stage(step.PLAN, reps)
 
-    # Gather alone through the drop-in entry point, on the plans the chain produced.
-    from ds355.compact_kv import rebuild_compact_kv_from_plan
+    # Gather alone through its C entry point (prebuilt arguments, so host
+    # overhead stays below the kernel time), on the plans the chain produced.
+    gather_args = []
+    for inp, st in zip(copies, states):
+        ra = None if row_active is None else row_active[:rows]
+        gather_args.append((
+            stream, _lib.DS_BF16, inp["raw_k"].data_ptr(), inp["raw_v"].data_ptr(), st["work_k"].data_ptr(),
+            st["work_v"].data_ptr(), st["plan"].data_ptr(), rows, st["plan"].shape[1], cos_sin.data_ptr(),
+            cos_sin.stride(0), cos_sin.shape[0], st["work_k"].shape[0], inp["raw_k"].shape[1], hkv, d, token_budget,
+            chunk, d, 1, hb, None if ra is None else ra.data_ptr()))
     gather_ev = []
     for i in range(reps + 3):
-        inp, st = copies[i % len(copies)], states[i % len(copies)]
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
-        rebuild_compact_kv_from_plan(inp["raw_k"], inp["raw_v"], st["work_k"], st["work_v"], st["plan"][:rows],
-                                     cos_sin, chunk_size=chunk, max_width=hb, rotary_dim=d, is_neox_style=True,
-                                     row_active=None if row_active is None else row_active[:rows])
+        _lib.check(lib.ds_rebuild_compact_kv(*gather_args[i % len(gather_args)]))
         b.record()
         gather_ev.append((a, b))
     torch.cuda.synchronize()
@@ -298,7 +305,8 @@ def run(args):
             "workload": f"{args.workload}: {rows} requests"
                         + (f" + {spec.get('pad')} padding rows" if spec.get("pad") else "")
                         + f", context {spec['lens']}, Hq {spec['hq']} / Hkv {hkv} x {d} bf16, chunk {chunk}, "
-                          f"token budget {token_budget}, history {hb}, paged K block {BLOCK_SIZE}, "
+                          f"token budget {token_budget}, history {hb}, recent window "
+                          f"{spec.get('window', RECENT_WINDOW)}, paged K block {BLOCK_SIZE}, "
                           f"{len(copies)} rotated input copies",
             "global_batch": rows,
             "seq_len": max(inp0["tlens"]),
@@ -357,7 +365,7 @@ def cpu_baseline(spec, inp, cos_sin, hb, rows_t, active, reuse):
     def one():
         O.retrieval_step(query, lse, key_cache, table, lengths, raw_k, raw_v, work_k, work_v, slots, ends, cs,
                          chunk_size=chunk, budget=hb, token_budget=token_budget, scale=inp["scale"], rotary_dim=d,
-                         is_neox_style=True, regather=regather)
+                         is_neox_style=True, regather=regather, recent_window=spec.get("window", RECENT_WINDOW))
 
     t = time.perf_counter()
     one()  # warm-up

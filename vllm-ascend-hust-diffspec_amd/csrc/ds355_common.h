@@ -110,6 +110,20 @@ __device__ __forceinline__ float wave_sum_to_lane63(float v) {
   return v;
 }
 
+// Load through the constant address space: a wave-uniform address becomes a
+// scalar (SMEM) load, counted by lgkmcnt instead of the in-order vmcnt, so
+// waiting for it never drains vector loads in flight.  Only for memory the
+// kernel does not write (a launch starts with the scalar cache invalidated,
+// so data written by an earlier kernel on the stream is seen).
+__device__ __forceinline__ int32_t scalar_load(const int32_t* p) {
+  typedef const __attribute__((address_space(4))) int32_t* const_ptr;
+  return *(const_ptr)(p);
+}
+__device__ __forceinline__ int64_t scalar_load(const int64_t* p) {
+  typedef const __attribute__((address_space(4))) int64_t* const_ptr;
+  return *(const_ptr)(p);
+}
+
 // Inclusive scan within the wave (lane order).
 __device__ __forceinline__ int wave_inclusive_scan(int v) {
   const int lane = threadIdx.x & 63;

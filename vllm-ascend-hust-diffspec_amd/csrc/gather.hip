@@ -2,13 +2,15 @@
 // positions, and working-cache write — one ragged launch over all rows.
 //
 // Counterpart of diffspec/compact_kv.py:8-133 (kernel) and :184-242 (entry).
-// Work list: each (row, block of kTileP local positions) is a tile; tiles of
-// all rows are numbered through an exclusive prefix sum of per-row tile
-// counts that every workgroup builds in LDS from the plan's history_len
-// column, so short rows cost nothing and one launch covers a ragged batch.
-// Inside a tile, lanes_per_row lanes own one (position, head) row of D
-// elements; each lane moves exactly two 16-byte K vectors and two 16-byte V
-// vectors, and for neox rotates its pair (x[i], x[i + rot/2]) in registers.
+// Work list: the positions of every row are cut into tasks of a few
+// consecutive local positions; tasks of all rows are numbered through an
+// exclusive prefix sum of per-row task counts that every workgroup builds in
+// LDS from the plan's history_len column, so short rows cost nothing and one
+// launch covers a ragged batch.  In the vector path each wave works through
+// its own task list; a lane owns one position and one slice of the head
+// dimension (two 16-byte K and two 16-byte V vectors per head), rotates its
+// neox pairs (x[i], x[i + rot/2]) or GPT-J pairs in registers, and reuses the
+// position's cos/sin for every head.
 #include "ds355_common.h"
 
 namespace ds355 {
@@ -16,7 +18,6 @@ namespace {
 
 constexpr int kTileP = 32;     // local positions per tile
 constexpr int kThreads = 256;  // 4 waves
-constexpr int kUnroll = 4;     // (position, head) rows in flight per lane
 
 struct GatherArgs {
   const void* raw_k;
@@ -49,10 +50,16 @@ __device__ __forceinline__ RowPlan load_row(const GatherArgs& a, int r) {
   return rp;
 }
 
-__device__ __forceinline__ int row_tiles(const GatherArgs& a, int r) {
+// Local positions of row r that the gather moves (0 for inactive, padding
+// or empty rows).
+__device__ __forceinline__ int row_len(const GatherArgs& a, int r) {
   if (a.row_active != nullptr && a.row_active[r] == 0) return 0;
   const RowPlan rp = load_row(a, r);
-  return rp.len > 0 ? static_cast<int>((rp.len + kTileP - 1) / kTileP) : 0;
+  return rp.len > 0 ? static_cast<int>(rp.len) : 0;
+}
+
+__device__ __forceinline__ int row_tiles(const GatherArgs& a, int r) {
+  return (row_len(a, r) + kTileP - 1) / kTileP;
 }
 
 // Absolute raw position of local position p (compact_kv.py:40-52); -1 when
@@ -82,21 +89,18 @@ __device__ __forceinline__ void rotate_pair(float x1, float x2, float c, float s
   o2 = d + e;
 }
 
-// 16-byte and 8-byte vectors carried as 32-bit words.
-struct alignas(16) W4 {
-  uint32_t w[4];
-};
-struct alignas(8) W2 {
-  uint32_t w[2];
-};
+// 16-byte and 8-byte vectors carried as 32-bit words.  Native vector types
+// (not arrays in a struct) keep arrays of them in registers.
+typedef uint32_t W4 __attribute__((ext_vector_type(4)));
+typedef uint32_t W2 __attribute__((ext_vector_type(2)));
 
 // Element e of a word vector, widened to fp32 (16-bit types pack two per word).
 template <int DT, typename W>
 __device__ __forceinline__ float elem(const W& v, int e) {
   if constexpr (sizeof(typename Elem<DT>::T) == 2) {
-    return Elem<DT>::load(static_cast<uint16_t>(v.w[e >> 1] >> ((e & 1) * 16)));
+    return Elem<DT>::load(static_cast<uint16_t>(v[e >> 1] >> ((e & 1) * 16)));
   } else {
-    return __uint_as_float(v.w[e]);
+    return __uint_as_float(v[e]);
   }
 }
 
@@ -107,161 +111,218 @@ __device__ __forceinline__ W pack(const float (&f)[N]) {
   if constexpr (sizeof(typename Elem<DT>::T) == 2) {
 #pragma unroll
     for (int j = 0; j < N / 2; ++j) {
-      out.w[j] = static_cast<uint32_t>(Elem<DT>::store(f[2 * j])) |
+      out[j] = static_cast<uint32_t>(Elem<DT>::store(f[2 * j])) |
                  (static_cast<uint32_t>(Elem<DT>::store(f[2 * j + 1])) << 16);
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < N; ++j) out.w[j] = __float_as_uint(f[j]);
+    for (int j = 0; j < N; ++j) out[j] = __float_as_uint(f[j]);
   }
   return out;
 }
 
-// Vectorised path: every lane moves 2 K + 2 V 16-byte vectors per row.
-//   neox : lanes [0, half/V) rotate the pair (jV, half + jV); the other lanes
-//          copy K vectors rot + (2(j - half/V) + {0,1}) V.
-//   gptj : lane j handles vectors jV and D/2 + jV, each rotated in place
+// Raw buffer access (CDNA buffer instructions): a 128-bit resource in SGPRs
+// holds a wave-uniform base and a byte size; lanes pass 32-bit byte offsets
+// and the scalar offset steps between heads.  An offset at or past the size
+// reads zeros and drops stores in hardware, which masks idle lanes without
+// branches.  0x00020000 is the raw (untyped) resource word of the gfx9 family.
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr uint32_t kOutOfRange = 0x80000000u;  // beyond every resource size used here (< 2 GiB)
+
+__device__ __forceinline__ Rsrc make_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ W4 buf_load16(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voff), static_cast<int>(soff), 0);
+}
+__device__ __forceinline__ W2 buf_load8(Rsrc r, uint32_t voff) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(voff), 0, 0);
+}
+// Working-cache rows are written once per rebuild and not read again by
+// this launch: non-temporal stores (cache policy bit 1, nt) keep them from
+// displacing cached lines, measured about 15% faster than cached stores when
+// the gathered rows are not already in the MALL.
+constexpr int kStoreNT = 2;
+__device__ __forceinline__ void buf_store16(W4 v, Rsrc r, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, static_cast<int>(voff), static_cast<int>(soff), kStoreNT);
+}
+
+// Vectorised path.  Waves are independent workers (no block barrier after
+// the prologue).  A task is (row, ppw consecutive local positions) for every
+// head; ppw = 64 / lanes_per_row.  Lane l owns position p0 + l / lanes_per_row
+// and slice j = l % lanes_per_row of the head dimension, where it moves two
+// 16-byte K vectors and two 16-byte V vectors per head:
+//   neox : slices [0, half/V) rotate the pair (jV, half + jV); the other
+//          slices copy K vectors rot + (2(j - half/V) + {0,1}) V.
+//   gptj : slice j handles vectors jV and D/2 + jV, each rotated in place
 //          when below rot, copied otherwise.
-//   V    : lane j copies vectors jV and D/2 + jV.
-template <int DT, bool NEOX>
-__global__ __launch_bounds__(kThreads) void gather_vec_kernel(GatherArgs a) {
+//   V    : slice j copies vectors jV and D/2 + jV.
+// The cos/sin vectors of the lane's position are loaded once and reused for
+// every head.  Plan fields are wave-uniform and come through scalar loads;
+// only the chunk id of a prefix position is a per-lane load.  Resources span
+// one slot's raw cache ([max_model_len, H, D], below 2 GiB: checked on the
+// host) and one slot's working cache ([H, budget, D]); a lane with nothing
+// to move uses an out-of-range offset.  HG = heads in flight at once.
+template <int DT, bool NEOX, int HG>
+__global__ __launch_bounds__(kThreads) void gather_wave_kernel(GatherArgs a) {
   using E = Elem<DT>;
   using T = typename E::T;
   constexpr int V = 16 / sizeof(T);
+  constexpr int SZ = sizeof(T);
   __shared__ int s_prefix[kMaxRows + 1];
   __shared__ int s_scratch[4];
 
-  build_row_prefix(a.rows, s_prefix, s_scratch, [&](int r) { return row_tiles(a, r); });
+  const int lpr = a.lanes_per_row;
+  const int ppw = 64 / lpr;
+  build_row_prefix(a.rows, s_prefix, s_scratch, [&](int r) { return (row_len(a, r) + ppw - 1) / ppw; });
   const int total = s_prefix[a.rows];
 
   const int D = a.head_dim;
   const int H = a.heads;
   const int half = a.rot / 2;
-  const int lpr = a.lanes_per_row;
-  const int rows_per_pass = kThreads / lpr;
-  const int lane = static_cast<int>(threadIdx.x) % lpr;
-  const int row_slot = static_cast<int>(threadIdx.x) / lpr;
-  if (row_slot >= rows_per_pass) return;  // idle tail lanes when lpr does not divide 256
-  const int items = kTileP * H;
+  const int lane = static_cast<int>(threadIdx.x) & 63;
+  const int q = lane / lpr;      // position within the task
+  const int j = lane - q * lpr;  // slice of the head dimension
+  const bool lane_ok = q < ppw;  // false only for idle tail lanes when lpr does not divide 64
 
-  // Per-lane K job (fixed for the whole launch).
-  int k_off0, k_off1;      // element offsets of the two K vectors
-  bool rot0, rot1;         // gptj: rotate vector in place; neox: lane owns a pair
+  int k_off0, k_off1;  // element offsets of the two K vectors
+  bool rot0, rot1;     // gptj: rotate the vector in place; neox: the lane owns a pair
   int cs_off0 = 0, cs_off1 = 0;
   if (NEOX) {
     const int pairs = half / V;
-    if (lane < pairs) {
-      k_off0 = lane * V;
-      k_off1 = half + lane * V;
+    if (j < pairs) {
+      k_off0 = j * V;
+      k_off1 = half + j * V;
       rot0 = rot1 = true;
-      cs_off0 = lane * V;
+      cs_off0 = j * V;
     } else {
-      k_off0 = a.rot + (2 * (lane - pairs)) * V;
+      k_off0 = a.rot + (2 * (j - pairs)) * V;
       k_off1 = k_off0 + V;
       rot0 = rot1 = false;
     }
   } else {
-    k_off0 = lane * V;
-    k_off1 = D / 2 + lane * V;
+    k_off0 = j * V;
+    k_off1 = D / 2 + j * V;
     rot0 = k_off0 < a.rot;
     rot1 = k_off1 < a.rot;
     cs_off0 = k_off0 / 2;
     cs_off1 = k_off1 / 2;
   }
-  const int v_off0 = lane * V;
-  const int v_off1 = D / 2 + lane * V;
+  const int v_off0 = j * V;
+  const int v_off1 = D / 2 + j * V;
 
-  const T* __restrict__ raw_k = static_cast<const T*>(a.raw_k);
-  const T* __restrict__ raw_v = static_cast<const T*>(a.raw_v);
-  T* __restrict__ work_k = static_cast<T*>(a.work_k);
-  T* __restrict__ work_v = static_cast<T*>(a.work_v);
-  const T* __restrict__ cos_sin = static_cast<const T*>(a.cos_sin);
+  const int64_t raw_slot_bytes = static_cast<int64_t>(a.max_model_len) * H * D * SZ;
+  const int64_t work_slot_bytes = static_cast<int64_t>(H) * a.budget * D * SZ;
+  const uint32_t raw_head = static_cast<uint32_t>(D * SZ);
+  const uint32_t work_head = static_cast<uint32_t>(static_cast<int64_t>(a.budget) * D * SZ);
+  const Rsrc cs = make_rsrc(a.cos_sin, static_cast<int64_t>(a.pos_limit) * a.cs_stride * SZ);
+  const int ncol = a.plan_width - 5;  // chunk-id columns of a plan row
 
-  for (int tile = blockIdx.x; tile < total; tile += gridDim.x) {
-    const int r = find_row(s_prefix, a.rows, tile);
-    const RowPlan rp = load_row(a, r);
-    const int64_t p0 = static_cast<int64_t>(tile - s_prefix[r]) * kTileP;
+  const int gw = __builtin_amdgcn_readfirstlane(blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6));
+  const int tw = gridDim.x * (kThreads / 64);
+  int hint = 0;
+  for (int task = gw; task < total; task += tw) {
+    int lo = hint, hi = a.rows - 1;  // task numbers grow along the wave's list
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_prefix[mid] <= task) lo = mid; else hi = mid - 1;
+    }
+    hint = lo;
+    const int r = __builtin_amdgcn_readfirstlane(lo);  // uniform (LDS reads are not known to be)
+    const int p0 = __builtin_amdgcn_readfirstlane((task - s_prefix[r]) * ppw);
+    const int64_t* prow = a.plan + static_cast<int64_t>(r) * a.plan_width;
+    const int64_t slot = scalar_load(prow + 0);
+    const int64_t len = min(scalar_load(prow + 1), static_cast<int64_t>(a.pos_limit));
+    const int64_t tail_start = scalar_load(prow + 2);
+    const int64_t prefix_len = scalar_load(prow + 3);
+    const int64_t drop = scalar_load(prow + 4);
 
-    for (int base = row_slot; base < items; base += rows_per_pass * kUnroll) {
-      W4 k0[kUnroll], k1[kUnroll], v0[kUnroll], v1[kUnroll];
-      W4 c16[kUnroll], s16[kUnroll];
-      W2 c8a[kUnroll], s8a[kUnroll], c8b[kUnroll], s8b[kUnroll];
-      int64_t dst[kUnroll];
-      // Load phase: every row of the unrolled group issues its loads first.
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int item = base + u * rows_per_pass;
-        const int h = item / kTileP;
-        const int64_t p = p0 + item % kTileP;
-        const int64_t ap = (item < items && p < rp.len) ? abs_position(a, r, rp, p) : -1;
-        dst[u] = ap >= 0 ? ((rp.slot * H + h) * static_cast<int64_t>(a.budget) + p) * D : -1;
-        k0[u] = k1[u] = v0[u] = v1[u] = c16[u] = s16[u] = W4{{0u, 0u, 0u, 0u}};
-        c8a[u] = s8a[u] = c8b[u] = s8b[u] = W2{{0u, 0u}};
-        if (ap >= 0) {
-          const int64_t src = ((rp.slot * a.max_model_len + ap) * H + h) * static_cast<int64_t>(D);
-          k0[u] = *reinterpret_cast<const W4*>(raw_k + src + k_off0);
-          k1[u] = *reinterpret_cast<const W4*>(raw_k + src + k_off1);
-          v0[u] = *reinterpret_cast<const W4*>(raw_v + src + v_off0);
-          v1[u] = *reinterpret_cast<const W4*>(raw_v + src + v_off1);
-          const T* cs_row = cos_sin + p * a.cs_stride;
-          if (NEOX) {
-            if (rot0) {
-              c16[u] = *reinterpret_cast<const W4*>(cs_row + cs_off0);
-              s16[u] = *reinterpret_cast<const W4*>(cs_row + half + cs_off0);
-            }
-          } else {
-            if (rot0) {
-              c8a[u] = *reinterpret_cast<const W2*>(cs_row + cs_off0);
-              s8a[u] = *reinterpret_cast<const W2*>(cs_row + half + cs_off0);
-            }
-            if (rot1) {
-              c8b[u] = *reinterpret_cast<const W2*>(cs_row + cs_off1);
-              s8b[u] = *reinterpret_cast<const W2*>(cs_row + half + cs_off1);
-            }
-          }
-        }
+    // Absolute raw position of local position p (compact_kv.py:40-52).
+    const int64_t p = p0 + q;
+    const int64_t pp = p + drop;
+    const int64_t col = pp >= 0 ? pp / a.chunk : -1;
+    int64_t cid = 0;
+    if (ncol > 0) cid = prow[5 + min(max(col, static_cast<int64_t>(0)), static_cast<int64_t>(ncol - 1))];
+    const bool in_prefix = p < prefix_len;
+    const int64_t pos = in_prefix ? cid * a.chunk + (pp - col * a.chunk) : tail_start + p - prefix_len;
+    const bool ok = lane_ok && p < len && (!in_prefix || (col >= 0 && col < ncol)) && pos >= 0 &&
+                    pos < a.max_model_len;
+
+    const Rsrc rk = make_rsrc(static_cast<const char*>(a.raw_k) + slot * raw_slot_bytes, raw_slot_bytes);
+    const Rsrc rv = make_rsrc(static_cast<const char*>(a.raw_v) + slot * raw_slot_bytes, raw_slot_bytes);
+    const Rsrc wk = make_rsrc(static_cast<const char*>(a.work_k) + slot * work_slot_bytes, work_slot_bytes);
+    const Rsrc wv = make_rsrc(static_cast<const char*>(a.work_v) + slot * work_slot_bytes, work_slot_bytes);
+    const uint32_t src = ok ? static_cast<uint32_t>(pos * H * D * SZ) : kOutOfRange;
+    const uint32_t dst = ok ? static_cast<uint32_t>(p * D * SZ) : kOutOfRange;
+    const uint32_t csr = ok ? static_cast<uint32_t>(p * a.cs_stride * SZ) : kOutOfRange;
+
+    W4 c16 = W4{0u, 0u, 0u, 0u}, s16 = W4{0u, 0u, 0u, 0u};
+    W2 c8a = W2{0u, 0u}, s8a = W2{0u, 0u}, c8b = W2{0u, 0u}, s8b = W2{0u, 0u};
+    if (NEOX) {
+      if (rot0) {
+        c16 = buf_load16(cs, csr + cs_off0 * SZ, 0);
+        s16 = buf_load16(cs, csr + (half + cs_off0) * SZ, 0);
       }
-      // Rotate + store phase.
+    } else {
+      if (rot0) {
+        c8a = buf_load8(cs, csr + cs_off0 * SZ);
+        s8a = buf_load8(cs, csr + (half + cs_off0) * SZ);
+      }
+      if (rot1) {
+        c8b = buf_load8(cs, csr + cs_off1 * SZ);
+        s8b = buf_load8(cs, csr + (half + cs_off1) * SZ);
+      }
+    }
+
+    for (int h0 = 0; h0 < H; h0 += HG) {
+      W4 k0[HG], k1[HG], v0[HG], v1[HG];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        if (dst[u] >= 0) {
-          W4 ok0 = k0[u], ok1 = k1[u];
-          if (NEOX) {
-            if (rot0) {
-              float f1[V], f2[V];
+      for (int u = 0; u < HG; ++u) {
+        const uint32_t hs = static_cast<uint32_t>(min(h0 + u, H - 1)) * raw_head;
+        k0[u] = buf_load16(rk, src + k_off0 * SZ, hs);
+        k1[u] = buf_load16(rk, src + k_off1 * SZ, hs);
+        v0[u] = buf_load16(rv, src + v_off0 * SZ, hs);
+        v1[u] = buf_load16(rv, src + v_off1 * SZ, hs);
+      }
 #pragma unroll
-              for (int e = 0; e < V; ++e) {
-                rotate_pair(elem<DT>(k0[u], e), elem<DT>(k1[u], e), elem<DT>(c16[u], e), elem<DT>(s16[u], e),
-                            f1[e], f2[e]);
-              }
-              ok0 = pack<DT, W4>(f1);
-              ok1 = pack<DT, W4>(f2);
+      for (int u = 0; u < HG; ++u) {
+        if (h0 + u >= H) break;  // wave-uniform
+        W4 ok0 = k0[u], ok1 = k1[u];
+        if (NEOX) {
+          if (rot0) {
+            float f1[V], f2[V];
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+              rotate_pair(elem<DT>(k0[u], e), elem<DT>(k1[u], e), elem<DT>(c16, e), elem<DT>(s16, e), f1[e], f2[e]);
             }
-          } else {
-            if (rot0) {
-              float f[V];
-#pragma unroll
-              for (int e = 0; e < V / 2; ++e) {
-                rotate_pair(elem<DT>(k0[u], 2 * e), elem<DT>(k0[u], 2 * e + 1), elem<DT>(c8a[u], e),
-                            elem<DT>(s8a[u], e), f[2 * e], f[2 * e + 1]);
-              }
-              ok0 = pack<DT, W4>(f);
-            }
-            if (rot1) {
-              float f[V];
-#pragma unroll
-              for (int e = 0; e < V / 2; ++e) {
-                rotate_pair(elem<DT>(k1[u], 2 * e), elem<DT>(k1[u], 2 * e + 1), elem<DT>(c8b[u], e),
-                            elem<DT>(s8b[u], e), f[2 * e], f[2 * e + 1]);
-              }
-              ok1 = pack<DT, W4>(f);
-            }
+            ok0 = pack<DT, W4>(f1);
+            ok1 = pack<DT, W4>(f2);
           }
-          *reinterpret_cast<W4*>(work_k + dst[u] + k_off0) = ok0;
-          *reinterpret_cast<W4*>(work_k + dst[u] + k_off1) = ok1;
-          *reinterpret_cast<W4*>(work_v + dst[u] + v_off0) = v0[u];
-          *reinterpret_cast<W4*>(work_v + dst[u] + v_off1) = v1[u];
+        } else {
+          if (rot0) {
+            float f[V];
+#pragma unroll
+            for (int e = 0; e < V / 2; ++e) {
+              rotate_pair(elem<DT>(k0[u], 2 * e), elem<DT>(k0[u], 2 * e + 1), elem<DT>(c8a, e), elem<DT>(s8a, e),
+                          f[2 * e], f[2 * e + 1]);
+            }
+            ok0 = pack<DT, W4>(f);
+          }
+          if (rot1) {
+            float f[V];
+#pragma unroll
+            for (int e = 0; e < V / 2; ++e) {
+              rotate_pair(elem<DT>(k1[u], 2 * e), elem<DT>(k1[u], 2 * e + 1), elem<DT>(c8b, e), elem<DT>(s8b, e),
+                          f[2 * e], f[2 * e + 1]);
+            }
+            ok1 = pack<DT, W4>(f);
+          }
         }
+        const uint32_t hd = static_cast<uint32_t>(h0 + u) * work_head;
+        buf_store16(ok0, wk, dst + k_off0 * SZ, hd);
+        buf_store16(ok1, wk, dst + k_off1 * SZ, hd);
+        buf_store16(v0[u], wv, dst + v_off0 * SZ, hd);
+        buf_store16(v1[u], wv, dst + v_off1 * SZ, hd);
       }
     }
   }
@@ -317,6 +378,26 @@ __global__ __launch_bounds__(kThreads) void gather_scalar_kernel(GatherArgs a, i
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// One wave per task, capped at the workgroups that fit on the device at once
+// (occupancy from the runtime, cached per kernel instance): waves loop over
+// their task lists instead of waiting for a second round of workgroups.
+template <auto Kernel>
+int launch_wave(hipStream_t stream, const GatherArgs& a, int64_t tasks) {
+  static int resident = 0;
+  if (resident == 0) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, Kernel, kThreads, 0) != hipSuccess || per_cu <= 0) {
+      per_cu = 2;
+    }
+    resident = per_cu * device_cu_count();
+  }
+  const int64_t wgs = (tasks + kThreads / 64 - 1) / (kThreads / 64);
+  const int grid = static_cast<int>(wgs < resident ? wgs : resident);
+  if (grid <= 0) return clear_error();
+  Kernel<<<grid, kThreads, 0, stream>>>(a);
+  return check_launch("ds_rebuild_compact_kv");
+}
+
 template <int DT>
 int launch_gather(hipStream_t stream, GatherArgs a, bool neox, int grid) {
   using T = typename Elem<DT>::T;
@@ -329,14 +410,30 @@ int launch_gather(hipStream_t stream, GatherArgs a, bool neox, int grid) {
     if (neox) vec = vec && ((a.rot / 2) % V == 0);
     else vec = vec && (a.rot % V == 0);
   }
+  // Buffer offsets are 32-bit: one slot's raw and working caches and the
+  // used cos/sin rows must each stay below 2 GiB.
+  const int64_t lim = int64_t{1} << 31;
+  vec = vec && D / (2 * V) <= 64 &&
+        static_cast<int64_t>(a.max_model_len) * a.heads * D * static_cast<int64_t>(sizeof(T)) < lim &&
+        static_cast<int64_t>(a.heads) * a.budget * D * static_cast<int64_t>(sizeof(T)) < lim &&
+        static_cast<int64_t>(a.pos_limit) * a.cs_stride * static_cast<int64_t>(sizeof(T)) < lim;
   if (vec) {
     a.lanes_per_row = D / (2 * V);
-    if (neox) gather_vec_kernel<DT, true><<<grid, kThreads, 0, stream>>>(a);
-    else gather_vec_kernel<DT, false><<<grid, kThreads, 0, stream>>>(a);
-  } else {
-    a.lanes_per_row = 1;
-    gather_scalar_kernel<DT><<<grid, kThreads, 0, stream>>>(a, neox ? 1 : 0);
+    const int ppw = 64 / a.lanes_per_row;
+    const int64_t tasks = static_cast<int64_t>(a.rows) * ((a.pos_limit + ppw - 1) / ppw);
+    if (a.heads >= 4) {
+      if (neox) return launch_wave<gather_wave_kernel<DT, true, 4>>(stream, a, tasks);
+      return launch_wave<gather_wave_kernel<DT, false, 4>>(stream, a, tasks);
+    }
+    if (a.heads >= 2) {
+      if (neox) return launch_wave<gather_wave_kernel<DT, true, 2>>(stream, a, tasks);
+      return launch_wave<gather_wave_kernel<DT, false, 2>>(stream, a, tasks);
+    }
+    if (neox) return launch_wave<gather_wave_kernel<DT, true, 1>>(stream, a, tasks);
+    return launch_wave<gather_wave_kernel<DT, false, 1>>(stream, a, tasks);
   }
+  a.lanes_per_row = 1;
+  gather_scalar_kernel<DT><<<grid, kThreads, 0, stream>>>(a, neox ? 1 : 0);
   return check_launch("ds_rebuild_compact_kv");
 }
 

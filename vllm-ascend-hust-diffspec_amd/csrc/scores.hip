@@ -81,14 +81,6 @@ __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirs
 __device__ __forceinline__ int udiv(int x, int d, int lg) { return lg >= 0 ? (x >> lg) : x / d; }
 __device__ __forceinline__ int umod(int x, int d, int lg) { return lg >= 0 ? (x & (d - 1)) : x % d; }
 
-// Load through the constant address space: a wave-uniform address becomes a
-// scalar (SMEM) load, counted by lgkmcnt instead of the in-order vmcnt, so
-// waiting for it never drains the key loads in flight.  Only for memory the
-// kernel does not write.
-__device__ __forceinline__ int32_t scalar_load(const int32_t* p) {
-  typedef const __attribute__((address_space(4))) int32_t* const_ptr;
-  return *(const_ptr)(p);
-}
 
 // Where a batch sits in the wave's stream.  All fields are wave-uniform.
 struct BatchCtx {

@@ -105,12 +105,13 @@ struct Batch {
   BatchCtx c;
 };
 
-// STEPS = head_dim / 32.  KB = 16-token groups per batch.  HMAX = per-token
-// head max.  UNIFORM_PAGE = every 16-token group lies inside one block
-// (block_size and the unit start are multiples of 16), so its block-table
-// entry is one scalar load.
-template <int DT, int STEPS, int KB, bool HMAX, bool UNIFORM_PAGE>
-__global__ __launch_bounds__(kThreads, 2) void chunk_score_kernel(ScoreArgs a) {
+// STEPS = head_dim / 32.  KB = 16-token groups per batch.  WGS = workgroups
+// per CU the register budget is sized for.  HMAX = per-token head max.
+// UNIFORM_PAGE = every 16-token group lies inside one block (block_size and
+// the unit start are multiples of 16), so its block-table entry is one
+// scalar load.
+template <int DT, int STEPS, int KB, int WGS, bool HMAX, bool UNIFORM_PAGE>
+__global__ __launch_bounds__(kThreads, WGS) void chunk_score_kernel(ScoreArgs a) {
   __shared__ int s_prefix[kMaxRows + 1];
   __shared__ int s_len[kMaxRows];
   __shared__ int s_qrow[kMaxRows];
@@ -361,17 +362,25 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(const float* __restr
 }
 
 template <int DT, int STEPS, bool HMAX>
-void launch_kb(hipStream_t stream, const ScoreArgs& a, int grid, bool uniform_page) {
-  constexpr int KB = (16 / STEPS) >= 4 ? 4 : ((16 / STEPS) >= 2 ? 2 : 1);
+void launch_kb(hipStream_t stream, const ScoreArgs& a, int64_t upper_blocks, bool uniform_page) {
+  // Batch shape, measured on 16 x 40k-token rows: batches of about 8 KB of
+  // keys per wave with three workgroups per CU stream faster than 16 KB
+  // batches at two (5.4 vs 5.1 TB/s at head_dim 128).  Wider heads and the
+  // head max keep two workgroups per CU: their registers do not fit three.
+  constexpr bool narrow = !HMAX && STEPS <= 4;
+  constexpr int KB = narrow ? (STEPS <= 2 ? 4 : 2) : ((16 / STEPS) >= 4 ? 4 : ((16 / STEPS) >= 2 ? 2 : 1));
+  constexpr int WGS = narrow ? 3 : 2;
+  const int64_t cap = static_cast<int64_t>(device_cu_count()) * WGS;
+  const int grid = static_cast<int>(std::max<int64_t>(1, std::min(upper_blocks, cap)));
   if (uniform_page) {
-    chunk_score_kernel<DT, STEPS, KB, HMAX, true><<<grid, kThreads, 0, stream>>>(a);
+    chunk_score_kernel<DT, STEPS, KB, WGS, HMAX, true><<<grid, kThreads, 0, stream>>>(a);
   } else {
-    chunk_score_kernel<DT, STEPS, KB, HMAX, false><<<grid, kThreads, 0, stream>>>(a);
+    chunk_score_kernel<DT, STEPS, KB, WGS, HMAX, false><<<grid, kThreads, 0, stream>>>(a);
   }
 }
 
 template <int DT, bool HMAX>
-void launch_steps(hipStream_t stream, const ScoreArgs& a, int grid, bool uniform_page) {
+void launch_steps(hipStream_t stream, const ScoreArgs& a, int64_t grid, bool uniform_page) {
   switch (a.D / 32) {
     case 1: launch_kb<DT, 1, HMAX>(stream, a, grid, uniform_page); break;
     case 2: launch_kb<DT, 2, HMAX>(stream, a, grid, uniform_page); break;
@@ -472,15 +481,13 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
   const int64_t spans = (static_cast<int64_t>(max_chunks) * chunk_size + U - 1) / U;
   const int64_t upper_units = static_cast<int64_t>(batch) * spans * (hmax ? 1 : num_kv_heads);
   const int64_t upper_blocks = (upper_units + kWaves - 1) / kWaves;
-  const int64_t cap = static_cast<int64_t>(device_cu_count()) * 2;
-  const int grid = static_cast<int>(std::max<int64_t>(1, std::min(upper_blocks, cap)));
   const bool uniform_page = (block_size % 16 == 0) && (U % 16 == 0);
   if (dtype == DS_BF16) {
-    if (hmax) launch_steps<DS_BF16, true>(stream, a, grid, uniform_page);
-    else launch_steps<DS_BF16, false>(stream, a, grid, uniform_page);
+    if (hmax) launch_steps<DS_BF16, true>(stream, a, upper_blocks, uniform_page);
+    else launch_steps<DS_BF16, false>(stream, a, upper_blocks, uniform_page);
   } else {
-    if (hmax) launch_steps<DS_FP16, true>(stream, a, grid, uniform_page);
-    else launch_steps<DS_FP16, false>(stream, a, grid, uniform_page);
+    if (hmax) launch_steps<DS_FP16, true>(stream, a, upper_blocks, uniform_page);
+    else launch_steps<DS_FP16, false>(stream, a, upper_blocks, uniform_page);
   }
   return check_launch("ds_chunk_scores");
 }

@@ -21,6 +21,7 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kLdsKeys = 12288;  // candidates kept in LDS; larger rows read keys from global memory
 constexpr int kMaxSel = 2048;    // chunk ids per selection
+constexpr int kPre = 4;          // chunks per thread whose partials are loaded at kernel start
 
 struct SelectArgs {
   float* scores;           // final scores [batch, score_stride]; written here when partials are given
@@ -52,18 +53,63 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Inclusive scan over 256 threads; result for this thread; scratch[4]; 2 barriers.
+// Workgroup barrier for LDS hand-offs only.  Unlike __syncthreads it does
+// not wait for this wave's outstanding global stores (the score row), which
+// other kernels read and this workgroup does not.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Exclusive scan over the 256 threads through LDS; `total` gets the sum.
+__device__ __forceinline__ int lds_exclusive_scan(int v, int* scratch, int& total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int inc = wave_inclusive_scan(v);
+  if (lane == 63) scratch[wave] = inc;
+  lds_barrier();
+  int base = 0;
+  total = 0;
+#pragma unroll
+  for (int w = 0; w < kThreads / 64; ++w) {
+    const int t = scratch[w];
+    if (w < wave) base += t;
+    total += t;
+  }
+  lds_barrier();
+  return base + inc - v;
+}
+
 __device__ __forceinline__ int block_inclusive_scan(int v, int* scratch) {
   int total;
-  return block_exclusive_scan(v, scratch, total) + v;
+  return lds_exclusive_scan(v, scratch, total) + v;
 }
 
 __device__ __forceinline__ int block_sum(int v, int* scratch) {
   int total;
-  block_exclusive_scan(v, scratch, total);
+  lds_exclusive_scan(v, scratch, total);
   return total;
 }
 
+// Sum of one chunk's per-KV-head partials in head order (HKV == 0: runtime
+// count); the HKV loads are unconditional and issued together.
+template <int HKV>
+__device__ __forceinline__ float head_sum(const float* pp, int hkv) {
+  float sum = 0.f;
+  if constexpr (HKV > 0) {
+    float v[HKV];
+#pragma unroll
+    for (int g = 0; g < HKV; ++g) v[g] = pp[g];
+#pragma unroll
+    for (int g = 0; g < HKV; ++g) sum += v[g];
+  } else {
+    for (int g = 0; g < hkv; ++g) sum += pp[g];
+  }
+  return sum;
+}
+
+template <int HKV>
 __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
   __shared__ uint32_t s_keys[kLdsKeys];
   __shared__ int s_hist[256];
@@ -73,9 +119,25 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
 
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
+  // Every independent load is issued here, before any is waited for: the
+  // row description, the slot, the committed length, the slot's stored
+  // selection count (slots of distinct rows are distinct, so no other
+  // workgroup writes counts[slot] in this launch) and the score partials of
+  // the row's first kPre * 256 chunks (clamped to the buffer; masked below).
   const RowDesc d = a.do_select ? row_desc(a.src, b) : RowDesc{0, 0, 0};
   const int slot = a.slots != nullptr ? a.slots[b] : b;
   const bool slot_ok = slot >= 0 && slot < a.num_slots;
+  const int committed = a.do_plan ? a.committed_lens[b] : 0;
+  const int stored_count = (a.do_plan && slot_ok) ? a.counts[slot] : 0;
+  const float* part = a.partials + static_cast<int64_t>(b) * a.max_chunks * a.hkv;
+  float pre[kPre];
+  if (a.do_select && a.partials != nullptr) {
+#pragma unroll
+    for (int u = 0; u < kPre; ++u) {
+      const int i = min(u * kThreads + tid, a.max_chunks - 1);
+      pre[u] = head_sum<HKV>(part + static_cast<int64_t>(i) * a.hkv, a.hkv);
+    }
+  }
   int n_sel = -1;  // selection made by this workgroup (in s_ids), -1 if none
 
   if (a.do_select && d.active && slot_ok) {
@@ -91,19 +153,28 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
     if (a.partials != nullptr) {
       // Final scores from the per-KV-head partials (fixed head order):
       // sum_g / n_valid / Hq, the same rounding steps as the drop-in finalize.
-      const float* part = a.partials + static_cast<int64_t>(b) * a.max_chunks * a.hkv;
-      for (int i = tid; i < C; i += kThreads) {
-        float sum = 0.f;
-        for (int g = 0; g < a.hkv; ++g) sum += part[static_cast<int64_t>(i) * a.hkv + g];
+      auto finish = [&](int i, float sum) {
         const int n_valid = min(a.chunk, d.len - i * a.chunk);
         const float v = (sum / static_cast<float>(n_valid)) / static_cast<float>(a.hq);
         row_scores[i] = v;
         if (in_lds && i < N) s_keys[i] = order_key(v);
+      };
+#pragma unroll
+      for (int u = 0; u < kPre; ++u) {
+        const int i = u * kThreads + tid;
+        if (i < C) finish(i, pre[u]);
+      }
+      for (int i = kPre * kThreads + tid; i < C; i += kThreads) {
+        finish(i, head_sum<HKV>(part + static_cast<int64_t>(i) * a.hkv, a.hkv));
       }
     } else if (in_lds) {
       for (int i = tid; i < N; i += kThreads) s_keys[i] = order_key(row_scores[i]);
     }
-    __syncthreads();
+    if (in_lds) {
+      lds_barrier();
+    } else {
+      __syncthreads();  // keys are read back from the score row in global memory
+    }
     if (C > K) {
       int need = K - 1;
       auto key_at = [&](int i) -> uint32_t { return in_lds ? s_keys[i] : order_key(row_scores[i]); };
@@ -113,12 +184,12 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
       if (need > 0) {
         for (int shift = 24; shift >= 0; shift -= 8) {
           s_hist[tid] = 0;
-          __syncthreads();
+          lds_barrier();
           for (int i = tid; i < N; i += kThreads) {
             const uint32_t k = key_at(i);
             if ((k & pmask) == prefix) atomicAdd(&s_hist[(k >> shift) & 0xffu], 1);
           }
-          __syncthreads();
+          lds_barrier();
           const int digit = 255 - tid;  // thread t scans bins in descending digit order
           const int cnt = s_hist[digit];
           const int incl = block_inclusive_scan(cnt, s_scratch);
@@ -127,12 +198,12 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
             s_above = incl - cnt;
             s_eq = cnt;
           }
-          __syncthreads();
+          lds_barrier();
           prefix |= static_cast<uint32_t>(s_digit) << shift;
           pmask |= 0xffu << shift;
           need -= s_above;
           if (shift == 0) take_all_ties = (need == s_eq);
-          __syncthreads();
+          lds_barrier();
         }
       }
       // need = ties (key == T) still to take, lowest indices first.
@@ -150,12 +221,12 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
             sel = gt || eq;
           } else {
             int eq_total;
-            const int eq_ex = block_exclusive_scan(eq ? 1 : 0, s_scratch, eq_total);
+            const int eq_ex = lds_exclusive_scan(eq ? 1 : 0, s_scratch, eq_total);
             sel = gt || (eq && carry_eq + eq_ex < need);
             carry_eq += eq_total;
           }
           int sel_total;
-          const int sel_ex = block_exclusive_scan(sel ? 1 : 0, s_scratch, sel_total);
+          const int sel_ex = lds_exclusive_scan(sel ? 1 : 0, s_scratch, sel_total);
           if (sel && carry_sel + sel_ex < kMaxSel) s_ids[carry_sel + sel_ex] = i;
           carry_sel += sel_total;
         }
@@ -163,7 +234,7 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
       if (tid == 0) s_ids[K - 1] = C - 1;
       n_sel = K;
     }
-    __syncthreads();
+    lds_barrier();
     int32_t* out = a.ids + static_cast<int64_t>(slot) * a.ids_stride;
     for (int j = tid; j < n_sel; j += kThreads) out[j] = s_ids[j];
     if (tid == 0) a.counts[slot] = n_sel;
@@ -176,13 +247,12 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
     return;
   }
   // The slot's selection: just made here, or the stored one.
-  const int stored_count = a.counts[slot];
   const int64_t cap = min(static_cast<int64_t>(a.plan_width - 5), a.ids_stride);
   const int count = n_sel >= 0 ? n_sel : static_cast<int>(min(static_cast<int64_t>(stored_count), cap));
   const int32_t* stored = a.ids + static_cast<int64_t>(slot) * a.ids_stride;
   auto chunk_id = [&](int j) -> int64_t { return n_sel >= 0 ? s_ids[j] : stored[j]; };
 
-  const int64_t end = max(0, a.committed_lens[b] - 1);
+  const int64_t end = max(0, committed - 1);
   const int64_t hb = a.budget;
   int64_t len, tail_start, prefix_len = 0, drop = 0;
   int ncols = 0;
@@ -267,7 +337,13 @@ int launch_select_plan(hipStream_t stream, float* scores, int64_t score_stride, 
   a.plan_width = plan_width;
   a.working_lens = working_lens;
   a.recent_window = recent_window;
-  select_plan_kernel<<<batch, kThreads, 0, stream>>>(a);
+  switch (do_select && partials != nullptr ? hkv : 0) {
+    case 1: select_plan_kernel<1><<<batch, kThreads, 0, stream>>>(a); break;
+    case 2: select_plan_kernel<2><<<batch, kThreads, 0, stream>>>(a); break;
+    case 4: select_plan_kernel<4><<<batch, kThreads, 0, stream>>>(a); break;
+    case 8: select_plan_kernel<8><<<batch, kThreads, 0, stream>>>(a); break;
+    default: select_plan_kernel<0><<<batch, kThreads, 0, stream>>>(a); break;
+  }
   return check_launch("select/plan");
 }
 

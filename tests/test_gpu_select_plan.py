@@ -51,8 +51,8 @@ def test_batched_selection_with_ties_and_edges(cuda):
     g = gen(21)
     chunk, budget = 16, 512  # K = 32
     rows, lengths = [], []
-    for trial in range(64):
-        kind = trial % 4
+    for trial in range(72):
+        kind = trial % 6
         length = int(torch.randint(0, 20000, (1,), generator=g))
         c = (length + chunk - 1) // chunk
         if kind == 0:
@@ -61,6 +61,10 @@ def test_batched_selection_with_ties_and_edges(cuda):
             s = torch.randint(0, 4, (c,), generator=g).float()
         elif kind == 2:  # all equal
             s = torch.full((c,), 0.5)
+        elif kind == 3:  # a narrow band with repeats: duplicates inside one small threshold bucket
+            s = 1.0 + torch.randint(0, 300, (c,), generator=g).float() * 1e-4
+        elif kind == 4:  # chunk scores of one magnitude, as softmax means are
+            s = (1.0 + 0.3 * torch.randn(c, generator=g)).abs() * 3e-5
         else:  # signed values, +-0 and infinities
             s = torch.randn(c, generator=g)
             if c > 4:

@@ -1,0 +1,185 @@
+"""Host logic of DiffSpecDraftCache on the CPU, with the launch chain replaced by a recorder.
+
+Mirrors the reference's runtime tests, which replace the score kernel by
+attribute (tests/test_runtime.py:127, :566-579): slot stability across
+reorder and cancellation (tests/test_runtime.py:755-778), the retrieval
+skip rules and counters (tests/test_runtime.py:532-612), the verifier rows
+handed to the device (committed query, rejected-suffix cut, graph padding;
+diffspec/runtime.py:1211-1276), the LSE orientations
+(diffspec/runtime.py:880-894) and the compact-prefill rebuild
+(diffspec/runtime.py:1737-1765).  No GPU is used: every launch is recorded.
+"""
+
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from ds355 import runtime, step
+
+
+class _Rotary:
+    rotary_dim = 2
+    is_neox_style = True
+
+    def __init__(self, positions=64):
+        self.cos_sin_cache = torch.zeros((positions, 2))
+
+
+def _cache(**overrides):
+    settings = dict(chunk_size=2, token_budget=8, retrieval_interval=2, max_tree_nodes=4, max_tree_depth=2,
+                    tree_threshold=0.7, adaptive_profile=False)
+    settings.update(overrides.pop("settings", {}))
+    kwargs = dict(max_num_reqs=4, max_model_len=16, num_kv_heads=1, head_dim=2, target_num_layers=2,
+                  dtype=torch.float32, device=torch.device("cpu"), rotary_embedding=_Rotary())
+    kwargs.update(overrides)
+    return runtime.DiffSpecDraftCache(runtime.DiffSpecSettings(**settings), **kwargs)
+
+
+@pytest.fixture
+def launches(monkeypatch):
+    calls = []
+
+    def record(**kw):
+        calls.append({k: (v.clone() if isinstance(v, torch.Tensor) else v) for k, v in kw.items()})
+
+    monkeypatch.setattr(step, "retrieval_step", record)
+    return calls
+
+
+def _metadata(query_ends, seq_lens, prefill):
+    return SimpleNamespace(actual_seq_lengths_q=query_ends, seq_lens_list=seq_lens,
+                           block_tables=torch.zeros((len(seq_lens), 1), dtype=torch.int32),
+                           num_prefills=1 if prefill else 0)
+
+
+def test_slots_stay_stable_across_reorder_and_cancellation():
+    cache = _cache()
+    cache.set_active_requests(["a", "b", "c"])
+    slots = dict(cache._request_slots)
+    assert sorted(slots.values()) == [0, 1, 2]
+    cache.set_active_requests(["c", "a"])  # reorder + cancel "b"
+    assert cache._request_slots == {"a": slots["a"], "c": slots["c"]}
+    assert cache._active_slots == [slots["c"], slots["a"]]
+    cache.sel_count[slots["b"]] = 5
+    cache.set_active_requests(["c", "a", "d"])  # "d" takes the lowest free slot, b's
+    assert cache._request_slots["d"] == slots["b"]
+    with pytest.raises(RuntimeError, match="exhausted"):
+        cache.set_active_requests(["a", "c", "d", "e", "f"])
+
+
+def test_freed_slot_forgets_its_selection():
+    cache = _cache()
+    cache.set_active_requests(["a", "b"])
+    cache.sel_count[:2] = 3
+    cache.working_lens[:2] = 7
+    cache.set_active_requests(["b"])
+    freed = 0 if cache._request_slots["b"] == 1 else 1
+    assert int(cache.sel_count[freed]) == -1 and int(cache.working_lens[freed]) == 0
+
+
+def test_retrieval_skips_prefill_snapshot_and_interval(launches):
+    cache = _cache()
+    q = torch.arange(20, dtype=torch.float32).view(5, 2, 2)
+    lse = torch.arange(10, dtype=torch.float32).view(5, 2, 1)
+    key_cache = torch.zeros((1, 2, 1, 2))
+    cache.begin_target_forward(["r0", "r1"])
+    cache.capture_target_attention(q, lse, key_cache, _metadata([3, 5], [6, 4], prefill=True), 0.5)
+    assert cache._target_query.shape == (2, 2, 2)  # the last query token of each prefill row
+    torch.testing.assert_close(cache._target_query, q[[2, 4]])
+    cache.accept_target_queries(torch.ones(2), is_prefill=True)
+    assert launches == []
+    cache.begin_target_forward(["r0", "r1"])
+    cache.capture_target_attention(q[[2, 4]], lse[[2, 4]], key_cache, _metadata([1, 2], [6, 4], prefill=False), 0.5)
+    cache.accept_target_queries(torch.ones(2), is_prefill=False)  # interval 2: first decode cycle skipped
+    assert launches == []
+    cache.accept_target_queries(torch.tensor([1, 1]), is_prefill=False)
+    assert len(launches) == 1
+    call = launches[0]
+    assert call["stages"] == step.SCORE | step.SELECT
+    assert call["rows"].counts.tolist() == [1, 1]
+    assert call["rows"].query_start.tolist() == [0, 1]
+    assert call["rows"].query_len.tolist() == [1, 1]
+    assert call["rows"].target_len.tolist() == [6, 4]
+    assert call["slots"].tolist() == cache._active_slots
+    assert call["snapshot"].scale == 0.5
+    status = cache.retrieval_status()
+    assert status["retrieval_skipped_prefill"] == 1
+    assert status["retrieval_skipped_interval"] == 1
+    assert status["retrieval_count"] == 1
+    cache.begin_target_forward(["r1"])  # no capture: the previous snapshot must not be reused
+    cache.accept_target_queries(torch.ones(1), is_prefill=cache.target_is_prefill)
+    assert cache.retrieval_status()["retrieval_skipped_no_snapshot"] == 1
+    assert len(launches) == 1
+
+
+def test_speculative_rows_and_graph_padding(launches):
+    """Linear verification: per-row query lengths, accepted counts and padded rows beyond the scheduler's."""
+    cache = _cache(settings=dict(retrieval_interval=1), max_model_len=32)
+    cache.begin_target_forward(["a", "b", "c"])
+    q = torch.zeros((15, 2, 2))
+    lse = torch.zeros((15, 2))
+    # Three real rows of 5 query tokens; the capture holds two extra padded rows.
+    meta = _metadata([5, 10, 15, 15, 15], [20, 30, 12, 1, 1], prefill=False)
+    meta.block_tables = torch.zeros((5, 3), dtype=torch.int32)
+    cache.capture_target_attention(q, lse, torch.zeros((4, 8, 1, 2)), meta, 1.0)
+    cache.accept_target_queries(torch.tensor([3, 0, 5, 9, 9]), is_prefill=False)
+    call = launches[-1]
+    assert call["rows"].batch_size == 3  # padding rows are dropped (runtime.py:1211-1222)
+    assert call["rows"].counts.tolist() == [3, 0, 5]
+    assert call["rows"].query_start.tolist() == [0, 5, 10]
+    assert call["rows"].query_len.tolist() == [5, 5, 5]
+    assert call["rows"].target_len.tolist() == [20, 30, 12]
+    assert call["score_partials"].shape == (3, cache.max_chunks, 1)
+    # A verifier longer than the score buffer is refused on the host.
+    meta.seq_lens_list = [40, 30, 12, 1, 1]
+    cache.capture_target_attention(q, lse, torch.zeros((4, 8, 1, 2)), meta, 1.0)
+    with pytest.raises(ValueError, match="exceeds the score buffer"):
+        cache.accept_target_queries(torch.tensor([3, 0, 5, 9, 9]), is_prefill=False)
+
+
+def test_lse_orientations_are_accepted():
+    q = torch.zeros((3, 2, 4))
+    flat = torch.arange(6.0)
+    for lse in (flat, flat.view(3, 2), flat.view(3, 2).t().contiguous(), flat.view(3, 2, 1)):
+        got = runtime.DiffSpecDraftCache._reshape_target_lse(q, lse)
+        assert got.shape == (3, 2)
+    transposed = runtime.DiffSpecDraftCache._reshape_target_lse(q, flat.view(3, 2).t().contiguous())
+    torch.testing.assert_close(transposed, flat.view(3, 2))
+    with pytest.raises(ValueError, match="does not match"):
+        runtime.DiffSpecDraftCache._reshape_target_lse(q, torch.zeros(7))
+
+
+def test_compact_prefill_launches_the_plan_stage(launches):
+    cache = _cache(settings=dict(recent_window=4))
+    cache.set_active_requests(["a", "b"])
+    out = cache.prepare_compact_prefill(None, 2, committed_seq_lens=[9, 5])
+    call = launches[-1]
+    assert call["stages"] == step.PLAN
+    assert call["slots"].tolist() == cache._active_slots
+    assert call["committed_lens"].tolist() == [9, 5]
+    assert call["recent_window"] == 4
+    assert call["history_budget"] == 4  # ((8 - 2 - 1) // 2) * 2
+    assert call["chunk_size"] == 2 and call["rotary_dim"] == 2 and call["is_neox_style"]
+    assert out.shape == (2,)
+    with pytest.raises(RuntimeError, match="omit active request rows"):
+        cache.prepare_compact_prefill(None, 3, committed_seq_lens=[9, 5, 1])
+
+
+def test_compact_prefill_reads_committed_lengths_from_device_tensor(launches):
+    cache = _cache()
+    cache.set_active_requests(["a"])
+    cache.prepare_compact_prefill(None, 1, committed_seq_lens=torch.tensor([7], dtype=torch.int32))
+    assert launches[-1]["committed_lens"].tolist() == [7]
+    assert launches[-1]["recent_window"] == 2  # default: one chunk, the reference's tail
+
+
+def test_tensor_parallel_scoring_is_refused(launches):
+    cache = _cache(settings=dict(retrieval_interval=1), target_tensor_parallel_size=2)
+    cache.begin_target_forward(["a"])
+    cache.capture_target_attention(torch.zeros((1, 2, 2)), torch.zeros((1, 2)), torch.zeros((1, 4, 1, 2)),
+                                   _metadata([1], [4], prefill=False), 1.0)
+    with pytest.raises(NotImplementedError, match="all-reduce"):
+        cache.accept_target_queries(torch.ones(1), is_prefill=False)
+    with pytest.raises(ValueError, match="positive"):
+        _cache(target_tensor_parallel_size=0)

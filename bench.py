@@ -175,6 +175,8 @@ def run(args):
             work_k=torch.zeros((rows, hkv, token_budget, d), dtype=torch.bfloat16, device=device),
         )
         st["work_v"] = torch.zeros_like(st["work_k"])
+        if args.path == "fused":
+            st["workspace"] = step.new_workspace(total_rows, max_chunks, hkv, token_budget, device)
         states.append(st)
 
     descs = []
@@ -187,7 +189,7 @@ def run(args):
             raw_key=inp["raw_k"], raw_value=inp["raw_v"], working_key=st["work_k"], working_value=st["work_v"],
             cos_sin_cache=cos_sin, rotary_dim=d, is_neox_style=True, chunk_size=chunk, history_budget=hb,
             recent_window=spec.get("window", RECENT_WINDOW),
-            row_active=row_active,
+            row_active=row_active, workspace=st.get("workspace"),
         )
         descs.append(desc)
     stream = torch.cuda.current_stream(device).cuda_stream
@@ -205,6 +207,10 @@ def run(args):
     for i in range(len(descs)):
         launch(i)
     torch.cuda.synchronize()
+    if args.path == "fused":
+        epochs = [step.workspace_epoch(st["workspace"]) for st in states]
+        if epochs != [1] * len(states):
+            raise RuntimeError(f"the single-launch step did not run for this workload (epochs {epochs})")
 
     # Untimed warmup, then exactly K timed steps bracketed by synchronisation.
     for i in range(args.warmup):
@@ -234,6 +240,7 @@ def run(args):
         return statistics.mean(a.elapsed_time(b) for a, b in ev) * 1e3  # µs
 
     reps = max(20, args.steps // 2)
+    step_us = time_stage(step.ALL, reps)
     score_us = time_stage(step.SCORE, reps)
     select_us = time_stage(step.SELECT, reps)
     plan_gather_us = time_stage(step.PLAN, reps)
@@ -279,10 +286,18 @@ def run(args):
     copy_gbps = 2 * src.numel() * 2 * 10 / (a.elapsed_time(b) * 1e-3) / 1e9
     del src, dst
 
+    fused = args.path == "fused"
     traffic = None
     traffic_file = ROOT / "profiles" / f"traffic_{args.workload}.json"
     if traffic_file.exists():
-        traffic = json.loads(traffic_file.read_text()).get("score_kernel_hbm_bytes_per_launch")
+        key = "fused_kernel_hbm_bytes_per_launch" if fused else "score_kernel_hbm_bytes_per_launch"
+        traffic = json.loads(traffic_file.read_text()).get(key)
+    if fused:
+        # The whole step is one kernel: it is the dominant (and only) one.
+        roof_kernel, roof_bytes, roof_us = "fused_step_kernel", chain_bytes, step_us
+    else:
+        roof_kernel, roof_bytes, roof_us = "chunk_score_kernel", score_bytes, score_us
+    roof_gbps = roof_bytes / (roof_us * 1e-6) / 1e9
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(spec, copies[0], cos_sin, hb, rows_t, active, reuse)
     if cpu is not None:
@@ -315,17 +330,20 @@ def run(args):
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "chunk_score_kernel",
-            "achieved": round(score_gbps, 1),
+            "kernel": roof_kernel,
+            "achieved": round(roof_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
-            "frac": round(score_gbps / HBM_PEAK_GBPS, 4),
+            "frac": round(roof_gbps / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
-            "algorithmic_bytes": score_bytes,
-            "avg_us": round(score_us, 2),
+            "algorithmic_bytes": roof_bytes,
+            "avg_us": round(roof_us, 2),
         },
-        "kernels_us": {"chunk_score": round(score_us, 2), "select": round(select_us, 2),
+        "path": "single launch (fused_step_kernel)" if fused else "three-kernel chain",
+        "kernels_us": {"step": round(step_us, 2), "chunk_score": round(score_us, 2), "select": round(select_us, 2),
                        "plan_and_gather": round(plan_gather_us, 2), "gather": round(gather_us, 2)},
+        "score_roofline": {"achieved": round(score_gbps, 1), "frac": round(score_gbps / HBM_PEAK_GBPS, 4),
+                           "algorithmic_bytes": score_bytes},
         "gather_roofline": {"achieved": round(gather_gbps, 1), "frac": round(gather_gbps / HBM_PEAK_GBPS, 4),
                             "algorithmic_bytes": gather_bytes},
         "chain": {"algorithmic_bytes": chain_bytes, "achieved_gbps": round(chain_gbps, 1),
@@ -405,6 +423,8 @@ def main():
     parser.add_argument("--copies", type=int, default=3, help="rotated input copies (defeats the 256 MB MALL)")
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--path", choices=("fused", "chain"), default="fused",
+                        help="fused: the single-launch step (default); chain: the three-kernel chain")
     args = parser.parse_args()
     run(args)
 

@@ -155,7 +155,10 @@ int ds_rebuild_compact_kv(ds_stream_t stream, int dtype,
  * `stages` is a bit mask; all three = one retrieval step.  SELECT and PLAN
  * share one kernel launch.  At most three kernels on `stream`, no host
  * synchronisation, launch shapes fixed by the descriptor's upper bounds
- * (graph-capturable).
+ * (graph-capturable).  With all three stages and a workspace, shapes the
+ * fused kernel covers (bf16/fp16 KV, head_dim 64 or 128, <= 8 KV heads,
+ * <= 256 rows, 16-token-aligned pages) run as one launch with the same
+ * results.
  */
 enum ds_stage { DS_STAGE_SCORE = 1, DS_STAGE_SELECT = 2, DS_STAGE_PLAN = 4, DS_STAGE_ALL = 7 };
 
@@ -203,9 +206,25 @@ typedef struct ds_step_desc {
   const int32_t* row_active;         /* [batch_rows] or NULL: rows to re-gather */
   /* policy */
   int chunk_size, history_budget, recent_window;
+  /* single-launch step: zero-filled once, ds_step_workspace_bytes() bytes,
+   * 64-byte aligned; NULL runs the kernel chain */
+  void* workspace;
+  size_t workspace_bytes;
 } ds_step_desc;
 
 int ds_retrieval_step(ds_stream_t stream, const ds_step_desc* desc);
+
+/*
+ * Workspace of the single-launch step for these buffer sizes (0 when one of
+ * them is not positive).  No reference counterpart: it holds the stages'
+ * hand-over state (64 header bytes; a 256-byte line per row for its plan
+ * flag; a 4-byte state per gather task, ceil(token_budget / 8) per row,
+ * rounded up to 256 bytes; tagged score partials [batch_rows, max_chunks,
+ * num_kv_heads] x 8 bytes).  A workspace serves one launch at a time; word 2
+ * of its header is a status word that stays 0 unless a wait of the fused
+ * kernel expired (then that launch's results are not valid).
+ */
+size_t ds_step_workspace_bytes(int batch_rows, int max_chunks, int num_kv_heads, int token_budget);
 
 #ifdef __cplusplus
 }

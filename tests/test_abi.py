@@ -26,7 +26,7 @@ def _step_desc_fields():
         decl = " ".join(decl.split())
         if not decl:
             continue
-        m = re.match(r"(const )?(int64_t|int32_t|int|float|void)\s*(\*?)\s*(.*)", decl)
+        m = re.match(r"(const )?(int64_t|int32_t|int|float|void|size_t)\s*(\*?)\s*(.*)", decl)
         assert m, decl
         kind = "ptr" if m.group(3) else m.group(2)
         for name in m.group(4).split(","):
@@ -54,7 +54,7 @@ def test_step_desc_matches_header_fields():
     from ds355 import _lib
 
     sizes = {"ptr": ctypes.c_void_p, "int": ctypes.c_int, "int64_t": ctypes.c_int64, "float": ctypes.c_float,
-             "int32_t": ctypes.c_int32}
+             "int32_t": ctypes.c_int32, "size_t": ctypes.c_size_t}
     header = _step_desc_fields()
     py = [(name, t) for name, t in _lib.StepDesc._fields_]
     assert [n for n, _ in header] == [n for n, _ in py]
@@ -152,3 +152,16 @@ def test_reference_validation_order_on_host():
         rebuild_compact_kv_from_plan(raw, raw, work, work, torch.zeros((1, 9), dtype=torch.int64),
                                      torch.zeros((8, 32)), chunk_size=2, max_width=2, rotary_dim=32,
                                      is_neox_style=True)
+
+
+def test_step_workspace_size():
+    """Header (64 B), a 256-byte line per row for its plan flag, 4-byte task states
+    (ceil(token_budget / 8) per row, rounded up to 256 B), 8-byte tagged partials."""
+    from ds355 import _lib
+
+    lib = _lib.load()
+    assert lib.ds_step_workspace_bytes(3, 10, 4, 2048) == 64 + 3 * 256 + 3 * 256 * 4 + 3 * 10 * 4 * 8
+    assert lib.ds_step_workspace_bytes(17, 640, 4, 100) == 64 + 17 * 256 + 1024 + 17 * 640 * 4 * 8  # 17 * 13 * 4 -> 1024
+    assert lib.ds_step_workspace_bytes(0, 10, 4, 2048) == 0
+    assert lib.ds_step_workspace_bytes(3, 0, 4, 2048) == 0
+    assert lib.ds_step_workspace_bytes(3, 10, 4, 0) == 0

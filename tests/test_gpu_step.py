@@ -51,7 +51,13 @@ def build_case(seed, *, real_rows, pad_rows, target_lens, query_len, counts, hq,
     )
 
 
-def run_gpu(case, device, *, stages=None, state=None, row_active=None):
+@pytest.fixture(params=["chain", "fused"])
+def path(request):
+    """Both implementations of a full step: the three-kernel chain and the single launch."""
+    return request.param
+
+
+def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="chain", single_launch=True):
     from ds355 import step
 
     i32 = lambda xs: torch.tensor(xs, dtype=torch.int32, device=device)  # noqa: E731
@@ -73,6 +79,11 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None):
             table=case["table"].to(device), cos_sin=case["cos_sin"].to(device),
         )
         state["work_v"] = torch.full_like(state["work_k"], float("nan"))
+    fused = path == "fused" and (stages is None or stages == step.ALL)
+    if fused and "workspace" not in state:
+        state["workspace"] = step.new_workspace(rows, state["scores"].shape[1], case["hkv"], case["token_budget"],
+                                                device)
+    epoch = step.workspace_epoch(state["workspace"]) if fused else None
     step.retrieval_step(
         stages=step.ALL if stages is None else stages,
         snapshot=step.VerifierSnapshot(state["query"], state["lse"], state["key_cache"], state["table"],
@@ -85,8 +96,12 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None):
         working_value=state["work_v"], cos_sin_cache=state["cos_sin"], rotary_dim=case["head_dim"],
         is_neox_style=True, chunk_size=case["chunk"], history_budget=case["budget"],
         row_active=None if row_active is None else i32(row_active),
+        workspace=state.get("workspace") if fused else None,
     )
     torch.cuda.synchronize()
+    if fused:  # the single launch ran (epoch + 1) or, for other shapes, the chain did
+        assert step.workspace_epoch(state["workspace"]) == epoch + (1 if single_launch else 0)
+        assert step.workspace_status(state["workspace"]) == 0
     return state
 
 
@@ -138,26 +153,26 @@ def check_step(case, state, *, previous=None, row_active=None):
     return selections
 
 
-def test_single_request_8k(cuda):
+def test_single_request_8k(cuda, path):
     """One request, 8192 tokens, chunk 64, budget 2048 (K = 4 gives 1984 history tokens)."""
     case = build_case(0, real_rows=1, pad_rows=0, target_lens=[8192], query_len=1, counts=[1], hq=32, hkv=4,
                       head_dim=128, chunk=64, token_budget=2048, block_size=128, lmax=8192, slots=[0], num_slots=1)
-    state = run_gpu(case, cuda)
+    state = run_gpu(case, cuda, path=path)
     check_step(case, state)
 
 
-def test_ragged_16_requests_40k(cuda):
+def test_ragged_16_requests_40k(cuda, path):
     """16 requests, L ~ U[4096, 40960], contiguous slots in request order."""
     g = gen(1)
     lens = [int(x) for x in torch.randint(4096, 40961, (16,), generator=g)]
     case = build_case(1, real_rows=16, pad_rows=0, target_lens=lens, query_len=1, counts=[1] * 16, hq=32, hkv=4,
                       head_dim=128, chunk=64, token_budget=2048, block_size=128, lmax=40960,
                       slots=list(range(16)), num_slots=16)
-    state = run_gpu(case, cuda)
+    state = run_gpu(case, cuda, path=path)
     check_step(case, state)
 
 
-def test_spec_decode_mask_padding_and_permuted_slots(cuda):
+def test_spec_decode_mask_padding_and_permuted_slots(cuda, path):
     """Batch 16 + 16 graph-padding rows, K = 4 draft tail with accepted 0..4, random slot permutation."""
     g = gen(4)
     lens = [int(x) for x in torch.randint(8192, 40961, (16,), generator=g)]
@@ -167,18 +182,18 @@ def test_spec_decode_mask_padding_and_permuted_slots(cuda):
     case = build_case(4, real_rows=16, pad_rows=16, target_lens=lens, query_len=5, counts=counts, hq=32, hkv=4,
                       head_dim=128, chunk=64, token_budget=2048, block_size=128, lmax=40960, slots=slots,
                       num_slots=16)
-    state = run_gpu(case, cuda)
+    state = run_gpu(case, cuda, path=path)
     check_step(case, state)
 
 
-def test_zero_count_rows_keep_previous_selection(cuda):
+def test_zero_count_rows_keep_previous_selection(cuda, path):
     """Rows that committed nothing are not scored and keep their last selection (runtime.py:1254)."""
     g = gen(6)
     lens = [int(x) for x in torch.randint(3000, 9000, (6,), generator=g)]
     case = build_case(6, real_rows=6, pad_rows=2, target_lens=lens, query_len=5, counts=[1, 2, 3, 4, 5, 1],
                       hq=16, hkv=2, head_dim=64, chunk=32, token_budget=1024, block_size=64, lmax=9000,
                       slots=[5, 3, 1, 0, 2, 4], num_slots=6)
-    state = run_gpu(case, cuda)
+    state = run_gpu(case, cuda, path=path)
     first = check_step(case, state)
     # Next cycle: rows 1 and 4 commit nothing; the others advance by their count.
     case2 = dict(case)
@@ -187,29 +202,29 @@ def test_zero_count_rows_keep_previous_selection(cuda):
                           zip(case["tlens"], case["qlens"], case2["counts"])]
     state["work_k"].fill_(float("nan"))  # fresh sentinel: only this cycle's writes are checked
     state["work_v"].fill_(float("nan"))
-    state = run_gpu(case2, cuda, state=state)
+    state = run_gpu(case2, cuda, state=state, path=path)
     check_step(case2, state, previous=first)
 
 
-def test_stress_64_rows_reuse_half(cuda):
+def test_stress_64_rows_reuse_half(cuda, path):
     """64 rows, 8 KV heads / 64 q heads, chunk 128, budget 4096; half the rows keep their working rows."""
     g = gen(5)
     lens = [int(x) for x in torch.randint(2048, 6145, (64,), generator=g)]
     case = build_case(5, real_rows=64, pad_rows=0, target_lens=lens, query_len=1, counts=[1] * 64, hq=64, hkv=8,
                       head_dim=128, chunk=128, token_budget=4096, block_size=256, lmax=6144,
                       slots=list(range(64)), num_slots=64)
-    state = run_gpu(case, cuda)
+    state = run_gpu(case, cuda, path=path)
     check_step(case, state)
     full_k, full_v = state["work_k"].clone(), state["work_v"].clone()
     # Same step again with a random half flagged for reuse: the result must not change.
     active = [int(x) for x in (torch.rand(64, generator=g) < 0.5)]
-    run_gpu(case, cuda, state=state, row_active=active)
+    run_gpu(case, cuda, state=state, row_active=active, path=path)
     assert torch.equal(torch.nan_to_num(state["work_k"]), torch.nan_to_num(full_k))
     assert torch.equal(torch.nan_to_num(state["work_v"]), torch.nan_to_num(full_v))
     # Re-gathered rows really are rewritten; reused rows are not touched.
     state["work_k"].fill_(float("nan"))
     state["work_v"].fill_(float("nan"))
-    run_gpu(case, cuda, state=state, row_active=active)
+    run_gpu(case, cuda, state=state, row_active=active, path=path)
     for b in range(64):
         n = int(state["plan"][b, 1])
         if active[b]:
@@ -218,8 +233,8 @@ def test_stress_64_rows_reuse_half(cuda):
             assert torch.isnan(state["work_k"][b]).all()
 
 
-def test_stage_split_equals_full_chain(cuda):
-    """SCORE | SELECT then PLAN (the runtime's two call sites) equals the one-call chain."""
+def test_stage_split_equals_full_chain(cuda, path):
+    """SCORE | SELECT then PLAN (the runtime's two call sites) equals the one-call step."""
     from ds355 import step
 
     g = gen(7)
@@ -227,7 +242,7 @@ def test_stage_split_equals_full_chain(cuda):
     case = build_case(7, real_rows=8, pad_rows=0, target_lens=lens, query_len=5, counts=[5, 1, 2, 3, 4, 5, 1, 2],
                       hq=32, hkv=4, head_dim=128, chunk=64, token_budget=2048, block_size=128, lmax=20000,
                       slots=[7, 6, 5, 4, 3, 2, 1, 0], num_slots=8)
-    full = run_gpu(case, cuda)
+    full = run_gpu(case, cuda, path=path)
     split = run_gpu(case, cuda, stages=step.SCORE | step.SELECT)
     assert torch.isnan(split["work_k"]).all()
     run_gpu(case, cuda, stages=step.PLAN, state=split)

@@ -124,6 +124,18 @@ __device__ __forceinline__ int64_t scalar_load(const int64_t* p) {
   return *(const_ptr)(p);
 }
 
+// Device-scope (coherent) loads and stores: relaxed atomics at agent scope,
+// which read and write past the per-XCD L2 caches.  Used for values that
+// workgroups of one launch hand to each other.
+template <typename T>
+__device__ __forceinline__ T coherent_load(const T* p) {
+  return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ void coherent_store(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Inclusive scan within the wave (lane order).
 __device__ __forceinline__ int wave_inclusive_scan(int v) {
   const int lane = threadIdx.x & 63;

@@ -1,0 +1,562 @@
+// One retrieval step (score -> select -> plan -> gather) as a single
+// persistent launch.
+//
+// The three-kernel chain pays each kernel's ramp and drain and leaves the
+// device idle while one workgroup per row selects.  Here the stages hand
+// work over through memory inside one launch:
+//   - workgroups [0, G - S) score: they stream the scored keys exactly as
+//     chunk_score_kernel does (units numbered row-major and dealt
+//     round-robin, so rows finish roughly in order), then each wave takes its
+//     gather tasks, (row, ppw local positions) numbered row-major and dealt
+//     round-robin, each once its row's plan is published;
+//   - the last S workgroups select: selector s takes rows s, s + S, ... in
+//     order, publishes each row's plan, and finally makes sure every gather
+//     task of its rows has been done.
+//
+// Hand-over is by value through device-scope (coherent) accesses, with no
+// cache write-back on either side:
+//   - a score partial is stored as (tag << 32) | fp32 bits.  `tag` is unique
+//     to the launch, so stale values of earlier launches never match.  A
+//     selector first polls one sentinel, the partial of the row's newest
+//     chunk and last KV head (written in the row's last round of units),
+//     then reads the row's partials until all carry the tag;
+//   - a selector stores the plan row with coherent stores, waits until they
+//     have completed, then stores flags[row] = tag.  Gathering waves poll the
+//     flag and read the plan row with one coherent wave-wide load;
+//   - after each gather task its wave stores state[row][task] = tag (done),
+//     or tag | kSkipped when it gave up waiting for the plan.
+// Polling is the costly part of this design: every poll is a device-scope
+// request to one memory channel, and thousands of waves polling one line
+// slow every stream that shares the channel.  So each row's flag has its own
+// line, polls sleep between tries, and a selector reads its full row only
+// after the sentinel arrived.
+//
+// Forward progress does not depend on all workgroups being resident at once
+// (the launch is an ordinary one).  Workgroups are dispatched in index order
+// on each XCD, and a workgroup waits without a deadline only on lower-indexed
+// ones: selectors on scorers (partials, task states) and on nobody else.
+// Scorers wait for plans, held by higher-indexed selectors, only up to
+// kOwnerSpins polls; a task they give up on is marked skipped and redone by
+// the row's selector.  A gather task writes fixed bytes that depend only on
+// the published plan, so doing one twice is harmless.  The waits without a
+// deadline still end after kSpinLimit polls (then a status bit is set and
+// the results are not valid), so every wave of the launch finishes.
+//
+// The tag is the workspace epoch + 1.  The last workgroup to finish (a
+// device-scope counter) stores the tag as the new epoch, so graph replays of
+// the launch get fresh tags.  Tags stay below 2^31 (bit 31 marks skipped
+// tasks).
+//
+// Workspace (zero-filled once by its owner; one launch at a time):
+//   uint32 header[16]               epoch, done counter, status
+//   uint32 flags[rows]              plan published (tag), one per 256-byte line
+//   uint32 state[rows][task_cap]    gather task done / skipped
+//   uint64 partials[rows, max_chunks, Hkv]
+#include "gather_body.h"
+#include "score_body.h"
+#include "select_body.h"
+
+namespace ds355 {
+
+int make_score_args(score::ScoreArgs& a, int64_t& upper_units, bool& uniform_page, int dtype, const void* query,
+                    int64_t q_stride, const void* key_cache, int64_t k_block_stride, int64_t k_token_stride,
+                    int64_t k_head_stride, const float* lse, int64_t lse_row_stride, int64_t lse_head_stride,
+                    const int32_t* block_table, int64_t bt_stride, const RowSource& src, int batch, int num_q_heads,
+                    int num_kv_heads, int head_dim, int block_size, int chunk_size, int max_chunks, float scale,
+                    int head_reduce, float* partial, float* out, int64_t out_stride, int write_tail,
+                    size_t partial_bytes);
+int make_select_args(select::SelectArgs& a, float* scores, int64_t score_stride, const float* partials,
+                     int max_chunks, int hkv, int hq, const RowSource& src, int batch, int chunk, int budget,
+                     int do_select, int do_plan, int32_t* ids, int64_t ids_stride, int32_t* counts,
+                     const int32_t* slots, int num_slots, const int32_t* committed_lens, int64_t* plan,
+                     int plan_width, int32_t* working_lens, int recent_window);
+int make_gather_args(gather::GatherArgs& a, bool& vec, int& scalar_grid, int dtype, const void* raw_key,
+                     const void* raw_value, void* working_key, void* working_value, const int64_t* plan, int rows,
+                     int plan_width, const void* cos_sin, int64_t cs_stride, int cs_rows, int num_slots,
+                     int max_model_len, int heads, int head_dim, int token_budget, int chunk_size, int rotary_dim,
+                     int is_neox_style, int max_width, const int32_t* row_active, bool padded_rows);
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kSelectors = 16;     // selecting workgroups (fewer when the batch has fewer rows)
+constexpr int kFusedKeys = 8192;   // candidate keys a selector keeps in LDS
+constexpr int kFusedRows = 256;    // batch rows per fused launch
+constexpr int kPoll = 4;           // chunks per thread polled together
+constexpr int kMaxHkv = 8;         // KV heads per chunk polled together
+constexpr int kGatherHeads = 4;    // heads in flight per gather task
+constexpr int kMinTaskPositions = 8;  // ppw >= 8 for the fused shapes: task_cap = ceil(token_budget / 8)
+constexpr uint32_t kSpinLimit = 1u << 21;   // polls before a wait without deadline gives up (~2 s)
+constexpr uint32_t kOwnerSpins = 1u << 12;  // polls before a scorer leaves a task to the selector (~4 ms)
+constexpr uint32_t kSkipped = 0x80000000u;
+constexpr int kSleep = 8;          // s_sleep units (64 cycles each) between polls
+
+enum { kEpoch = 0, kDone = 1, kStatus = 2, kHeaderWords = 16 };
+enum { kStatusPartials = 1u, kStatusTasks = 2u };
+// Each row's plan flag sits on its own 256-byte line, so waves polling
+// different rows do not queue on one line.
+constexpr int kLine = 256;
+constexpr int kFlagStride = kLine / sizeof(uint32_t);
+constexpr int kStatusEvery = 256;  // polls between looks at the shared status word
+
+struct FusedArgs {
+  score::ScoreArgs s;
+  select::SelectArgs p;
+  gather::GatherArgs g;
+  uint32_t* header;
+  uint32_t* flags;
+  uint32_t* state;  // [rows, task_cap]
+  int task_cap;
+  int selectors;
+};
+
+__device__ __forceinline__ void raise_status(uint32_t* header, uint32_t bit) {
+  __hip_atomic_fetch_or(header + kStatus, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// A wait without deadline gives up after kSpinLimit polls, or early once
+// another one has.
+__device__ __forceinline__ bool give_up(uint32_t spin, const uint32_t* header) {
+  return spin >= kSpinLimit ||
+         (spin % kStatusEvery == kStatusEvery - 1 &&
+          __builtin_amdgcn_readfirstlane(coherent_load(header + kStatus)) != 0u);
+}
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+__device__ __forceinline__ int64_t lane_value(int64_t v, int lane) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(u), lane);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(u >> 32), lane);
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Waits (one load per wave and poll) until *p carries the tag.
+__device__ __forceinline__ void wait_sentinel(const uint64_t* p, uint32_t tag, uint32_t* header) {
+  for (uint32_t spin = 0;; ++spin) {
+    const uint64_t v = static_cast<uint64_t>(uniform64(static_cast<int64_t>(coherent_load(p))));
+    if (static_cast<uint32_t>(v >> 32) == tag) return;
+    if (give_up(spin, header)) {
+      raise_status(header, kStatusPartials);
+      return;
+    }
+    __builtin_amdgcn_s_sleep(kSleep);
+  }
+}
+
+// Head sums of chunks base + u * kThreads + tid (u < kPoll, below C), in head
+// order, once all of their partials carry `tag`.
+__device__ __forceinline__ void poll_chunk_sums(const uint64_t* part, int base, int C, int hkv, uint32_t tag,
+                                                uint32_t* header, float (&sum)[kPoll]) {
+  uint64_t v[kPoll][kMaxHkv] = {};
+  for (uint32_t spin = 0;; ++spin) {
+    bool ready = true;
+#pragma unroll
+    for (int u = 0; u < kPoll; ++u) {
+      const int i = base + u * kThreads + static_cast<int>(threadIdx.x);
+#pragma unroll
+      for (int g = 0; g < kMaxHkv; ++g) {
+        if (g < hkv && i < C) v[u][g] = coherent_load(part + static_cast<int64_t>(i) * hkv + g);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kPoll; ++u) {
+      const int i = base + u * kThreads + static_cast<int>(threadIdx.x);
+#pragma unroll
+      for (int g = 0; g < kMaxHkv; ++g) {
+        if (g < hkv && i < C && static_cast<uint32_t>(v[u][g] >> 32) != tag) ready = false;
+      }
+    }
+    if (ready) break;
+    if (spin >= kSpinLimit || (spin % kStatusEvery == kStatusEvery - 1 && coherent_load(header + kStatus) != 0u)) {
+      raise_status(header, kStatusPartials);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(kSleep);
+  }
+#pragma unroll
+  for (int u = 0; u < kPoll; ++u) {
+    sum[u] = 0.f;
+#pragma unroll
+    for (int g = 0; g < kMaxHkv; ++g) {
+      if (g < hkv) sum[u] += __uint_as_float(static_cast<uint32_t>(v[u][g]));
+    }
+  }
+}
+
+// Selection and plan of batch row b (the select_plan_kernel steps, with the
+// partials polled from the workspace), then the row's flag.
+__device__ __forceinline__ void select_row(const FusedArgs& f, int b, uint32_t tag,
+                                           select::SelectShared<kFusedKeys>& sh) {
+  using namespace select;
+  const SelectArgs& a = f.p;
+  const int tid = threadIdx.x;
+  const RowDesc d = row_desc(a.src, b);
+  const int slot = a.slots[b];
+  const bool slot_ok = slot >= 0 && slot < a.num_slots;
+  const int committed = a.committed_lens[b];
+  const int stored_count = slot_ok ? a.counts[slot] : 0;
+  int n_sel = -1;
+  if (d.active && slot_ok) {
+    const int C = (d.len + a.chunk - 1) / a.chunk;
+    const int K = a.budget / a.chunk;
+    if (C <= K) {
+      for (int i = tid; i < C; i += kThreads) sh.ids[i] = i;
+      n_sel = C;
+    }
+    float* row_scores = a.scores + static_cast<int64_t>(b) * a.score_stride;
+    const int N = C - 1;
+    const bool in_lds = C > K && N <= kFusedKeys;
+    const uint64_t* part = f.s.tagged + static_cast<int64_t>(b) * a.max_chunks * a.hkv;
+    if (C > 0) wait_sentinel(part + static_cast<int64_t>(C) * a.hkv - 1, tag, f.header);
+    for (int base = 0; base < C; base += kPoll * kThreads) {
+      float sum[kPoll];
+      poll_chunk_sums(part, base, C, a.hkv, tag, f.header, sum);
+#pragma unroll
+      for (int u = 0; u < kPoll; ++u) {
+        const int i = base + u * kThreads + tid;
+        if (i < C) {
+          const float v = chunk_score(sum[u], a.chunk, d.len, i, a.hq);
+          row_scores[i] = v;
+          if (in_lds && i < N) sh.keys[i] = order_key(v);
+        }
+      }
+    }
+    if (in_lds) {
+      lds_barrier();
+    } else {
+      __syncthreads();  // keys are read back from the score row in global memory
+    }
+    if (C > K) {
+      select_top(sh, N, K, [&](int i) -> uint32_t { return in_lds ? sh.keys[i] : order_key(row_scores[i]); });
+      n_sel = K;
+    }
+    lds_barrier();
+    int32_t* out = a.ids + static_cast<int64_t>(slot) * a.ids_stride;
+    for (int j = tid; j < n_sel; j += kThreads) out[j] = sh.ids[j];
+    if (tid == 0) a.counts[slot] = n_sel;
+  }
+  if (slot_ok) {
+    write_plan_row<true>(a, b, slot, committed, n_sel, stored_count, sh);
+  } else {
+    int64_t* prow = a.plan + static_cast<int64_t>(b) * a.plan_width;
+    for (int j = tid; j < a.plan_width; j += kThreads) coherent_store(prow + j, int64_t{0});
+  }
+  // Every wave's device-scope stores have completed before the flag is stored.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) coherent_store(f.flags + static_cast<int64_t>(b) * kFlagStride, tag);
+}
+
+// Plan row fields of one row, wave-uniform, and (when the row fits one
+// wave-wide load) the whole row with lane l holding column l.
+struct PlanView {
+  int64_t slot, len, tail_start, prefix_len, drop, pv;
+  const int64_t* prow;
+};
+
+__device__ __forceinline__ PlanView load_plan(const gather::GatherArgs& ga, int r) {
+  PlanView v;
+  const int lane = threadIdx.x & 63;
+  v.prow = ga.plan + static_cast<int64_t>(r) * ga.plan_width;
+  v.pv = 0;
+  if (ga.plan_width <= 64) {
+    v.pv = lane < ga.plan_width ? coherent_load(v.prow + lane) : 0;
+    v.slot = lane_value(v.pv, 0);
+    v.len = lane_value(v.pv, 1);
+    v.tail_start = lane_value(v.pv, 2);
+    v.prefix_len = lane_value(v.pv, 3);
+    v.drop = lane_value(v.pv, 4);
+  } else {
+    v.slot = uniform64(coherent_load(v.prow + 0));
+    v.len = uniform64(coherent_load(v.prow + 1));
+    v.tail_start = uniform64(coherent_load(v.prow + 2));
+    v.prefix_len = uniform64(coherent_load(v.prow + 3));
+    v.drop = uniform64(coherent_load(v.prow + 4));
+  }
+  v.len = min(v.len, static_cast<int64_t>(ga.pos_limit));
+  if (v.slot < 0 || v.slot >= ga.num_slots) v.len = 0;
+  return v;
+}
+
+// Gather task t (local positions t * ppw ...) of the row in `v`.
+template <int DT, bool NEOX>
+__device__ __forceinline__ void run_task(const gather::GatherArgs& ga, const gather::GatherLane& L,
+                                         const PlanView& v, int t) {
+  const int ppw = 64 / ga.lanes_per_row;
+  const bool one_load = ga.plan_width <= 64;
+  gather::gather_task<DT, NEOX, kGatherHeads>(
+      ga, L, t * ppw, v.slot, v.len, v.tail_start, v.prefix_len, v.drop, [&](int64_t c) {
+        if (one_load) {
+          // Chunk ids sit in lanes 5.. of pv; they are below 2^31.
+          return static_cast<int64_t>(__builtin_amdgcn_ds_bpermute(static_cast<int>(5 + c) << 2,
+                                                                   static_cast<int>(static_cast<uint64_t>(v.pv))));
+        }
+        return coherent_load(v.prow + 5 + c);
+      });
+}
+
+// A scoring wave's gather tasks: task numbers gw, gw + tw, ... of the
+// row-major numbering in task_prefix (exclusive prefix of the rows' task
+// counts).  Each waits for its row's plan at most kOwnerSpins polls; a task
+// whose plan did not come in time is marked skipped for the selector.
+template <int DT, bool NEOX>
+__device__ __forceinline__ void gather_owned(const FusedArgs& f, const int* task_prefix, int gw, int tw,
+                                             uint32_t tag) {
+  const gather::GatherArgs& ga = f.g;
+  const int rows = f.p.batch;
+  const gather::GatherLane L = gather::gather_lane<DT, NEOX>(ga);
+  const int total = task_prefix[rows];
+  int cur = -1, hint = 0;
+  bool published = false;
+  PlanView v{};
+  for (int task = gw; task < total; task += tw) {
+    int lo = hint, hi = rows - 1;  // task numbers grow along the wave's list
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (task_prefix[mid] <= task) lo = mid; else hi = mid - 1;
+    }
+    hint = lo;
+    const int r = __builtin_amdgcn_readfirstlane(lo);
+    if (r != cur) {
+      cur = r;
+      published = false;
+      const uint32_t* flag = f.flags + static_cast<int64_t>(r) * kFlagStride;
+      for (uint32_t spin = 0; spin < kOwnerSpins; ++spin) {
+        if (__builtin_amdgcn_readfirstlane(coherent_load(flag)) == tag) {
+          published = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(kSleep);
+      }
+      if (published) v = load_plan(ga, r);
+    }
+    const int t = __builtin_amdgcn_readfirstlane(task - task_prefix[r]);
+    if (published) run_task<DT, NEOX>(ga, L, v, t);
+    if ((threadIdx.x & 63) == 0) {
+      coherent_store(f.state + static_cast<int64_t>(r) * f.task_cap + t, published ? tag : (tag | kSkipped));
+    }
+  }
+}
+
+// A selector's last duty: every gather task of row b is done or skipped by
+// its scoring wave (lower-indexed workgroups); skipped ones are done here.
+// Each wave checks 64 tasks at a time.
+template <int DT, bool NEOX>
+__device__ __forceinline__ void finish_row_tasks(const FusedArgs& f, const gather::GatherLane& L, int b, int tasks,
+                                                 uint32_t tag) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t* st = f.state + static_cast<int64_t>(b) * f.task_cap;
+  bool have_plan = false;
+  PlanView v{};
+  for (int t0 = static_cast<int>(threadIdx.x >> 6) * 64; t0 < tasks; t0 += kThreads) {
+    const int t = t0 + lane;
+    uint32_t s = 0;
+    for (uint32_t spin = 0;; ++spin) {
+      s = t < tasks ? coherent_load(st + t) : tag;
+      if (__ballot((s & ~kSkipped) != tag) == 0) break;
+      if (give_up(spin, f.header)) {
+        raise_status(f.header, kStatusTasks);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(kSleep);
+    }
+    uint64_t skipped = __ballot(t < tasks && s == (tag | kSkipped));
+    while (skipped != 0) {
+      const int k = __builtin_ctzll(skipped);
+      skipped &= skipped - 1;
+      if (!have_plan) {
+        v = load_plan(f.g, b);
+        have_plan = true;
+      }
+      run_task<DT, NEOX>(f.g, L, v, t0 + k);
+    }
+  }
+}
+
+struct WorkShared {
+  int unit_prefix[kFusedRows + 1];
+  int len[kFusedRows];
+  int qrow[kFusedRows];
+  int scratch[4];
+};
+
+template <int DT, int STEPS, bool NEOX>
+__global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
+  constexpr int KB = STEPS <= 2 ? 4 : 2;  // the chunk-score batch shape for head_dim <= 128
+  __shared__ union {
+    select::SelectShared<kFusedKeys> sel;
+    WorkShared w;
+  } lds;
+  __shared__ int s_task_prefix[kFusedRows + 1];
+  __shared__ int s_scratch[4];
+  __shared__ uint32_t s_tag;
+
+  const int rows = f.p.batch;
+  const gather::GatherArgs& ga = f.g;
+  if (threadIdx.x == 0) {
+    const uint32_t t = (coherent_load(f.header + kEpoch) + 1u) & ~kSkipped;
+    s_tag = t == 0u ? 1u : t;
+  }
+  // Gather tasks of row r: its history length is at most
+  // min(committed - 1, pos_limit) (plan construction bounds it by the
+  // history end), so the task list is known before any plan exists.
+  const int ppw = 64 / ga.lanes_per_row;
+  build_row_prefix(rows, s_task_prefix, s_scratch, [&](int r) {
+    const int slot = f.p.slots[r];
+    if ((ga.row_active != nullptr && ga.row_active[r] == 0) || slot < 0 || slot >= ga.num_slots) return 0;
+    return (min(max(f.p.committed_lens[r] - 1, 0), ga.pos_limit) + ppw - 1) / ppw;
+  });
+  const uint32_t tag = s_tag;
+  const int first_selector = static_cast<int>(gridDim.x) - f.selectors;
+
+  if (static_cast<int>(blockIdx.x) >= first_selector) {
+    const int s = static_cast<int>(blockIdx.x) - first_selector;
+    for (int b = s; b < rows; b += f.selectors) select_row(f, b, tag, lds.sel);
+    const gather::GatherLane L = gather::gather_lane<DT, NEOX>(ga);
+    for (int b = s; b < rows; b += f.selectors) {
+      finish_row_tasks<DT, NEOX>(f, L, b, s_task_prefix[b + 1] - s_task_prefix[b], tag);
+    }
+  } else {
+    WorkShared& w = lds.w;
+    const score::ScoreArgs& sa = f.s;
+    for (int r = threadIdx.x; r < rows; r += kThreads) {
+      const RowDesc d = row_desc(sa.src, r);
+      w.len[r] = d.active ? d.len : 0;
+      w.qrow[r] = static_cast<int>(d.qrow);
+    }
+    __syncthreads();
+    build_row_prefix(rows, w.unit_prefix, w.scratch, [&](int r) { return (w.len[r] + sa.U - 1) / sa.U * sa.Hkv; });
+    const int gw = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x) * kWaves +
+                                                  static_cast<int>(threadIdx.x >> 6));
+    const int tw = first_selector * kWaves;
+    score::score_stream<DT, STEPS, KB, false, true, true>(sa, w.unit_prefix, w.len, w.qrow, w.unit_prefix[rows], gw,
+                                                          tw, tag);
+    gather_owned<DT, NEOX>(f, s_task_prefix, gw, tw, tag);
+  }
+
+  // The last workgroup to finish publishes this launch's tag as the epoch.
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(f.header + kDone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == gridDim.x - 1) {
+      coherent_store(f.header + kDone, 0u);
+      coherent_store(f.header + kEpoch, tag);
+    }
+  }
+}
+
+size_t flags_bytes(int rows) { return static_cast<size_t>(rows) * kLine; }
+int task_cap(int token_budget) { return (token_budget + kMinTaskPositions - 1) / kMinTaskPositions; }
+size_t state_bytes(int rows, int token_budget) {
+  return (static_cast<size_t>(rows) * task_cap(token_budget) * sizeof(uint32_t) + kLine - 1) / kLine * kLine;
+}
+
+// Grid: the workgroups that fit on the device at once (occupancy from the
+// runtime), fewer when the work is smaller; the last `selectors` select.
+template <auto Kernel>
+int launch_fused(hipStream_t stream, const FusedArgs& f, int64_t upper_units, int64_t upper_tasks, bool& launched) {
+  static int per_cu = -1;
+  if (per_cu < 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, Kernel, kThreads, 0) != hipSuccess) n = 0;
+    per_cu = n;
+  }
+  const int64_t resident = static_cast<int64_t>(per_cu) * device_cu_count();
+  if (resident < f.selectors + 1) return clear_error();  // does not fit: the chain runs instead
+  const int64_t work_wgs = std::max<int64_t>(
+      1, std::max((upper_units + kWaves - 1) / kWaves, (upper_tasks + kWaves - 1) / kWaves));
+  const int grid = static_cast<int>(f.selectors + std::min(resident - f.selectors, work_wgs));
+  Kernel<<<grid, kThreads, 0, stream>>>(f);
+  const int rc = check_launch("fused retrieval step");
+  launched = rc == DS_OK;
+  return rc;
+}
+
+template <int DT>
+int launch_dt(hipStream_t stream, const FusedArgs& f, int steps, bool neox, int64_t upper_units,
+              int64_t upper_tasks, bool& launched) {
+  if (steps == 4) {
+    if (neox) return launch_fused<fused_step_kernel<DT, 4, true>>(stream, f, upper_units, upper_tasks, launched);
+    return launch_fused<fused_step_kernel<DT, 4, false>>(stream, f, upper_units, upper_tasks, launched);
+  }
+  if (neox) return launch_fused<fused_step_kernel<DT, 2, true>>(stream, f, upper_units, upper_tasks, launched);
+  return launch_fused<fused_step_kernel<DT, 2, false>>(stream, f, upper_units, upper_tasks, launched);
+}
+
+}  // namespace
+
+size_t fused_workspace_bytes(int rows, int max_chunks, int num_kv_heads, int token_budget) {
+  if (rows <= 0 || max_chunks <= 0 || num_kv_heads <= 0 || token_budget <= 0) return 0;
+  return kHeaderWords * sizeof(uint32_t) + flags_bytes(rows) + state_bytes(rows, token_budget) +
+         static_cast<size_t>(rows) * max_chunks * num_kv_heads * sizeof(uint64_t);
+}
+
+// Runs the whole step as one launch when the descriptor fits the fused
+// kernel; `launched` stays false (and nothing is launched) otherwise.
+int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource& src, bool& launched) {
+  launched = false;
+  if (d->workspace == nullptr || d->stages != DS_STAGE_ALL) return clear_error();
+  const size_t need = fused_workspace_bytes(d->batch_rows, d->max_chunks, d->num_kv_heads, d->token_budget);
+  DS_REQUIRE(need > 0 && d->workspace_bytes >= need,
+             "step workspace too small: need %zu bytes for %d rows, %d chunks, %d KV heads, token budget %d", need,
+             d->batch_rows, d->max_chunks, d->num_kv_heads, d->token_budget);
+  DS_REQUIRE((reinterpret_cast<uintptr_t>(d->workspace) & 63u) == 0, "step workspace must be 64-byte aligned");
+
+  FusedArgs f{};
+  int64_t upper_units = 0;
+  bool uniform_page = false;
+  int rc = make_score_args(f.s, upper_units, uniform_page, d->dtype, d->query, d->q_stride, d->key_cache,
+                           d->k_block_stride, d->k_token_stride, d->k_head_stride, d->lse, d->lse_token_stride,
+                           d->lse_head_stride, d->block_table, d->bt_stride, src, d->batch_rows, d->num_q_heads,
+                           d->num_kv_heads, d->head_dim, d->block_size, d->chunk_size, d->max_chunks, d->scale,
+                           DS_HEAD_MEAN, d->score_partials, nullptr, 0, 0, SIZE_MAX);
+  if (rc != DS_OK) return rc;
+  rc = make_select_args(f.p, d->scores, d->max_chunks, d->score_partials, d->max_chunks, d->num_kv_heads,
+                        d->num_q_heads, src, d->batch_rows, d->chunk_size, d->history_budget, 1, 1, d->sel_ids,
+                        d->sel_stride, d->sel_count, d->slots, d->num_slots, d->committed_lens, d->plan,
+                        d->plan_width, d->working_lens, d->recent_window);
+  if (rc != DS_OK) return rc;
+  bool vec = false;
+  int scalar_grid = 0;
+  rc = make_gather_args(f.g, vec, scalar_grid, d->kv_dtype, d->raw_key, d->raw_value, d->working_key,
+                        d->working_value, d->plan, d->batch_rows, d->plan_width, d->cos_sin, d->cs_stride,
+                        d->cs_rows, d->num_slots, d->max_model_len, d->draft_heads, d->draft_head_dim,
+                        d->token_budget, d->chunk_size, d->rotary_dim, d->is_neox_style, d->history_budget,
+                        d->row_active, true);
+  if (rc != DS_OK) return rc;
+
+  // Shapes the fused kernel is built for; everything else runs the chain.
+  const int steps = d->head_dim / 32;
+  const bool fits = d->dtype == d->kv_dtype && (d->dtype == DS_BF16 || d->dtype == DS_FP16) &&
+                    (d->head_dim == 64 || d->head_dim == 128) && d->num_kv_heads <= kMaxHkv &&
+                    d->batch_rows >= 1 && d->batch_rows <= kFusedRows && uniform_page && vec &&
+                    scalar_grid > 0 && d->slots != nullptr && d->history_budget / d->chunk_size <= select::kMaxSel &&
+                    64 / f.g.lanes_per_row >= kMinTaskPositions;
+  if (!fits) return clear_error();
+
+  char* ws = static_cast<char*>(d->workspace);
+  f.header = reinterpret_cast<uint32_t*>(ws);
+  ws += kHeaderWords * sizeof(uint32_t);
+  f.flags = reinterpret_cast<uint32_t*>(ws);
+  ws += flags_bytes(d->batch_rows);
+  f.state = reinterpret_cast<uint32_t*>(ws);
+  f.task_cap = task_cap(d->token_budget);
+  ws += state_bytes(d->batch_rows, d->token_budget);
+  f.s.tagged = reinterpret_cast<uint64_t*>(ws);
+  f.selectors = std::min(d->batch_rows, kSelectors);
+  const int ppw = 64 / f.g.lanes_per_row;
+  const int64_t upper_tasks = static_cast<int64_t>(d->batch_rows) * ((f.g.pos_limit + ppw - 1) / ppw);
+  const bool neox = d->is_neox_style != 0;
+  if (d->dtype == DS_BF16) return launch_dt<DS_BF16>(stream, f, steps, neox, upper_units, upper_tasks, launched);
+  return launch_dt<DS_FP16>(stream, f, steps, neox, upper_units, upper_tasks, launched);
+}
+
+}  // namespace ds355
+
+extern "C" size_t ds_step_workspace_bytes(int batch_rows, int max_chunks, int num_kv_heads, int token_budget) {
+  return ds355::fused_workspace_bytes(batch_rows, max_chunks, num_kv_heads, token_budget);
+}

@@ -24,86 +24,12 @@
 // in the selection kernel for a retrieval step, or in finalize_kernel for
 // the drop-in entry point.  The per-token head max (head_reduce = max) keeps
 // all KV heads of a span in one wave and writes final scores directly.
-#include "rowdesc.h"
+#include "score_body.h"
 
 namespace ds355 {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = 4;
-constexpr int kMaxNtu = 8;  // 16-token groups per unit with head_reduce = max (U <= 128)
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-
-struct alignas(16) Raw16 {
-  uint32_t w[4];
-};
-
-struct ScoreArgs {
-  const uint16_t* q;
-  int64_t q_stride;
-  const uint16_t* k;
-  int64_t k_block_stride, k_token_stride, k_head_stride;
-  const float* lse;
-  int64_t lse_row_stride, lse_head_stride;
-  const int32_t* bt;
-  int64_t bt_stride;
-  RowSource src;
-  int batch, Hq, Hkv, G, D, block_size, chunk, max_chunks;
-  int U;    // tokens per unit
-  int cpu;  // chunks per unit
-  int ntu;  // 16-token groups per unit
-  int hkv_log2, bs_log2;  // log2 when a power of two, else -1
-  int ci_shift;  // chunk of a unit's token t = t >> ci_shift (31 when a unit is one chunk)
-  float scale;
-  float* partial;  // [batch, max_chunks, Hkv] (head mean) — per-KV-head sums
-  float* out;      // [batch, out_stride] final scores (head max; tail zeros)
-  int64_t out_stride;
-  int write_tail;
-};
-
-template <int DT>
-__device__ __forceinline__ f32x4_t mfma16x16x32(const Raw16& a, const Raw16& b, f32x4_t c) {
-  if constexpr (DT == DS_BF16) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
-                                                   c, 0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
-                                                  0, 0, 0);
-  }
-}
-
-__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
-
-// x / d and x % d for x >= 0, by shifts when d is a power of two (lg >= 0).
-__device__ __forceinline__ int udiv(int x, int d, int lg) { return lg >= 0 ? (x >> lg) : x / d; }
-__device__ __forceinline__ int umod(int x, int d, int lg) { return lg >= 0 ? (x & (d - 1)) : x % d; }
-
-
-// Where a batch sits in the wave's stream.  All fields are wave-uniform.
-struct BatchCtx {
-  int valid;
-  int b;
-  int t0;    // first token of the unit
-  int len;   // row's scored length
-  int qrow;  // query / LSE row
-  int g;     // KV head
-  int tg0;   // first 16-token group of the batch within the unit
-  int last;  // last batch of the unit
-  int c0;    // first chunk of the unit
-  int64_t qbase;  // element offset of (qrow, first query head of g) in q
-  int64_t lbase;  // element offset of (qrow, first query head of g) in lse
-};
-
-template <int KB, int STEPS>
-struct Batch {
-  Raw16 k[KB][STEPS];
-  Raw16 q[STEPS];
-  float lse[4];
-  BatchCtx c;
-};
+using namespace score;
 
 // STEPS = head_dim / 32.  KB = 16-token groups per batch.  WGS = workgroups
 // per CU the register budget is sized for.  HMAX = per-token head max.
@@ -127,205 +53,9 @@ __global__ __launch_bounds__(kThreads, WGS) void chunk_score_kernel(ScoreArgs a)
   build_row_prefix(a.batch, s_prefix, s_scratch,
                    [&](int r) { return (s_len[r] + a.U - 1) / a.U * units_per_span; });
   const int total = s_prefix[a.batch];
-
-  const int lane = threadIdx.x & 63;
-  const int col = lane & 15;   // A row (query head in group) / B column (token in group)
-  const int kgrp = lane >> 4;  // 8-element k slice of the 32-wide MFMA step
   const int gw = uniform(blockIdx.x * kWaves + (threadIdx.x >> 6));
-  const int tw = gridDim.x * kWaves;
-  const int bph = (a.ntu + KB - 1) / KB;     // batches per KV head of a unit
-  const int bpu = bph * (HMAX ? a.Hkv : 1);  // batches per unit
-
-  int row_hint = 0;
-  auto ctx_of = [&](int n) -> BatchCtx {
-    BatchCtx c{};
-    const int k = bpu == 1 ? n : n / bpu;
-    const int j = n - k * bpu;
-    const int unit = gw + k * tw;
-    if (unit >= total) return c;
-    int lo = row_hint, hi = a.batch - 1;  // unit positions grow along the stream
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_prefix[mid] <= unit) lo = mid; else hi = mid - 1;
-    }
-    row_hint = lo;
-    const int r = unit - s_prefix[lo];
-    const int span = HMAX ? r : udiv(r, a.Hkv, a.hkv_log2);
-    const int head_in_unit = bph == 1 ? j : j / bph;
-    c.valid = 1;
-    c.b = lo;
-    c.t0 = span * a.U;
-    c.len = s_len[lo];
-    c.qrow = s_qrow[lo];
-    c.g = (HMAX ? 0 : r - span * a.Hkv) + head_in_unit;
-    c.tg0 = (j - head_in_unit * bph) * KB;
-    c.last = j == bpu - 1;
-    c.c0 = span * a.cpu;
-    c.qbase = static_cast<int64_t>(c.qrow) * a.q_stride + static_cast<int64_t>(c.g * a.G) * a.D;
-    c.lbase = static_cast<int64_t>(c.qrow) * a.lse_row_stride + static_cast<int64_t>(c.g * a.G) * a.lse_head_stride;
-    return c;
-  };
-
-  // Every load below is issued unconditionally, from wave-uniform bases plus
-  // small per-lane offsets: lanes and batches with nothing to read use a
-  // valid dummy address (row 0, or a clamped head / in-block row) and
-  // compute() masks them.  Each batch therefore adds a fixed number of loads,
-  // and the wait for the batch being computed never drains the next batch.
-  //
-  // kb[i] = element offset of token group i's first row for KV head g
-  // (uniform: the group lies inside one block).  Reading lanes past the row
-  // end stays inside that block.
-  auto pages_of = [&](const BatchCtx& c, int64_t (&kb)[KB]) {
-#pragma unroll
-    for (int i = 0; i < KB; ++i) {
-      kb[i] = 0;
-      if (UNIFORM_PAGE) {
-        const int tg = c.tg0 + i;
-        const int tok0 = c.t0 + tg * 16;
-        const bool ok = c.valid && tg < a.ntu && tok0 < c.len;
-        const int64_t idx = ok ? static_cast<int64_t>(c.b) * a.bt_stride + uniform(udiv(tok0, a.block_size, a.bs_log2)) : 0;
-        const int64_t page = scalar_load(a.bt + idx);
-        kb[i] = ok ? page * a.k_block_stride + static_cast<int64_t>(umod(tok0, a.block_size, a.bs_log2)) * a.k_token_stride +
-                         static_cast<int64_t>(c.g) * a.k_head_stride
-                   : 0;
-      }
-    }
-  };
-
-  const int64_t lane_k = static_cast<int64_t>(col) * a.k_token_stride + kgrp * 8;
-  const int q_head = min(col, a.G - 1);  // rows >= G read a real head; masked later
-
-  auto load = [&](const BatchCtx& c, const int64_t (&kb)[KB], Batch<KB, STEPS>& out) {
-    out.c = c;
-#pragma unroll
-    for (int i = 0; i < KB; ++i) {
-      const uint16_t* krow;
-      if (UNIFORM_PAGE) {
-        krow = a.k + kb[i] + lane_k;
-      } else {
-        const int tg = c.tg0 + i;
-        const int tin = tg * 16 + col;
-        const int tok = c.t0 + tin;
-        const bool ok = c.valid && tg < a.ntu && tin < a.U && tok < c.len;
-        const int64_t page = a.bt[ok ? static_cast<int64_t>(c.b) * a.bt_stride + tok / a.block_size : 0];
-        const int64_t off = ok ? page * a.k_block_stride + static_cast<int64_t>(tok % a.block_size) * a.k_token_stride +
-                                     static_cast<int64_t>(c.g) * a.k_head_stride
-                               : 0;
-        krow = a.k + off + kgrp * 8;
-      }
-#pragma unroll
-      for (int s = 0; s < STEPS; ++s) out.k[i][s] = *reinterpret_cast<const Raw16*>(krow + 32 * s);
-    }
-    const uint16_t* qh = a.q + c.qbase + static_cast<int64_t>(q_head) * a.D + kgrp * 8;
-#pragma unroll
-    for (int s = 0; s < STEPS; ++s) out.q[s] = *reinterpret_cast<const Raw16*>(qh + 32 * s);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = min(4 * kgrp + i, a.G - 1);
-      out.lse[i] = a.lse[c.lbase + static_cast<int64_t>(m) * a.lse_head_stride];
-    }
-  };
-
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};  // per chunk of the unit (head mean)
-  float tmax[kMaxNtu];                  // per 16-token group (head max)
-#pragma unroll
-  for (int t = 0; t < kMaxNtu; ++t) tmax[t] = 0.f;
-
-  auto compute = [&](const Batch<KB, STEPS>& bt) {
-    const BatchCtx& c = bt.c;
-#pragma unroll
-    for (int i = 0; i < KB; ++i) {
-      const int tg = c.tg0 + i;
-      if (tg >= a.ntu) continue;  // wave-uniform
-      // Everything between the MFMA chain and the first read of its result
-      // stays branch-free: the chunk index is one shift, computed up front.
-      const int ci = (tg * 16) >> a.ci_shift;
-      f32x4_t logit = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < STEPS; ++s) logit = mfma16x16x32<DT>(bt.q[s], bt.k[i][s], logit);
-      const int tin = tg * 16 + col;
-      const bool tok_ok = tin < a.U && c.t0 + tin < c.len;
-      if (HMAX) {
-        float m4 = 0.f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (4 * kgrp + e < a.G && tok_ok) m4 = fmaxf(m4, __expf(logit[e] * a.scale - bt.lse[e]));
-        }
-        m4 = fmaxf(m4, __shfl_xor(m4, 16, 64));
-        m4 = fmaxf(m4, __shfl_xor(m4, 32, 64));
-#pragma unroll
-        for (int t = 0; t < kMaxNtu; ++t) {
-          if (t == tg) tmax[t] = fmaxf(tmax[t], m4);
-        }
-      } else {
-        float s = 0.f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (4 * kgrp + e < a.G && tok_ok) s += __expf(logit[e] * a.scale - bt.lse[e]);
-        }
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) acc[cc] += cc == ci ? s : 0.f;
-      }
-    }
-    if (!c.last) return;
-    const int chunks_row = (c.len + a.chunk - 1) / a.chunk;
-    if (HMAX) {
-      for (int cc = 0; cc < a.cpu; ++cc) {
-        float s = 0.f;
-#pragma unroll
-        for (int t = 0; t < kMaxNtu; ++t) {
-          if (kgrp == 0 && t < a.ntu && (t * 16) / a.chunk == cc && t * 16 + col < a.U &&
-              c.t0 + t * 16 + col < c.len) {
-            s += tmax[t];
-          }
-        }
-        s = wave_sum(s);
-        const int ch = c.c0 + cc;
-        if (lane == 0 && ch < chunks_row) {
-          const int n_valid = min(a.chunk, c.len - ch * a.chunk);
-          a.out[static_cast<int64_t>(c.b) * a.out_stride + ch] = s / static_cast<float>(n_valid);
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < kMaxNtu; ++t) tmax[t] = 0.f;
-    } else {
-#pragma unroll
-      for (int cc = 0; cc < 4; ++cc) {
-        if (cc < a.cpu) {
-          const float s = wave_sum_to_lane63(acc[cc]);
-          const int ch = c.c0 + cc;
-          if (lane == 63 && ch < chunks_row) {
-            a.partial[(static_cast<int64_t>(c.b) * a.max_chunks + ch) * a.Hkv + c.g] = s;
-          }
-        }
-        acc[cc] = 0.f;
-      }
-    }
-  };
-
-  // Three-stage pipeline, unrolled by two so every buffer index is static.
-  // Per half: vector loads for batch n+1 (their block-table entries arrived
-  // a half earlier), then the block-table lookups for n+2, then the maths of
-  // batch n.  Scalar loads complete out of order, so the lookups are issued
-  // after the loads that consume the previous ones.
-  BatchCtx cx0 = ctx_of(0), cx1 = ctx_of(1);
-  int64_t pg0[KB], pg1[KB];
-  pages_of(cx0, pg0);
-  pages_of(cx1, pg1);
-  Batch<KB, STEPS> d0, d1;
-  load(cx0, pg0, d0);
-  for (int n = 0;; n += 2) {
-    if (!d0.c.valid) break;
-    load(cx1, pg1, d1);
-    cx0 = ctx_of(n + 2);
-    pages_of(cx0, pg0);
-    compute(d0);
-    if (!d1.c.valid) break;
-    load(cx0, pg0, d0);
-    cx1 = ctx_of(n + 3);
-    pages_of(cx1, pg1);
-    compute(d1);
-  }
+  score_stream<DT, STEPS, KB, HMAX, UNIFORM_PAGE, false>(a, s_prefix, s_len, s_qrow, total, gw,
+                                                         gridDim.x * kWaves, 0u);
 
   if (a.write_tail) {
     // Head max writes final scores; chunks at or beyond a row's length are 0.
@@ -398,12 +128,14 @@ void launch_steps(hipStream_t stream, const ScoreArgs& a, int64_t grid, bool uni
 // Shared by ds_chunk_scores and the fused step.  With head_reduce = mean the
 // kernel writes per-KV-head partials ([batch, max_chunks, Hkv] in `partial`);
 // with max it writes final scores to `out` (and zero tails if write_tail).
-int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_t q_stride, const void* key_cache,
-                        int64_t k_block_stride, int64_t k_token_stride, int64_t k_head_stride, const float* lse,
-                        int64_t lse_row_stride, int64_t lse_head_stride, const int32_t* block_table,
-                        int64_t bt_stride, const RowSource& src, int batch, int num_q_heads, int num_kv_heads,
-                        int head_dim, int block_size, int chunk_size, int max_chunks, float scale, int head_reduce,
-                        float* partial, float* out, int64_t out_stride, int write_tail, size_t partial_bytes) {
+int make_score_args(ScoreArgs& a, int64_t& upper_units, bool& uniform_page, int dtype, const void* query,
+                    int64_t q_stride, const void* key_cache, int64_t k_block_stride, int64_t k_token_stride,
+                    int64_t k_head_stride, const float* lse, int64_t lse_row_stride, int64_t lse_head_stride,
+                    const int32_t* block_table, int64_t bt_stride, const RowSource& src, int batch, int num_q_heads,
+                    int num_kv_heads, int head_dim, int block_size, int chunk_size, int max_chunks, float scale,
+                    int head_reduce, float* partial, float* out, int64_t out_stride, int write_tail,
+                    size_t partial_bytes) {
+  upper_units = 0;
   DS_REQUIRE(dtype == DS_BF16 || dtype == DS_FP16, "chunk scores support BF16 or FP16 query/key caches");
   DS_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0,
              "query heads must be divisible by KV heads");
@@ -437,7 +169,7 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
   DS_REQUIRE(!hmax || out != nullptr, "null score output pointer");
   DS_REQUIRE(src.seq_lens != nullptr || src.counts != nullptr, "null seq_lens pointer");
 
-  ScoreArgs a{};
+  a = ScoreArgs{};
   a.q = static_cast<const uint16_t*>(query);
   a.q_stride = q_stride;
   a.k = static_cast<const uint16_t*>(key_cache);
@@ -479,9 +211,27 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
   a.write_tail = hmax ? write_tail : 0;
 
   const int64_t spans = (static_cast<int64_t>(max_chunks) * chunk_size + U - 1) / U;
-  const int64_t upper_units = static_cast<int64_t>(batch) * spans * (hmax ? 1 : num_kv_heads);
+  upper_units = static_cast<int64_t>(batch) * spans * (hmax ? 1 : num_kv_heads);
+  uniform_page = (block_size % 16 == 0) && (U % 16 == 0);
+  return clear_error();
+}
+
+int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_t q_stride, const void* key_cache,
+                        int64_t k_block_stride, int64_t k_token_stride, int64_t k_head_stride, const float* lse,
+                        int64_t lse_row_stride, int64_t lse_head_stride, const int32_t* block_table,
+                        int64_t bt_stride, const RowSource& src, int batch, int num_q_heads, int num_kv_heads,
+                        int head_dim, int block_size, int chunk_size, int max_chunks, float scale, int head_reduce,
+                        float* partial, float* out, int64_t out_stride, int write_tail, size_t partial_bytes) {
+  ScoreArgs a{};
+  int64_t upper_units = 0;
+  bool uniform_page = false;
+  const int rc = make_score_args(a, upper_units, uniform_page, dtype, query, q_stride, key_cache, k_block_stride,
+                                 k_token_stride, k_head_stride, lse, lse_row_stride, lse_head_stride, block_table,
+                                 bt_stride, src, batch, num_q_heads, num_kv_heads, head_dim, block_size, chunk_size,
+                                 max_chunks, scale, head_reduce, partial, out, out_stride, write_tail, partial_bytes);
+  if (rc != DS_OK || upper_units == 0) return rc;
+  const bool hmax = head_reduce == DS_HEAD_MAX;
   const int64_t upper_blocks = (upper_units + kWaves - 1) / kWaves;
-  const bool uniform_page = (block_size % 16 == 0) && (U % 16 == 0);
   if (dtype == DS_BF16) {
     if (hmax) launch_steps<DS_BF16, true>(stream, a, upper_blocks, uniform_page);
     else launch_steps<DS_BF16, false>(stream, a, upper_blocks, uniform_page);

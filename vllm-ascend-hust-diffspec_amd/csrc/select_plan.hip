@@ -13,109 +13,19 @@
 //   4. the plan row [slot, history_len, tail_start, prefix_len, prefix_drop,
 //      chunk ids..., 0...] is built from the slot's selection in the same
 //      workgroup (block reduction for prefix_tokens).
-#include "rowdesc.h"
+#include "select_body.h"
 
 namespace ds355 {
 namespace {
 
-constexpr int kThreads = 256;
+using namespace select;
+
 constexpr int kLdsKeys = 12288;  // candidates kept in LDS; larger rows read keys from global memory
-constexpr int kMaxSel = 2048;    // chunk ids per selection
 constexpr int kPre = 4;          // chunks per thread whose partials are loaded at kernel start
-
-struct SelectArgs {
-  float* scores;           // final scores [batch, score_stride]; written here when partials are given
-  int64_t score_stride;
-  const float* partials;   // per-KV-head sums [batch, max_chunks, hkv] from the score pass, or nullptr
-  int max_chunks, hkv, hq;
-  RowSource src;
-  int batch;
-  int chunk;
-  int budget;  // history budget (multiple of chunk)
-  int do_select;
-  int do_plan;
-  int32_t* ids;  // selection output / state, row = slot (or b without slots)
-  int64_t ids_stride;
-  int32_t* counts;
-  const int32_t* slots;  // nullptr: row b writes selection row b
-  const int32_t* committed_lens;
-  int64_t* plan;
-  int plan_width;
-  int32_t* working_lens;
-  int recent_window;
-  int num_slots;
-};
-
-__device__ __forceinline__ uint32_t order_key(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;  // NaN: largest
-  if ((u & 0x7fffffffu) == 0u) u = 0u;                      // -0 == +0
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-// Workgroup barrier for LDS hand-offs only.  Unlike __syncthreads it does
-// not wait for this wave's outstanding global stores (the score row), which
-// other kernels read and this workgroup does not.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-// Exclusive scan over the 256 threads through LDS; `total` gets the sum.
-__device__ __forceinline__ int lds_exclusive_scan(int v, int* scratch, int& total) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int inc = wave_inclusive_scan(v);
-  if (lane == 63) scratch[wave] = inc;
-  lds_barrier();
-  int base = 0;
-  total = 0;
-#pragma unroll
-  for (int w = 0; w < kThreads / 64; ++w) {
-    const int t = scratch[w];
-    if (w < wave) base += t;
-    total += t;
-  }
-  lds_barrier();
-  return base + inc - v;
-}
-
-__device__ __forceinline__ int block_inclusive_scan(int v, int* scratch) {
-  int total;
-  return lds_exclusive_scan(v, scratch, total) + v;
-}
-
-__device__ __forceinline__ int block_sum(int v, int* scratch) {
-  int total;
-  lds_exclusive_scan(v, scratch, total);
-  return total;
-}
-
-// Sum of one chunk's per-KV-head partials in head order (HKV == 0: runtime
-// count); the HKV loads are unconditional and issued together.
-template <int HKV>
-__device__ __forceinline__ float head_sum(const float* pp, int hkv) {
-  float sum = 0.f;
-  if constexpr (HKV > 0) {
-    float v[HKV];
-#pragma unroll
-    for (int g = 0; g < HKV; ++g) v[g] = pp[g];
-#pragma unroll
-    for (int g = 0; g < HKV; ++g) sum += v[g];
-  } else {
-    for (int g = 0; g < hkv; ++g) sum += pp[g];
-  }
-  return sum;
-}
 
 template <int HKV>
 __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
-  __shared__ uint32_t s_keys[kLdsKeys];
-  __shared__ int s_hist[256];
-  __shared__ int s_ids[kMaxSel];
-  __shared__ int s_scratch[4];
-  __shared__ int s_digit, s_above, s_eq;
+  __shared__ SelectShared<kLdsKeys> sh;
 
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
@@ -138,26 +48,23 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
       pre[u] = head_sum<HKV>(part + static_cast<int64_t>(i) * a.hkv, a.hkv);
     }
   }
-  int n_sel = -1;  // selection made by this workgroup (in s_ids), -1 if none
+  int n_sel = -1;  // selection made by this workgroup (in sh.ids), -1 if none
 
   if (a.do_select && d.active && slot_ok) {
     const int C = (d.len + a.chunk - 1) / a.chunk;
     const int K = a.budget / a.chunk;
     if (C <= K) {
-      for (int i = tid; i < C; i += kThreads) s_ids[i] = i;
+      for (int i = tid; i < C; i += kThreads) sh.ids[i] = i;
       n_sel = C;
     }
     float* row_scores = a.scores + static_cast<int64_t>(b) * a.score_stride;
     const int N = C - 1;  // candidates (newest chunk excluded from the ranking)
     const bool in_lds = C > K && N <= kLdsKeys;
     if (a.partials != nullptr) {
-      // Final scores from the per-KV-head partials (fixed head order):
-      // sum_g / n_valid / Hq, the same rounding steps as the drop-in finalize.
       auto finish = [&](int i, float sum) {
-        const int n_valid = min(a.chunk, d.len - i * a.chunk);
-        const float v = (sum / static_cast<float>(n_valid)) / static_cast<float>(a.hq);
+        const float v = chunk_score(sum, a.chunk, d.len, i, a.hq);
         row_scores[i] = v;
-        if (in_lds && i < N) s_keys[i] = order_key(v);
+        if (in_lds && i < N) sh.keys[i] = order_key(v);
       };
 #pragma unroll
       for (int u = 0; u < kPre; ++u) {
@@ -168,7 +75,7 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
         finish(i, head_sum<HKV>(part + static_cast<int64_t>(i) * a.hkv, a.hkv));
       }
     } else if (in_lds) {
-      for (int i = tid; i < N; i += kThreads) s_keys[i] = order_key(row_scores[i]);
+      for (int i = tid; i < N; i += kThreads) sh.keys[i] = order_key(row_scores[i]);
     }
     if (in_lds) {
       lds_barrier();
@@ -176,129 +83,32 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
       __syncthreads();  // keys are read back from the score row in global memory
     }
     if (C > K) {
-      int need = K - 1;
-      auto key_at = [&](int i) -> uint32_t { return in_lds ? s_keys[i] : order_key(row_scores[i]); };
-
-      uint32_t prefix = 0u, pmask = 0u;
-      bool take_all_ties = true;
-      if (need > 0) {
-        for (int shift = 24; shift >= 0; shift -= 8) {
-          s_hist[tid] = 0;
-          lds_barrier();
-          for (int i = tid; i < N; i += kThreads) {
-            const uint32_t k = key_at(i);
-            if ((k & pmask) == prefix) atomicAdd(&s_hist[(k >> shift) & 0xffu], 1);
-          }
-          lds_barrier();
-          const int digit = 255 - tid;  // thread t scans bins in descending digit order
-          const int cnt = s_hist[digit];
-          const int incl = block_inclusive_scan(cnt, s_scratch);
-          if (incl - cnt < need && need <= incl) {
-            s_digit = digit;
-            s_above = incl - cnt;
-            s_eq = cnt;
-          }
-          lds_barrier();
-          prefix |= static_cast<uint32_t>(s_digit) << shift;
-          pmask |= 0xffu << shift;
-          need -= s_above;
-          if (shift == 0) take_all_ties = (need == s_eq);
-          lds_barrier();
-        }
-      }
-      // need = ties (key == T) still to take, lowest indices first.
-      const uint32_t T = prefix;
-      const bool none = (K - 1) == 0;
-      int carry_sel = 0, carry_eq = 0;
-      if (!none) {
-        for (int base = 0; base < N; base += kThreads) {
-          const int i = base + tid;
-          const uint32_t k = i < N ? key_at(i) : 0u;
-          const bool gt = i < N && k > T;
-          const bool eq = i < N && k == T;
-          bool sel;
-          if (take_all_ties) {
-            sel = gt || eq;
-          } else {
-            int eq_total;
-            const int eq_ex = lds_exclusive_scan(eq ? 1 : 0, s_scratch, eq_total);
-            sel = gt || (eq && carry_eq + eq_ex < need);
-            carry_eq += eq_total;
-          }
-          int sel_total;
-          const int sel_ex = lds_exclusive_scan(sel ? 1 : 0, s_scratch, sel_total);
-          if (sel && carry_sel + sel_ex < kMaxSel) s_ids[carry_sel + sel_ex] = i;
-          carry_sel += sel_total;
-        }
-      }
-      if (tid == 0) s_ids[K - 1] = C - 1;
+      select_top(sh, N, K, [&](int i) -> uint32_t { return in_lds ? sh.keys[i] : order_key(row_scores[i]); });
       n_sel = K;
     }
     lds_barrier();
     int32_t* out = a.ids + static_cast<int64_t>(slot) * a.ids_stride;
-    for (int j = tid; j < n_sel; j += kThreads) out[j] = s_ids[j];
+    for (int j = tid; j < n_sel; j += kThreads) out[j] = sh.ids[j];
     if (tid == 0) a.counts[slot] = n_sel;
   }
 
   if (!a.do_plan) return;
-  int64_t* prow = a.plan + static_cast<int64_t>(b) * a.plan_width;
   if (!slot_ok) {
+    int64_t* prow = a.plan + static_cast<int64_t>(b) * a.plan_width;
     for (int j = tid; j < a.plan_width; j += kThreads) prow[j] = 0;
     return;
   }
-  // The slot's selection: just made here, or the stored one.
-  const int64_t cap = min(static_cast<int64_t>(a.plan_width - 5), a.ids_stride);
-  const int count = n_sel >= 0 ? n_sel : static_cast<int>(min(static_cast<int64_t>(stored_count), cap));
-  const int32_t* stored = a.ids + static_cast<int64_t>(slot) * a.ids_stride;
-  auto chunk_id = [&](int j) -> int64_t { return n_sel >= 0 ? s_ids[j] : stored[j]; };
-
-  const int64_t end = max(0, committed - 1);
-  const int64_t hb = a.budget;
-  int64_t len, tail_start, prefix_len = 0, drop = 0;
-  int ncols = 0;
-  if (count < 0) {
-    len = min(end, hb);
-    tail_start = end - len;
-  } else {
-    const int64_t tail_len = min(min(end, static_cast<int64_t>(a.recent_window)), hb);
-    tail_start = end - tail_len;
-    len = tail_len;
-    if (count > 0) {
-      ncols = min(count, a.plan_width - 5);
-      const int64_t prefix_end = min(tail_start, chunk_id(count - 1) * a.chunk);
-      int64_t part = 0;
-      for (int j = tid; j < count; j += kThreads) {
-        const int64_t t = prefix_end - chunk_id(j) * a.chunk;
-        part += t <= 0 ? 0 : (t < a.chunk ? t : a.chunk);
-      }
-      // Block sum in int (each term <= chunk; the total <= count * chunk).
-      const int64_t prefix_tokens = block_sum(static_cast<int>(part), s_scratch);
-      prefix_len = min(prefix_tokens, hb - tail_len);
-      drop = prefix_tokens - prefix_len;
-      len = prefix_len + tail_len;
-    }
-  }
-  for (int j = tid; j < a.plan_width; j += kThreads) {
-    int64_t v;
-    if (j == 0) v = slot;
-    else if (j == 1) v = len;
-    else if (j == 2) v = tail_start;
-    else if (j == 3) v = prefix_len;
-    else if (j == 4) v = drop;
-    else v = (j - 5) < ncols ? chunk_id(j - 5) : 0;
-    prow[j] = v;
-  }
-  if (tid == 0 && a.working_lens != nullptr) a.working_lens[slot] = static_cast<int32_t>(len);
+  write_plan_row<false>(a, b, slot, committed, n_sel, stored_count, sh);
 }
 
 }  // namespace
 
-int launch_select_plan(hipStream_t stream, float* scores, int64_t score_stride, const float* partials,
-                       int max_chunks, int hkv, int hq, const RowSource& src,
-                       int batch, int chunk, int budget, int do_select, int do_plan, int32_t* ids,
-                       int64_t ids_stride, int32_t* counts, const int32_t* slots, int num_slots,
-                       const int32_t* committed_lens, int64_t* plan, int plan_width, int32_t* working_lens,
-                       int recent_window) {
+int make_select_args(SelectArgs& a, float* scores, int64_t score_stride, const float* partials, int max_chunks,
+                     int hkv, int hq, const RowSource& src, int batch, int chunk, int budget, int do_select,
+                     int do_plan, int32_t* ids, int64_t ids_stride, int32_t* counts, const int32_t* slots,
+                     int num_slots, const int32_t* committed_lens, int64_t* plan, int plan_width,
+                     int32_t* working_lens, int recent_window) {
+  a = SelectArgs{};
   DS_REQUIRE(chunk > 0, "chunk_size must be positive");
   DS_REQUIRE(budget >= chunk && budget % chunk == 0, "token_budget must be a positive chunk-size multiple");
   DS_SUPPORTED(budget / chunk <= kMaxSel, "at most %d selected chunks (got %d)", kMaxSel, budget / chunk);
@@ -314,7 +124,6 @@ int launch_select_plan(hipStream_t stream, float* scores, int64_t score_stride, 
   if (do_plan) DS_REQUIRE(ids && counts && committed_lens && plan, "null plan pointer");
 
   if (do_select && partials != nullptr) DS_REQUIRE(hkv > 0 && hq > 0 && max_chunks > 0, "bad score partial shape");
-  SelectArgs a{};
   a.scores = scores;
   a.score_stride = score_stride;
   a.partials = partials;
@@ -337,6 +146,20 @@ int launch_select_plan(hipStream_t stream, float* scores, int64_t score_stride, 
   a.plan_width = plan_width;
   a.working_lens = working_lens;
   a.recent_window = recent_window;
+  return clear_error();
+}
+
+int launch_select_plan(hipStream_t stream, float* scores, int64_t score_stride, const float* partials,
+                       int max_chunks, int hkv, int hq, const RowSource& src,
+                       int batch, int chunk, int budget, int do_select, int do_plan, int32_t* ids,
+                       int64_t ids_stride, int32_t* counts, const int32_t* slots, int num_slots,
+                       const int32_t* committed_lens, int64_t* plan, int plan_width, int32_t* working_lens,
+                       int recent_window) {
+  SelectArgs a;
+  const int rc = make_select_args(a, scores, score_stride, partials, max_chunks, hkv, hq, src, batch, chunk, budget,
+                                  do_select, do_plan, ids, ids_stride, counts, slots, num_slots, committed_lens, plan,
+                                  plan_width, working_lens, recent_window);
+  if (rc != DS_OK || batch == 0) return rc;
   switch (do_select && partials != nullptr ? hkv : 0) {
     case 1: select_plan_kernel<1><<<batch, kThreads, 0, stream>>>(a); break;
     case 2: select_plan_kernel<2><<<batch, kThreads, 0, stream>>>(a); break;

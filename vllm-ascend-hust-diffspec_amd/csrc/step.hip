@@ -1,4 +1,5 @@
-// One retrieval step as a launch chain on one stream:
+// One retrieval step on one stream: the single-launch kernel (fused.hip)
+// when the descriptor brings a workspace and fits it, otherwise a chain:
 //   chunk_score_kernel (rows with committed tokens; committed query; rejected
 //   suffix cut) -> select_plan_kernel (selection into the per-slot state,
 //   then a plan row for every real row) -> gather kernel over the plan.
@@ -28,6 +29,8 @@ int rebuild_compact_kv_impl(hipStream_t stream, int dtype, const void* raw_key, 
                             int max_model_len, int heads, int head_dim, int token_budget, int chunk_size,
                             int rotary_dim, int is_neox_style, int max_width, const int32_t* row_active,
                             bool padded_rows);
+
+int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource& src, bool& launched);
 
 }  // namespace ds355
 
@@ -60,7 +63,10 @@ extern "C" int ds_retrieval_step(ds_stream_t stream_handle, const ds_step_desc* 
                "score and score-partial buffers are required");
     DS_REQUIRE(d->num_kv_heads > 0 && d->num_q_heads > 0, "head counts must be positive");
   }
-  int rc;
+  src.max_len = static_cast<int>(std::min<int64_t>(static_cast<int64_t>(d->max_chunks) * d->chunk_size, INT32_MAX));
+  bool launched = false;
+  int rc = launch_fused_step(stream, d, src, launched);
+  if (rc != DS_OK || launched) return rc;
   if (score) {
     rc = launch_chunk_scores(stream, d->dtype, d->query, d->q_stride, d->key_cache, d->k_block_stride,
                              d->k_token_stride, d->k_head_stride, d->lse, d->lse_token_stride, d->lse_head_stride,
@@ -70,7 +76,6 @@ extern "C" int ds_retrieval_step(ds_stream_t stream_handle, const ds_step_desc* 
     if (rc != DS_OK) return rc;
   }
   if (select || rebuild) {
-    src.max_len = static_cast<int>(std::min<int64_t>(static_cast<int64_t>(d->max_chunks) * d->chunk_size, INT32_MAX));
     rc = launch_select_plan(stream, d->scores, d->max_chunks, d->score_partials, d->max_chunks, d->num_kv_heads,
                             d->num_q_heads, src, d->batch_rows, d->chunk_size, d->history_budget,
                             select ? 1 : 0, rebuild ? 1 : 0, d->sel_ids, d->sel_stride, d->sel_count, d->slots,

@@ -18,7 +18,7 @@ DS_OK, DS_ERR_INVALID, DS_ERR_UNSUPPORTED, DS_ERR_HIP = 0, 1, 2, 3
 DS_BF16, DS_FP16, DS_FP32 = 0, 1, 2
 DS_HEAD_MEAN, DS_HEAD_MAX = 0, 1
 DS_STAGE_SCORE, DS_STAGE_SELECT, DS_STAGE_PLAN, DS_STAGE_ALL = 1, 2, 4, 7
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 EXPORTED_SYMBOLS = (
     "ds_last_error",
@@ -28,6 +28,7 @@ EXPORTED_SYMBOLS = (
     "ds_build_plan",
     "ds_rebuild_compact_kv",
     "ds_retrieval_step",
+    "ds_step_workspace_bytes",
 )
 
 _DTYPES = {torch.bfloat16: DS_BF16, torch.float16: DS_FP16, torch.float32: DS_FP32}
@@ -70,6 +71,7 @@ class StepDesc(ctypes.Structure):
         ("rotary_dim", _i32), ("is_neox_style", _i32),
         ("row_active", _p),
         ("chunk_size", _i32), ("history_budget", _i32), ("recent_window", _i32),
+        ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -87,6 +89,7 @@ _SIGNATURES = {
         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p,
     ]),
     "ds_retrieval_step": (_i32, [_p, ctypes.POINTER(StepDesc)]),
+    "ds_step_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32, _i32]),
 }
 
 _lib: ctypes.CDLL | None = None

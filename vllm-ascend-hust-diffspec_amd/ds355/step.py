@@ -107,6 +107,7 @@ def build_step_desc(
     history_budget: int,
     recent_window: int | None = None,
     row_active: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
 ) -> tuple[_lib.StepDesc, torch.device]:
     """Validate and pack a step descriptor for ``stages`` (``SCORE | SELECT | PLAN``; ``ALL`` = one step).
 
@@ -115,7 +116,8 @@ def build_step_desc(
     ``ceil(max target_len / chunk_size)``; SELECT writes the final scores
     there) and ``score_partials`` (``[batch_rows, max_chunks, Hkv]`` fp32, the
     per-KV-head sums SCORE writes and SELECT reads).  PLAN writes ``plan`` and
-    gathers.
+    gathers.  ``workspace`` (from ``new_workspace``) lets a full step run as
+    one launch when its shapes allow it; the results are the same.
     """
     if stages & ~ALL:
         raise ValueError(f"unknown stage bits {stages:#x}")
@@ -145,8 +147,11 @@ def build_step_desc(
         _i32("working_lens", working_lens, num_slots)
     if row_active is not None:
         _i32("row_active", row_active, batch_rows)
+    if workspace is not None and (workspace.dtype != torch.uint8 or not workspace.is_contiguous()
+                                  or workspace.data_ptr() % 64 != 0):
+        raise ValueError("workspace must be a contiguous, 64-byte aligned uint8 tensor (see new_workspace)")
     tensors = [sel_ids, sel_count, slots, committed_lens, plan, raw_key, raw_value, working_key, working_value,
-               cos_sin_cache, working_lens, row_active]
+               cos_sin_cache, working_lens, row_active, workspace]
 
     desc = _lib.StepDesc()
     desc.stages = stages
@@ -215,4 +220,30 @@ def build_step_desc(
     desc.row_active = _lib.ptr(row_active)
     desc.chunk_size, desc.history_budget = chunk_size, history_budget
     desc.recent_window = chunk_size if recent_window is None else recent_window
+    desc.workspace = _lib.ptr(workspace)
+    desc.workspace_bytes = 0 if workspace is None else workspace.numel()
     return desc, device
+
+
+def workspace_bytes(batch_rows: int, max_chunks: int, num_kv_heads: int, token_budget: int) -> int:
+    """Bytes of the single-launch step's workspace for these buffer sizes."""
+    return int(_lib.load().ds_step_workspace_bytes(batch_rows, max_chunks, num_kv_heads, token_budget))
+
+
+def new_workspace(batch_rows: int, max_chunks: int, num_kv_heads: int, token_budget: int,
+                  device: torch.device) -> torch.Tensor:
+    """A zero-filled workspace; keep it for the life of the buffers (one step at a time)."""
+    n = workspace_bytes(batch_rows, max_chunks, num_kv_heads, token_budget)
+    if n <= 0:
+        raise ValueError("batch_rows, max_chunks, num_kv_heads and token_budget must be positive")
+    return torch.zeros((n,), dtype=torch.uint8, device=device)
+
+
+def workspace_epoch(workspace: torch.Tensor) -> int:
+    """Number of single-launch steps completed on this workspace (synchronises)."""
+    return int(workspace[:4].view(torch.int32).item()) & 0xFFFFFFFF
+
+
+def workspace_status(workspace: torch.Tensor) -> int:
+    """Status word: 0 unless a bounded wait of the single-launch step expired (synchronises)."""
+    return int(workspace[8:12].view(torch.int32).item()) & 0xFFFFFFFF

@@ -157,8 +157,8 @@ int ds_rebuild_compact_kv(ds_stream_t stream, int dtype,
  * synchronisation, launch shapes fixed by the descriptor's upper bounds
  * (graph-capturable).  With all three stages and a workspace, shapes the
  * fused kernel covers (bf16/fp16 KV, head_dim 64 or 128, <= 8 KV heads,
- * <= 256 rows, 16-token-aligned pages) run as one launch with the same
- * results.
+ * 8 to 256 batch rows, 16-token-aligned pages) run as one launch with the
+ * same results.
  */
 enum ds_stage { DS_STAGE_SCORE = 1, DS_STAGE_SELECT = 2, DS_STAGE_PLAN = 4, DS_STAGE_ALL = 7 };
 

@@ -45,7 +45,7 @@ def test_fused_equals_chain_bitwise(cuda):
 
 
 def test_fused_repeated_launches_and_reused_workspace(cuda):
-    """Three launches on one workspace, then a smaller batch with another layout in the same bytes."""
+    """Three launches on one workspace, then another batch shape and layout in the same bytes."""
     from ds355 import step
 
     case = _ragged(12, 8, 2000, 12000)
@@ -58,7 +58,7 @@ def test_fused_repeated_launches_and_reused_workspace(cuda):
         run_gpu(case, cuda, state=state, path="fused")
         _same(ref, state)
     assert step.workspace_epoch(state["workspace"]) == 3
-    small = _ragged(13, 3, 500, 4000, hkv=2, hq=16, head_dim=64, chunk=32, token_budget=1024, block_size=64)
+    small = _ragged(13, 9, 500, 4000, hkv=2, hq=16, head_dim=64, chunk=32, token_budget=1024, block_size=64)
     small_ref = run_gpu(small, cuda, path="chain")
     small_state = run_gpu(small, cuda, path="chain")
     small_state["work_k"].fill_(float("nan"))
@@ -73,6 +73,14 @@ def test_fused_repeated_launches_and_reused_workspace(cuda):
 def test_unsupported_shape_with_workspace_runs_chain(cuda):
     """head_dim 96 is outside the fused kernel: the same call runs the chain and leaves the epoch."""
     case = _ragged(14, 4, 300, 5000, head_dim=96)
+    chain = run_gpu(case, cuda, path="chain")
+    state = run_gpu(case, cuda, path="fused", single_launch=False)
+    _same(chain, state)
+
+
+def test_small_batch_with_workspace_runs_chain(cuda):
+    """Below 8 rows the chain is faster; the same call runs it and leaves the epoch."""
+    case = _ragged(15, 3, 2000, 9000)
     chain = run_gpu(case, cuda, path="chain")
     state = run_gpu(case, cuda, path="fused", single_launch=False)
     _same(chain, state)

@@ -83,8 +83,13 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kSelectors = 16;     // selecting workgroups (fewer when the batch has fewer rows)
 constexpr int kFusedKeys = 8192;   // candidate keys a selector keeps in LDS
 constexpr int kFusedRows = 256;    // batch rows per fused launch
-constexpr int kPoll = 4;           // chunks per thread polled together
-constexpr int kMaxHkv = 8;         // KV heads per chunk polled together
+// Fewer rows than this run the chain: the single launch gains by hiding
+// rows' selections and gathers behind other rows' scoring, and with a few
+// long rows the last selection dominates (measured: 4 rows of 128k tokens
+// 157 µs single launch against 130 µs chain; one 8k row 27 against 21).
+constexpr int kMinFusedRows = 8;
+constexpr int kPollLoads = 32;     // partials per thread polled together (kPollLoads / Hkv chunks)
+constexpr int kMaxHkv = 8;         // KV heads the fused kernel takes
 constexpr int kGatherHeads = 4;    // heads in flight per gather task
 constexpr int kMinTaskPositions = 8;  // ppw >= 8 for the fused shapes: task_cap = ceil(token_budget / 8)
 constexpr uint32_t kSpinLimit = 1u << 21;   // polls before a wait without deadline gives up (~2 s)
@@ -147,28 +152,26 @@ __device__ __forceinline__ void wait_sentinel(const uint64_t* p, uint32_t tag, u
   }
 }
 
-// Head sums of chunks base + u * kThreads + tid (u < kPoll, below C), in head
-// order, once all of their partials carry `tag`.
+// Head sums of chunks base + u * kThreads + tid (u < kPollLoads / hkv,
+// below C), in head order, once all of their partials carry `tag`.  The
+// kPollLoads loads of a poll are issued together.
 __device__ __forceinline__ void poll_chunk_sums(const uint64_t* part, int base, int C, int hkv, uint32_t tag,
-                                                uint32_t* header, float (&sum)[kPoll]) {
-  uint64_t v[kPoll][kMaxHkv] = {};
+                                                uint32_t* header, float (&sum)[kPollLoads]) {
+  const int per_chunk = hkv;  // loads per chunk; kPollLoads / hkv chunks per thread
+  uint64_t v[kPollLoads] = {};
   for (uint32_t spin = 0;; ++spin) {
     bool ready = true;
 #pragma unroll
-    for (int u = 0; u < kPoll; ++u) {
+    for (int e = 0; e < kPollLoads; ++e) {
+      const int u = e / per_chunk, g = e - u * per_chunk;
       const int i = base + u * kThreads + static_cast<int>(threadIdx.x);
-#pragma unroll
-      for (int g = 0; g < kMaxHkv; ++g) {
-        if (g < hkv && i < C) v[u][g] = coherent_load(part + static_cast<int64_t>(i) * hkv + g);
-      }
+      if (i < C) v[e] = coherent_load(part + static_cast<int64_t>(i) * hkv + g);
     }
 #pragma unroll
-    for (int u = 0; u < kPoll; ++u) {
+    for (int e = 0; e < kPollLoads; ++e) {
+      const int u = e / per_chunk;
       const int i = base + u * kThreads + static_cast<int>(threadIdx.x);
-#pragma unroll
-      for (int g = 0; g < kMaxHkv; ++g) {
-        if (g < hkv && i < C && static_cast<uint32_t>(v[u][g] >> 32) != tag) ready = false;
-      }
+      if (i < C && static_cast<uint32_t>(v[e] >> 32) != tag) ready = false;
     }
     if (ready) break;
     if (spin >= kSpinLimit || (spin % kStatusEvery == kStatusEvery - 1 && coherent_load(header + kStatus) != 0u)) {
@@ -177,13 +180,13 @@ __device__ __forceinline__ void poll_chunk_sums(const uint64_t* part, int base, 
     }
     __builtin_amdgcn_s_sleep(kSleep);
   }
+  // sum[u] = chunk u's head sum, heads added in order.
 #pragma unroll
-  for (int u = 0; u < kPoll; ++u) {
-    sum[u] = 0.f;
+  for (int u = 0; u < kPollLoads; ++u) sum[u] = 0.f;
 #pragma unroll
-    for (int g = 0; g < kMaxHkv; ++g) {
-      if (g < hkv) sum[u] += __uint_as_float(static_cast<uint32_t>(v[u][g]));
-    }
+  for (int e = 0; e < kPollLoads; ++e) {
+    const int u = e / per_chunk;
+    sum[u] += __uint_as_float(static_cast<uint32_t>(v[e]));
   }
 }
 
@@ -212,13 +215,14 @@ __device__ __forceinline__ void select_row(const FusedArgs& f, int b, uint32_t t
     const bool in_lds = C > K && N <= kFusedKeys;
     const uint64_t* part = f.s.tagged + static_cast<int64_t>(b) * a.max_chunks * a.hkv;
     if (C > 0) wait_sentinel(part + static_cast<int64_t>(C) * a.hkv - 1, tag, f.header);
-    for (int base = 0; base < C; base += kPoll * kThreads) {
-      float sum[kPoll];
+    const int per_poll = kPollLoads / a.hkv;  // chunks per thread and poll
+    for (int base = 0; base < C; base += per_poll * kThreads) {
+      float sum[kPollLoads];
       poll_chunk_sums(part, base, C, a.hkv, tag, f.header, sum);
 #pragma unroll
-      for (int u = 0; u < kPoll; ++u) {
+      for (int u = 0; u < kPollLoads; ++u) {
         const int i = base + u * kThreads + tid;
-        if (i < C) {
+        if (u < per_poll && i < C) {
           const float v = chunk_score(sum[u], a.chunk, d.len, i, a.hq);
           row_scores[i] = v;
           if (in_lds && i < N) sh.keys[i] = order_key(v);
@@ -231,7 +235,13 @@ __device__ __forceinline__ void select_row(const FusedArgs& f, int b, uint32_t t
       __syncthreads();  // keys are read back from the score row in global memory
     }
     if (C > K) {
-      select_top(sh, N, K, [&](int i) -> uint32_t { return in_lds ? sh.keys[i] : order_key(row_scores[i]); });
+      select_top(sh, N, K, [&](int q) -> U4 {
+        if (in_lds) return *reinterpret_cast<const U4*>(&sh.keys[4 * q]);
+        U4 k4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) k4[j] = order_key(row_scores[min(4 * q + j, N - 1)]);
+        return k4;
+      });
       n_sel = K;
     }
     lds_barrier();
@@ -533,7 +543,7 @@ int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource
   const int steps = d->head_dim / 32;
   const bool fits = d->dtype == d->kv_dtype && (d->dtype == DS_BF16 || d->dtype == DS_FP16) &&
                     (d->head_dim == 64 || d->head_dim == 128) && d->num_kv_heads <= kMaxHkv &&
-                    d->batch_rows >= 1 && d->batch_rows <= kFusedRows && uniform_page && vec &&
+                    d->batch_rows >= kMinFusedRows && d->batch_rows <= kFusedRows && uniform_page && vec &&
                     scalar_grid > 0 && d->slots != nullptr && d->history_budget / d->chunk_size <= select::kMaxSel &&
                     64 / f.g.lanes_per_row >= kMinTaskPositions;
   if (!fits) return clear_error();

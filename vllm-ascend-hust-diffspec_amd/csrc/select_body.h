@@ -37,10 +37,11 @@ struct SelectArgs {
 // LDS of one selecting workgroup.  KEYS = candidates whose keys stay in LDS.
 template <int KEYS>
 struct SelectShared {
-  uint32_t keys[KEYS];
+  alignas(16) uint32_t keys[KEYS + 4];  // + 4: a 4-key read at the end stays inside
   int hist[256];
   int ids[kMaxSel];
   int scratch[4];
+  int wcount[2 * kThreads / 64];  // per-wave counts of the compaction
   int digit, above, eq;
 };
 
@@ -114,11 +115,22 @@ __device__ __forceinline__ float chunk_score(float sum, int chunk, int len, int 
   return (sum / static_cast<float>(n_valid)) / static_cast<float>(hq);
 }
 
-// Top K - 1 of the N candidates (chunks 0..N-1, keys from key_at) plus the
-// newest chunk N, ascending, into sh.ids[0..K).  Starts and ends on a
+typedef uint32_t U4 __attribute__((ext_vector_type(4)));
+
+// Top K - 1 of the N candidates (chunks 0..N-1) plus the newest chunk N,
+// ascending, into sh.ids[0..K).  key4_at(q) returns the keys of candidates
+// 4q .. 4q + 3 (values past N are ignored).  Starts and ends on a
 // barrier-separated LDS state; requires N + 1 > K.
-template <int KEYS, typename KeyAt>
-__device__ __forceinline__ void select_top(SelectShared<KEYS>& sh, int N, int K, KeyAt key_at) {
+//   - Four 8-bit MSB radix passes (LDS histogram, block scan over the bins)
+//     find T, the (K-1)-th largest key.  A thread reads 4 keys at a time.
+//   - Compaction: wave w owns the contiguous candidates
+//     [w * span, (w + 1) * span), 256 at a time, lane l holding candidates
+//     4l .. 4l + 3 of each 256.  A first sweep counts keys > T and ties
+//     (== T) with ballots; one barrier shares the four waves' counts, which
+//     fixes each wave's first output slot and how many ties it takes (ties
+//     go to the lowest indices); a second sweep writes the ids in order.
+template <int KEYS, typename Key4At>
+__device__ __forceinline__ void select_top(SelectShared<KEYS>& sh, int N, int K, Key4At key4_at) {
   const int tid = threadIdx.x;
   int need = K - 1;
   uint32_t prefix = 0u, pmask = 0u;
@@ -127,9 +139,12 @@ __device__ __forceinline__ void select_top(SelectShared<KEYS>& sh, int N, int K,
     for (int shift = 24; shift >= 0; shift -= 8) {
       sh.hist[tid] = 0;
       lds_barrier();
-      for (int i = tid; i < N; i += kThreads) {
-        const uint32_t k = key_at(i);
-        if ((k & pmask) == prefix) atomicAdd(&sh.hist[(k >> shift) & 0xffu], 1);
+      for (int q = tid; 4 * q < N; q += kThreads) {
+        const U4 k4 = key4_at(q);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (4 * q + j < N && (k4[j] & pmask) == prefix) atomicAdd(&sh.hist[(k4[j] >> shift) & 0xffu], 1);
+        }
       }
       lds_barrier();
       const int digit = 255 - tid;  // thread t scans bins in descending digit order
@@ -150,27 +165,71 @@ __device__ __forceinline__ void select_top(SelectShared<KEYS>& sh, int N, int K,
   }
   // need = ties (key == T) still to take, lowest indices first.
   const uint32_t T = prefix;
-  const bool none = (K - 1) == 0;
-  int carry_sel = 0, carry_eq = 0;
-  if (!none) {
-    for (int base = 0; base < N; base += kThreads) {
-      const int i = base + tid;
-      const uint32_t k = i < N ? key_at(i) : 0u;
-      const bool gt = i < N && k > T;
-      const bool eq = i < N && k == T;
-      bool sel;
-      if (take_all_ties) {
-        sel = gt || eq;
-      } else {
-        int eq_total;
-        const int eq_ex = lds_exclusive_scan(eq ? 1 : 0, sh.scratch, eq_total);
-        sel = gt || (eq && carry_eq + eq_ex < need);
-        carry_eq += eq_total;
+  if (K - 1 > 0) {
+    constexpr int kW = kThreads / 64;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const uint64_t below = (uint64_t{1} << lane) - 1;  // lanes before this one
+    const int span = ((N + kW - 1) / kW + 255) / 256 * 256;
+    const int lo = min(N, wave * span);
+    const int hi = min(N, lo + span);
+    int gt = 0, eq = 0;
+    for (int b = lo; b < hi; b += 256) {
+      const U4 k4 = key4_at((b >> 2) + lane);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = b + 4 * lane + j;
+        gt += static_cast<int>(__popcll(__ballot(i < hi && k4[j] > T)));
+        eq += static_cast<int>(__popcll(__ballot(i < hi && k4[j] == T)));
       }
-      int sel_total;
-      const int sel_ex = lds_exclusive_scan(sel ? 1 : 0, sh.scratch, sel_total);
-      if (sel && carry_sel + sel_ex < kMaxSel) sh.ids[carry_sel + sel_ex] = i;
-      carry_sel += sel_total;
+    }
+    if (lane == 0) {
+      sh.wcount[wave] = gt;
+      sh.wcount[kW + wave] = eq;
+    }
+    lds_barrier();
+    int out = 0, eq_before = 0, take_eq = 0;
+#pragma unroll
+    for (int w = 0; w < kW; ++w) {
+      const int w_eq = sh.wcount[kW + w];
+      const int w_take = take_all_ties ? w_eq : max(0, min(w_eq, need - eq_before));
+      if (w < wave) out += sh.wcount[w] + w_take;
+      if (w == wave) take_eq = w_take;
+      eq_before += w_eq;
+    }
+    int taken = 0;
+    for (int b = lo; b < hi; b += 256) {
+      const U4 k4 = key4_at((b >> 2) + lane);
+      uint64_t eq_mask[4], sel_mask[4];
+      bool sel[4];
+      // Ties of this lane's earlier keys in the 256, then of lanes below.
+      int tie_rank = taken;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = b + 4 * lane + j;
+        eq_mask[j] = __ballot(i < hi && k4[j] == T);
+        tie_rank += static_cast<int>(__popcll(eq_mask[j] & below));
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = b + 4 * lane + j;
+        const bool is_eq = i < hi && k4[j] == T;
+        sel[j] = i < hi && (k4[j] > T || (is_eq && tie_rank < take_eq));
+        if (is_eq) ++tie_rank;
+        sel_mask[j] = __ballot(sel[j]);
+      }
+      int pos = out;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pos += static_cast<int>(__popcll(sel_mask[j] & below));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (sel[j]) {
+          if (pos < kMaxSel) sh.ids[pos] = b + 4 * lane + j;
+          ++pos;
+        }
+        out += static_cast<int>(__popcll(sel_mask[j]));
+        taken += static_cast<int>(__popcll(eq_mask[j]));
+      }
     }
   }
   if (tid == 0) sh.ids[K - 1] = N;

@@ -71,8 +71,20 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
         const int i = u * kThreads + tid;
         if (i < C) finish(i, pre[u]);
       }
-      for (int i = kPre * kThreads + tid; i < C; i += kThreads) {
-        finish(i, head_sum<HKV>(part + static_cast<int64_t>(i) * a.hkv, a.hkv));
+      // Longer rows: kPre chunks per thread at a time, their loads issued
+      // together (clamped to the buffer, masked when finished).
+      for (int i0 = kPre * kThreads; i0 < C; i0 += kPre * kThreads) {
+        float v[kPre];
+#pragma unroll
+        for (int u = 0; u < kPre; ++u) {
+          const int i = min(i0 + u * kThreads + tid, a.max_chunks - 1);
+          v[u] = head_sum<HKV>(part + static_cast<int64_t>(i) * a.hkv, a.hkv);
+        }
+#pragma unroll
+        for (int u = 0; u < kPre; ++u) {
+          const int i = i0 + u * kThreads + tid;
+          if (i < C) finish(i, v[u]);
+        }
       }
     } else if (in_lds) {
       for (int i = tid; i < N; i += kThreads) sh.keys[i] = order_key(row_scores[i]);
@@ -83,7 +95,13 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
       __syncthreads();  // keys are read back from the score row in global memory
     }
     if (C > K) {
-      select_top(sh, N, K, [&](int i) -> uint32_t { return in_lds ? sh.keys[i] : order_key(row_scores[i]); });
+      select_top(sh, N, K, [&](int q) -> U4 {
+        if (in_lds) return *reinterpret_cast<const U4*>(&sh.keys[4 * q]);
+        U4 k4;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) k4[j] = order_key(row_scores[min(4 * q + j, N - 1)]);
+        return k4;
+      });
       n_sel = K;
     }
     lds_barrier();

@@ -217,10 +217,10 @@ int ds_retrieval_step(ds_stream_t stream, const ds_step_desc* desc);
 /*
  * Workspace of the single-launch step for these buffer sizes (0 when one of
  * them is not positive).  No reference counterpart: it holds the stages'
- * hand-over state (64 header bytes; a 256-byte line per row for its plan
- * flag; a 4-byte state per gather task, ceil(token_budget / 8) per row,
- * rounded up to 256 bytes; tagged score partials [batch_rows, max_chunks,
- * num_kv_heads] x 8 bytes).  A workspace serves one launch at a time; word 2
+ * hand-over state (64 header bytes; a tagged copy of each plan row, 128
+ * 8-byte columns per row; a 4-byte state per gather task,
+ * ceil(token_budget / 8) per row, rounded up to 256 bytes; tagged score
+ * partials [batch_rows, max_chunks, num_kv_heads] x 8 bytes).  A workspace serves one launch at a time; word 2
  * of its header is a status word that stays 0 unless a wait of the fused
  * kernel expired (then that launch's results are not valid).
  */

@@ -155,13 +155,13 @@ def test_reference_validation_order_on_host():
 
 
 def test_step_workspace_size():
-    """Header (64 B), a 256-byte line per row for its plan flag, 4-byte task states
+    """Header (64 B), a 1 KiB tagged plan copy per row, 4-byte task states
     (ceil(token_budget / 8) per row, rounded up to 256 B), 8-byte tagged partials."""
     from ds355 import _lib
 
     lib = _lib.load()
-    assert lib.ds_step_workspace_bytes(3, 10, 4, 2048) == 64 + 3 * 256 + 3 * 256 * 4 + 3 * 10 * 4 * 8
-    assert lib.ds_step_workspace_bytes(17, 640, 4, 100) == 64 + 17 * 256 + 1024 + 17 * 640 * 4 * 8  # 17 * 13 * 4 -> 1024
+    assert lib.ds_step_workspace_bytes(3, 10, 4, 2048) == 64 + 3 * 1024 + 3 * 256 * 4 + 3 * 10 * 4 * 8
+    assert lib.ds_step_workspace_bytes(17, 640, 4, 100) == 64 + 17 * 1024 + 1024 + 17 * 640 * 4 * 8  # 17 * 13 * 4 -> 1024
     assert lib.ds_step_workspace_bytes(0, 10, 4, 2048) == 0
     assert lib.ds_step_workspace_bytes(3, 0, 4, 2048) == 0
     assert lib.ds_step_workspace_bytes(3, 10, 4, 0) == 0

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from helpers import gen
-from test_gpu_step import build_case, run_gpu
+from test_gpu_step import build_case, check_step, run_gpu
 
 pytestmark = pytest.mark.gpu
 
@@ -84,3 +84,15 @@ def test_small_batch_with_workspace_runs_chain(cuda):
     chain = run_gpu(case, cuda, path="chain")
     state = run_gpu(case, cuda, path="fused", single_launch=False)
     _same(chain, state)
+
+
+@pytest.mark.parametrize("dtype,neox,head_dim", [(torch.float16, False, 128), (torch.float16, True, 64),
+                                                 (torch.bfloat16, False, 64)])
+def test_fused_fp16_and_gptj(cuda, dtype, neox, head_dim):
+    """The single launch's other instances (fp16 caches, GPT-J rotary, head_dim 64): oracle parity and
+    the chain's bytes."""
+    case = _ragged(16, 9, 700, 9000, dtype=dtype, neox=neox, head_dim=head_dim, hq=16, hkv=2)
+    fused = run_gpu(case, cuda, path="fused")
+    check_step(case, fused)
+    chain = run_gpu(case, cuda, path="chain")
+    _same(chain, fused)

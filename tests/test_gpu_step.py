@@ -19,7 +19,8 @@ pytestmark = pytest.mark.gpu
 
 
 def build_case(seed, *, real_rows, pad_rows, target_lens, query_len, counts, hq, hkv, head_dim, chunk,
-               token_budget, block_size, lmax, slots, num_slots, depth=4, prev_counts=None):
+               token_budget, block_size, lmax, slots, num_slots, depth=4, prev_counts=None, dtype=torch.bfloat16,
+               neox=True):
     g = gen(seed)
     rows = real_rows + pad_rows
     qlens = [query_len] * real_rows + [1] * pad_rows
@@ -27,9 +28,9 @@ def build_case(seed, *, real_rows, pad_rows, target_lens, query_len, counts, hq,
     ends = [sum(qlens[: i + 1]) for i in range(rows)]
     starts = [0, *ends[:-1]]
     tokens = ends[-1]
-    query = randn((tokens, hq, head_dim), torch.bfloat16, g)
+    query = randn((tokens, hq, head_dim), dtype, g)
     lse = torch.randn((tokens, hq), generator=g)
-    key_cache, table = paged_keys(tlens, hkv, head_dim, block_size, torch.bfloat16, g)
+    key_cache, table = paged_keys(tlens, hkv, head_dim, block_size, dtype, g)
     scale = default_scale(head_dim)
     # Exact LSE for each committed query over its causal prefix.
     _, q_index, lengths = O.retrieval_rows(counts, ends, tlens, real_rows)
@@ -38,8 +39,8 @@ def build_case(seed, *, real_rows, pad_rows, target_lens, query_len, counts, hq,
     exact = lse_for(query[q_index], key_cache, table[scored_rows], lengths, scale)
     for j, qi in enumerate(q_index):
         lse[qi] = exact[j]
-    raw_k = randn((num_slots, lmax, hkv, head_dim), torch.bfloat16, g)
-    raw_v = randn((num_slots, lmax, hkv, head_dim), torch.bfloat16, g)
+    raw_k = randn((num_slots, lmax, hkv, head_dim), dtype, g)
+    raw_v = randn((num_slots, lmax, hkv, head_dim), dtype, g)
     budget = O.history_budget(token_budget, depth, chunk)
     return dict(
         query=query, lse=lse, key_cache=key_cache, table=table, scale=scale, counts=counts + [0] * pad_rows,
@@ -47,7 +48,7 @@ def build_case(seed, *, real_rows, pad_rows, target_lens, query_len, counts, hq,
         slots=slots + [-1] * pad_rows, num_slots=num_slots, raw_k=raw_k, raw_v=raw_v, chunk=chunk,
         token_budget=token_budget, budget=budget, hq=hq, hkv=hkv, head_dim=head_dim, lmax=lmax,
         committed=[tl - ql + min(max(c, 1), ql) for tl, ql, c in zip(tlens, qlens, counts + [0] * pad_rows)],
-        cos_sin=O.rope_cos_sin_cache(head_dim, token_budget),
+        cos_sin=O.rope_cos_sin_cache(head_dim, token_budget).to(dtype), dtype=dtype, neox=neox,
     )
 
 
@@ -73,7 +74,7 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="cha
             plan=torch.zeros((rows, 5 + case["token_budget"] // case["chunk"]), dtype=torch.int64, device=device),
             working_lens=torch.zeros((case["num_slots"],), dtype=torch.int32, device=device),
             work_k=torch.full((case["num_slots"], case["hkv"], case["token_budget"], case["head_dim"]),
-                              float("nan"), dtype=torch.bfloat16, device=device),
+                              float("nan"), dtype=case["dtype"], device=device),
             raw_k=case["raw_k"].to(device), raw_v=case["raw_v"].to(device),
             query=case["query"].to(device), lse=case["lse"].to(device), key_cache=case["key_cache"].to(device),
             table=case["table"].to(device), cos_sin=case["cos_sin"].to(device),
@@ -94,7 +95,7 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="cha
         committed_lens=i32(case["committed"]), plan=state["plan"], working_lens=state["working_lens"],
         raw_key=state["raw_k"], raw_value=state["raw_v"], working_key=state["work_k"],
         working_value=state["work_v"], cos_sin_cache=state["cos_sin"], rotary_dim=case["head_dim"],
-        is_neox_style=True, chunk_size=case["chunk"], history_budget=case["budget"],
+        is_neox_style=case["neox"], chunk_size=case["chunk"], history_budget=case["budget"],
         row_active=None if row_active is None else i32(row_active),
         workspace=state.get("workspace") if fused else None,
     )
@@ -141,12 +142,12 @@ def check_step(case, state, *, previous=None, row_active=None):
     expected_plan = O.pad_plan(plans, case["token_budget"], chunk)
     assert torch.equal(state["plan"].cpu(), expected_plan)
     # Working cache.
-    exp_k = torch.full(tuple(state["work_k"].shape), float("nan"), dtype=torch.bfloat16)
+    exp_k = torch.full(tuple(state["work_k"].shape), float("nan"), dtype=case["dtype"])
     exp_v = exp_k.clone()
     width = max(p[1] for p in plans)
     O.rebuild_compact_kv_from_plan(case["raw_k"], case["raw_v"], exp_k, exp_v, expected_plan, case["cos_sin"],
                                    chunk_size=chunk, max_width=width, rotary_dim=case["head_dim"],
-                                   is_neox_style=True, row_active=row_active)
+                                   is_neox_style=case["neox"], row_active=row_active)
     got_k, got_v = state["work_k"].cpu(), state["work_v"].cpu()
     assert torch.equal(got_k.isnan(), exp_k.isnan())
     assert torch.equal(torch.nan_to_num(got_v), torch.nan_to_num(exp_v))

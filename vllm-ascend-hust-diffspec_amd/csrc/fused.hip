@@ -20,16 +20,19 @@
 //     selector first polls one sentinel, the partial of the row's newest
 //     chunk and last KV head (written in the row's last round of units),
 //     then reads the row's partials until all carry the tag;
-//   - a selector stores the plan row with coherent stores, waits until they
-//     have completed, then stores flags[row] = tag.  Gathering waves poll the
-//     flag and read the plan row with one coherent wave-wide load;
+//   - a selector stores the plan row twice: as the output (plain stores) and
+//     as a tagged copy, column j as (tag << 32) | value (plan values are
+//     below 2^31).  Gathering waves poll the tagged copy itself with one
+//     wave-wide load (lane l, columns l and 64 + l): it is valid once every
+//     column carries the tag, so no flag, and no wait for the stores to
+//     complete, stands between a plan and its gathers;
 //   - after each gather task its wave stores state[row][task] = tag (done),
 //     or tag | kSkipped when it gave up waiting for the plan.
 // Polling is the costly part of this design: every poll is a device-scope
 // request to one memory channel, and thousands of waves polling one line
-// slow every stream that shares the channel.  So each row's flag has its own
-// line, polls sleep between tries, and a selector reads its full row only
-// after the sentinel arrived.
+// slow every stream that shares the channel.  So each row's tagged plan has
+// lines of its own, polls sleep between tries, and a selector reads its full
+// row only after the sentinel arrived.
 //
 // Forward progress does not depend on all workgroups being resident at once
 // (the launch is an ordinary one).  Workgroups are dispatched in index order
@@ -49,7 +52,7 @@
 //
 // Workspace (zero-filled once by its owner; one launch at a time):
 //   uint32 header[16]               epoch, done counter, status
-//   uint32 flags[rows]              plan published (tag), one per 256-byte line
+//   uint64 plans[rows][kPlanCols]   tagged plan copies
 //   uint32 state[rows][task_cap]    gather task done / skipped
 //   uint64 partials[rows, max_chunks, Hkv]
 #include "gather_body.h"
@@ -88,7 +91,7 @@ constexpr int kFusedRows = 256;    // batch rows per fused launch
 // long rows the last selection dominates (measured: 4 rows of 128k tokens
 // 157 µs single launch against 130 µs chain; one 8k row 27 against 21).
 constexpr int kMinFusedRows = 8;
-constexpr int kPollLoads = 32;     // partials per thread polled together (kPollLoads / Hkv chunks)
+constexpr int kPollLoads = 16;     // partials per thread polled together (kPollLoads / Hkv chunks)
 constexpr int kMaxHkv = 8;         // KV heads the fused kernel takes
 constexpr int kGatherHeads = 4;    // heads in flight per gather task
 constexpr int kMinTaskPositions = 8;  // ppw >= 8 for the fused shapes: task_cap = ceil(token_budget / 8)
@@ -99,10 +102,8 @@ constexpr int kSleep = 8;          // s_sleep units (64 cycles each) between pol
 
 enum { kEpoch = 0, kDone = 1, kStatus = 2, kHeaderWords = 16 };
 enum { kStatusPartials = 1u, kStatusTasks = 2u };
-// Each row's plan flag sits on its own 256-byte line, so waves polling
-// different rows do not queue on one line.
 constexpr int kLine = 256;
-constexpr int kFlagStride = kLine / sizeof(uint32_t);
+constexpr int kPlanCols = 128;     // tagged plan columns per row (plan_width <= 128)
 constexpr int kStatusEvery = 256;  // polls between looks at the shared status word
 
 struct FusedArgs {
@@ -110,7 +111,7 @@ struct FusedArgs {
   select::SelectArgs p;
   gather::GatherArgs g;
   uint32_t* header;
-  uint32_t* flags;
+  uint64_t* plans;  // [rows, kPlanCols] tagged plan copies
   uint32_t* state;  // [rows, task_cap]
   int task_cap;
   int selectors;
@@ -130,12 +131,6 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
   const uint64_t u = static_cast<uint64_t>(v);
   const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
   const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
-  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-__device__ __forceinline__ int64_t lane_value(int64_t v, int lane) {
-  const uint64_t u = static_cast<uint64_t>(v);
-  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(u), lane);
-  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(u >> 32), lane);
   return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
@@ -249,47 +244,51 @@ __device__ __forceinline__ void select_row(const FusedArgs& f, int b, uint32_t t
     for (int j = tid; j < n_sel; j += kThreads) out[j] = sh.ids[j];
     if (tid == 0) a.counts[slot] = n_sel;
   }
+  uint64_t* tagged = f.plans + static_cast<int64_t>(b) * kPlanCols;
   if (slot_ok) {
-    write_plan_row<true>(a, b, slot, committed, n_sel, stored_count, sh);
+    write_plan_row(a, b, slot, committed, n_sel, stored_count, sh, tagged, tag);
   } else {
     int64_t* prow = a.plan + static_cast<int64_t>(b) * a.plan_width;
-    for (int j = tid; j < a.plan_width; j += kThreads) coherent_store(prow + j, int64_t{0});
+    for (int j = tid; j < a.plan_width; j += kThreads) {
+      prow[j] = 0;
+      coherent_store(tagged + j, static_cast<uint64_t>(tag) << 32);
+    }
   }
-  // Every wave's device-scope stores have completed before the flag is stored.
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0) coherent_store(f.flags + static_cast<int64_t>(b) * kFlagStride, tag);
 }
 
-// Plan row fields of one row, wave-uniform, and (when the row fits one
-// wave-wide load) the whole row with lane l holding column l.
+// A plan row as a gathering wave sees it: the fields, wave-uniform, and
+// the columns, lane l holding columns l (lo) and 64 + l (hi).
 struct PlanView {
-  int64_t slot, len, tail_start, prefix_len, drop, pv;
-  const int64_t* prow;
+  int64_t slot, len, tail_start, prefix_len, drop;
+  uint32_t lo, hi;
 };
 
-__device__ __forceinline__ PlanView load_plan(const gather::GatherArgs& ga, int r) {
-  PlanView v;
+// Polls row r's tagged plan until every column carries the tag, at most
+// `spins` polls (then returns false).
+__device__ __forceinline__ bool poll_plan(const FusedArgs& f, int r, uint32_t tag, uint32_t spins, PlanView& v) {
+  const gather::GatherArgs& ga = f.g;
   const int lane = threadIdx.x & 63;
-  v.prow = ga.plan + static_cast<int64_t>(r) * ga.plan_width;
-  v.pv = 0;
-  if (ga.plan_width <= 64) {
-    v.pv = lane < ga.plan_width ? coherent_load(v.prow + lane) : 0;
-    v.slot = lane_value(v.pv, 0);
-    v.len = lane_value(v.pv, 1);
-    v.tail_start = lane_value(v.pv, 2);
-    v.prefix_len = lane_value(v.pv, 3);
-    v.drop = lane_value(v.pv, 4);
-  } else {
-    v.slot = uniform64(coherent_load(v.prow + 0));
-    v.len = uniform64(coherent_load(v.prow + 1));
-    v.tail_start = uniform64(coherent_load(v.prow + 2));
-    v.prefix_len = uniform64(coherent_load(v.prow + 3));
-    v.drop = uniform64(coherent_load(v.prow + 4));
+  const uint64_t* row = f.plans + static_cast<int64_t>(r) * kPlanCols;
+  const bool has_lo = lane < ga.plan_width;
+  const bool has_hi = lane + 64 < ga.plan_width;
+  for (uint32_t spin = 0; spin < spins; ++spin) {
+    const uint64_t a = has_lo ? coherent_load(row + lane) : static_cast<uint64_t>(tag) << 32;
+    const uint64_t b = has_hi ? coherent_load(row + 64 + lane) : static_cast<uint64_t>(tag) << 32;
+    if (__ballot(static_cast<uint32_t>(a >> 32) != tag || static_cast<uint32_t>(b >> 32) != tag) == 0) {
+      v.lo = static_cast<uint32_t>(a);
+      v.hi = static_cast<uint32_t>(b);
+      v.slot = static_cast<int32_t>(__builtin_amdgcn_readlane(v.lo, 0));
+      v.len = min(static_cast<int64_t>(static_cast<int32_t>(__builtin_amdgcn_readlane(v.lo, 1))),
+                  static_cast<int64_t>(ga.pos_limit));
+      v.tail_start = static_cast<int32_t>(__builtin_amdgcn_readlane(v.lo, 2));
+      v.prefix_len = static_cast<int32_t>(__builtin_amdgcn_readlane(v.lo, 3));
+      v.drop = static_cast<int32_t>(__builtin_amdgcn_readlane(v.lo, 4));
+      if (v.slot < 0 || v.slot >= ga.num_slots) v.len = 0;
+      return true;
+    }
+    __builtin_amdgcn_s_sleep(kSleep);
   }
-  v.len = min(v.len, static_cast<int64_t>(ga.pos_limit));
-  if (v.slot < 0 || v.slot >= ga.num_slots) v.len = 0;
-  return v;
+  return false;
 }
 
 // Gather task t (local positions t * ppw ...) of the row in `v`.
@@ -297,15 +296,13 @@ template <int DT, bool NEOX>
 __device__ __forceinline__ void run_task(const gather::GatherArgs& ga, const gather::GatherLane& L,
                                          const PlanView& v, int t) {
   const int ppw = 64 / ga.lanes_per_row;
-  const bool one_load = ga.plan_width <= 64;
   gather::gather_task<DT, NEOX, kGatherHeads>(
       ga, L, t * ppw, v.slot, v.len, v.tail_start, v.prefix_len, v.drop, [&](int64_t c) {
-        if (one_load) {
-          // Chunk ids sit in lanes 5.. of pv; they are below 2^31.
-          return static_cast<int64_t>(__builtin_amdgcn_ds_bpermute(static_cast<int>(5 + c) << 2,
-                                                                   static_cast<int>(static_cast<uint64_t>(v.pv))));
-        }
-        return coherent_load(v.prow + 5 + c);
+        // Chunk id column 5 + c sits in lane (5 + c) % 64 of lo or hi.
+        const int col = static_cast<int>(5 + c);
+        const int lo = __builtin_amdgcn_ds_bpermute((col & 63) << 2, static_cast<int>(v.lo));
+        const int hi = __builtin_amdgcn_ds_bpermute((col & 63) << 2, static_cast<int>(v.hi));
+        return static_cast<int64_t>(col < 64 ? lo : hi);
       });
 }
 
@@ -333,16 +330,7 @@ __device__ __forceinline__ void gather_owned(const FusedArgs& f, const int* task
     const int r = __builtin_amdgcn_readfirstlane(lo);
     if (r != cur) {
       cur = r;
-      published = false;
-      const uint32_t* flag = f.flags + static_cast<int64_t>(r) * kFlagStride;
-      for (uint32_t spin = 0; spin < kOwnerSpins; ++spin) {
-        if (__builtin_amdgcn_readfirstlane(coherent_load(flag)) == tag) {
-          published = true;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(kSleep);
-      }
-      if (published) v = load_plan(ga, r);
+      published = poll_plan(f, r, tag, kOwnerSpins, v);
     }
     const int t = __builtin_amdgcn_readfirstlane(task - task_prefix[r]);
     if (published) run_task<DT, NEOX>(ga, L, v, t);
@@ -379,8 +367,11 @@ __device__ __forceinline__ void finish_row_tasks(const FusedArgs& f, const gathe
       const int k = __builtin_ctzll(skipped);
       skipped &= skipped - 1;
       if (!have_plan) {
-        v = load_plan(f.g, b);
-        have_plan = true;
+        have_plan = poll_plan(f, b, tag, kSpinLimit, v);  // published by this workgroup
+        if (!have_plan) {
+          raise_status(f.header, kStatusTasks);
+          break;
+        }
       }
       run_task<DT, NEOX>(f.g, L, v, t0 + k);
     }
@@ -459,7 +450,7 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
   }
 }
 
-size_t flags_bytes(int rows) { return static_cast<size_t>(rows) * kLine; }
+size_t plans_bytes(int rows) { return static_cast<size_t>(rows) * kPlanCols * sizeof(uint64_t); }
 int task_cap(int token_budget) { return (token_budget + kMinTaskPositions - 1) / kMinTaskPositions; }
 size_t state_bytes(int rows, int token_budget) {
   return (static_cast<size_t>(rows) * task_cap(token_budget) * sizeof(uint32_t) + kLine - 1) / kLine * kLine;
@@ -501,7 +492,7 @@ int launch_dt(hipStream_t stream, const FusedArgs& f, int steps, bool neox, int6
 
 size_t fused_workspace_bytes(int rows, int max_chunks, int num_kv_heads, int token_budget) {
   if (rows <= 0 || max_chunks <= 0 || num_kv_heads <= 0 || token_budget <= 0) return 0;
-  return kHeaderWords * sizeof(uint32_t) + flags_bytes(rows) + state_bytes(rows, token_budget) +
+  return kHeaderWords * sizeof(uint32_t) + plans_bytes(rows) + state_bytes(rows, token_budget) +
          static_cast<size_t>(rows) * max_chunks * num_kv_heads * sizeof(uint64_t);
 }
 
@@ -544,15 +535,15 @@ int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource
   const bool fits = d->dtype == d->kv_dtype && (d->dtype == DS_BF16 || d->dtype == DS_FP16) &&
                     (d->head_dim == 64 || d->head_dim == 128) && d->num_kv_heads <= kMaxHkv &&
                     d->batch_rows >= kMinFusedRows && d->batch_rows <= kFusedRows && uniform_page && vec &&
-                    scalar_grid > 0 && d->slots != nullptr && d->history_budget / d->chunk_size <= select::kMaxSel &&
+                    scalar_grid > 0 && d->slots != nullptr && d->plan_width <= kPlanCols &&
                     64 / f.g.lanes_per_row >= kMinTaskPositions;
   if (!fits) return clear_error();
 
   char* ws = static_cast<char*>(d->workspace);
   f.header = reinterpret_cast<uint32_t*>(ws);
   ws += kHeaderWords * sizeof(uint32_t);
-  f.flags = reinterpret_cast<uint32_t*>(ws);
-  ws += flags_bytes(d->batch_rows);
+  f.plans = reinterpret_cast<uint64_t*>(ws);
+  ws += plans_bytes(d->batch_rows);
   f.state = reinterpret_cast<uint32_t*>(ws);
   f.task_cap = task_cap(d->token_budget);
   ws += state_bytes(d->batch_rows, d->token_budget);

@@ -237,12 +237,14 @@ __device__ __forceinline__ void select_top(SelectShared<KEYS>& sh, int N, int K,
 
 // Plan row of batch row b for a valid slot, from the selection just made
 // (n_sel >= 0, ids in sh.ids) or the slot's stored one (n_sel < 0,
-// stored_count entries).  Writes plan[b] (with device-scope stores when
-// COHERENT) and working_lens[slot].  Contains barriers (block sum) when the
-// selection is non-empty.
-template <bool COHERENT, int KEYS>
+// stored_count entries).  Writes plan[b] and working_lens[slot]; with a
+// tagged copy, also stores column j as (tag << 32) | value in tagged[j]
+// with a device-scope store (plan values are below 2^31).  Contains
+// barriers (block sum) when the selection is non-empty.
+template <int KEYS>
 __device__ __forceinline__ void write_plan_row(const SelectArgs& a, int b, int slot, int committed, int n_sel,
-                                               int stored_count, SelectShared<KEYS>& sh) {
+                                               int stored_count, SelectShared<KEYS>& sh,
+                                               uint64_t* tagged = nullptr, uint32_t tag = 0) {
   const int tid = threadIdx.x;
   int64_t* prow = a.plan + static_cast<int64_t>(b) * a.plan_width;
   const int64_t cap = min(static_cast<int64_t>(a.plan_width - 5), a.ids_stride);
@@ -284,10 +286,9 @@ __device__ __forceinline__ void write_plan_row(const SelectArgs& a, int b, int s
     else if (j == 3) v = prefix_len;
     else if (j == 4) v = drop;
     else v = (j - 5) < ncols ? chunk_id(j - 5) : 0;
-    if constexpr (COHERENT) {
-      coherent_store(prow + j, v);
-    } else {
-      prow[j] = v;
+    prow[j] = v;
+    if (tagged != nullptr) {
+      coherent_store(tagged + j, (static_cast<uint64_t>(tag) << 32) | static_cast<uint32_t>(v));
     }
   }
   if (tid == 0 && a.working_lens != nullptr) a.working_lens[slot] = static_cast<int32_t>(len);

@@ -116,7 +116,7 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
     for (int j = tid; j < a.plan_width; j += kThreads) prow[j] = 0;
     return;
   }
-  write_plan_row<false>(a, b, slot, committed, n_sel, stored_count, sh);
+  write_plan_row(a, b, slot, committed, n_sel, stored_count, sh);
 }
 
 }  // namespace

@@ -226,6 +226,67 @@ int ds_retrieval_step(ds_stream_t stream, const ds_step_desc* desc);
  */
 size_t ds_step_workspace_bytes(int batch_rows, int max_chunks, int num_kv_heads, int token_budget);
 
+/*
+ * Draft decode attention over the working cache (linear drafting, one query
+ * token per row).
+ * Replaces DiffSpecDraftCache.forward_attention's linear path
+ * (diffspec/runtime.py:2024-2077 on the CPU, and the batched
+ * npu_fused_infer_attention_score call over the capacity view with
+ * actual_seq_lengths_kv = position + 1, diffspec/runtime.py:2079-2134).
+ *
+ * For every row r < rows, with s = slots[r] and
+ * p = positions ? positions[r] : working_lens[s] (read before this call
+ * changes it):
+ *   working_key[s, h, p] = key[r, h]; working_value[s, h, p] = value[r, h]
+ *   working_lens[s] = p + 1
+ *   out[r, hq] = sum_t softmax_t(scale * q[r, hq] . K[s, hq / G, t]) V[s, hq / G, t],
+ *                t = 0..p, G = num_q_heads / num_kv_heads (query head hq
+ *                uses KV head hq / G, the reference's repeat_interleave),
+ *                scores, softmax and the weighted sum in fp32, rounded once
+ *                to the output dtype;
+ * rows rows <= r < out_rows of `out` are written as zeros (the reference's
+ * output.zero_() for graph padding).  A row whose slot or position is out
+ * of range ([0, num_slots), [0, token_budget)) gets zeros, changes nothing
+ * else and sets bit 0 of the workspace status word (the reference raises
+ * "DiffSpec working cache exhausted" on the host).
+ *
+ * query  : [out_rows, Hq, D]   element (r, h, d) at r*q_row_stride + h*q_head_stride + d
+ * key, value: [rows, Hkv, D]   (new token's K/V, same addressing)
+ * out    : [out_rows, Hq, D]
+ * working_key / working_value: [num_slots, Hkv, token_budget, D] contiguous
+ * working_lens: int32 [num_slots]; slots, positions: int32 [rows]
+ * dtype  : DS_BF16 or DS_FP16 for every tensor; head_dim 64, 128 or 256;
+ *          row and head strides multiples of 8 elements, 16-byte aligned
+ *          pointers.
+ * workspace: zero-filled once, >= ds_draft_attention_workspace_bytes(),
+ *          256-byte aligned; reused across launches (one stream at a time).
+ *          Word 2 of its header is the status word (bit 1: a merge stopped
+ *          waiting for a partial result: that launch's output is not valid).
+ * One kernel launch, no host synchronisation, fixed launch shape for the
+ * given sizes (graph-capturable).
+ */
+int ds_draft_attention(ds_stream_t stream, int dtype,
+                       const void* query, int64_t q_row_stride, int64_t q_head_stride,
+                       const void* key, int64_t k_row_stride, int64_t k_head_stride,
+                       const void* value, int64_t v_row_stride, int64_t v_head_stride,
+                       void* out, int64_t o_row_stride, int64_t o_head_stride,
+                       void* working_key, void* working_value, int32_t* working_lens,
+                       const int32_t* slots, const int32_t* positions,
+                       int rows, int out_rows, int num_slots,
+                       int num_q_heads, int num_kv_heads, int head_dim, int token_budget,
+                       float scale, void* workspace, size_t workspace_bytes);
+
+/*
+ * Workspace bytes of ds_draft_attention for up to batch_rows rows (0 when
+ * an argument is not positive or Hq is not a multiple of Hkv).  No reference
+ * counterpart: 256 header bytes, 4 KiB of per-row counters, 512 KiB of
+ * per-(row, KV head, query block) counters, then tagged per-span partial
+ * results: batch_rows x Hkv x ceil(G / 16) x ceil(token_budget / span) x 16
+ * x (head_dim + 2) x 8 bytes, span = 256 tokens (128 for head_dim 256).
+ */
+size_t ds_draft_attention_workspace_bytes(int batch_rows, int num_q_heads, int num_kv_heads, int head_dim,
+                                          int token_budget);
+
 #ifdef __cplusplus
 }
 #endif

@@ -49,6 +49,7 @@ __all__ = [
     "rebuild_working_cache_per_request",
     "retrieval_rows",
     "retrieval_step",
+    "draft_linear_attention",
     "to_bf16_rne",
 ]
 
@@ -518,6 +519,50 @@ def retrieval_step(
     return {"scores": scores, "selections": selections, "plan": plan}
 
 
+def draft_linear_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    scale: float,
+    output: torch.Tensor,
+    working_key: torch.Tensor,
+    working_value: torch.Tensor,
+    working_lens: list[int] | torch.Tensor,
+    slots: list[int],
+    positions: list[int],
+) -> torch.Tensor:
+    """Linear draft attention over the working cache, in place.
+
+    Follows ``DiffSpecDraftCache.forward_attention`` (diffspec/runtime.py:2024-2077):
+    ``output`` is zeroed (rows past ``len(slots)`` stay zero, as graph padding
+    does in the batched NPU path, runtime.py:2097 and 2133); for row ``r`` with
+    slot ``s`` and local position ``p`` the new key/value row is written at
+    ``working[s, :, p]``, the working length becomes ``p + 1``, and every query
+    head ``h`` attends over positions ``0..p`` of KV head ``h // G`` (the
+    reference's ``repeat_interleave`` over the query-head axis).  Scores,
+    softmax and the weighted sum are fp32 with fp32 values, as the reference's
+    device test computes its expectation (tests/test_linear_attention_batch_npu.py:131-137;
+    the CPU loop itself only runs with fp32 caches, since ``einsum`` does not
+    mix fp32 probabilities with bf16 values); the result is rounded once to the
+    output dtype.
+    """
+    output.zero_()
+    kv_heads, head_dim = working_key.shape[1], working_key.shape[3]
+    group = query.shape[1] // kv_heads
+    for r, (slot, pos) in enumerate(zip(slots, positions)):
+        working_key[slot, :, pos] = key[r].reshape(kv_heads, head_dim)
+        working_value[slot, :, pos] = value[r].reshape(kv_heads, head_dim)
+        working_lens[slot] = pos + 1
+        keys = working_key[slot, :, : pos + 1].float()      # [Hkv, n, D]
+        values = working_value[slot, :, : pos + 1].float()
+        q = query[r].float().reshape(kv_heads, group, head_dim)
+        logits = torch.matmul(q, keys.transpose(1, 2)) * scale  # [Hkv, G, n]
+        weights = torch.softmax(logits, dim=-1)
+        out = torch.matmul(weights, values).reshape(kv_heads * group, head_dim)
+        output[r] = out.reshape(output[r].shape).to(output.dtype)
+    return output
+
+
 def to_bf16_rne(x: torch.Tensor) -> torch.Tensor:
     """fp32 -> bf16 with round-to-nearest-even, done on the bit pattern.
 
@@ -552,4 +597,8 @@ PINNING = {
     "retrieval_rows": "committed-query matrix test_runtime.py:72-142 and 532-605",
     "to_bf16_rne": "equals torch's fp32->bf16 cast on random and tie-heavy inputs",
     "retrieval_step": "composition of the pinned functions above; checked against them row by row",
+    "draft_linear_attention": "KAT of test_runtime.py:405-442 evaluated in closed form; single position -> "
+                               "the new value row; zero query -> mean of values; GQA head map h // G (planted "
+                               "h % Hkv map fails); NaN past each position never read "
+                               "(test_linear_attention_batch_npu.py:109-112)",
 }

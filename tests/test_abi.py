@@ -165,3 +165,58 @@ def test_step_workspace_size():
     assert lib.ds_step_workspace_bytes(0, 10, 4, 2048) == 0
     assert lib.ds_step_workspace_bytes(3, 0, 4, 2048) == 0
     assert lib.ds_step_workspace_bytes(3, 10, 4, 0) == 0
+
+
+def test_attention_workspace_size():
+    """256 header bytes, 4 KiB row counters, 512 KiB unit counters, then tagged
+    partials: rows x Hkv x ceil(G / 16) x spans x 16 x (D + 2) x 8 bytes."""
+    from ds355 import _lib
+
+    lib = _lib.load()
+    fixed = 256 + 4 * 1024 + 4 * 1024 * 128
+    assert lib.ds_draft_attention_workspace_bytes(16, 32, 4, 128, 2048) == fixed + 16 * 4 * 1 * 8 * 16 * 130 * 8
+    # G = 32 -> two query blocks; head_dim 256 -> 128-token spans; 100 tokens -> one span
+    assert lib.ds_draft_attention_workspace_bytes(3, 64, 2, 256, 2048) == fixed + 3 * 2 * 2 * 16 * 16 * 258 * 8
+    assert lib.ds_draft_attention_workspace_bytes(2, 8, 8, 64, 100) == fixed + 2 * 8 * 1 * 1 * 16 * 66 * 8
+    assert lib.ds_draft_attention_workspace_bytes(0, 32, 4, 128, 2048) == 0
+    assert lib.ds_draft_attention_workspace_bytes(4, 6, 4, 128, 2048) == 0  # 6 query heads over 4 KV heads
+
+
+def test_attention_validation_without_gpu():
+    """The attention entry point checks its arguments before any HIP call."""
+    from ds355 import _lib
+
+    lib = _lib.load()
+
+    def call(**kw):
+        args = dict(dtype=_lib.DS_BF16, rows=1, out_rows=1, num_slots=1, hq=8, hkv=2, d=128, budget=64,
+                    ws=None, ws_bytes=0, ptr=None)
+        args.update(kw)
+        p = args["ptr"]
+        return lib.ds_draft_attention(None, args["dtype"], p, 1024, 128, p, 256, 128, p, 256, 128, p, 1024, 128,
+                                      p, p, p, p, None, args["rows"], args["out_rows"], args["num_slots"],
+                                      args["hq"], args["hkv"], args["d"], args["budget"], 0.1, args["ws"],
+                                      args["ws_bytes"])
+
+    assert call(hq=6, hkv=4) == _lib.DS_ERR_INVALID
+    assert "multiple of KV heads" in lib.ds_last_error().decode()
+    assert call(rows=2, out_rows=1) == _lib.DS_ERR_INVALID
+    assert call(d=96) == _lib.DS_ERR_UNSUPPORTED
+    assert call(dtype=_lib.DS_FP32) == _lib.DS_ERR_UNSUPPORTED
+    assert call() == _lib.DS_ERR_INVALID  # null pointers
+    assert "null tensor pointer" in lib.ds_last_error().decode()
+    assert call(rows=0, out_rows=0) == _lib.DS_OK  # nothing to do, nothing launched
+
+
+def test_attention_refuses_cpu_tensors():
+    from ds355.attention import draft_linear_attention
+
+    q = torch.zeros((2, 8, 64), dtype=torch.bfloat16)
+    kv = torch.zeros((2, 2, 64), dtype=torch.bfloat16)
+    work = torch.zeros((2, 2, 32, 64), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU only"):
+        draft_linear_attention(q, kv, kv, torch.zeros_like(q), work, work.clone(), torch.zeros(2, dtype=torch.int32),
+                               [0, 1], [3, 4], scale=0.125, workspace=torch.zeros(16, dtype=torch.uint8))
+    with pytest.raises(RuntimeError, match="DiffSpec working cache exhausted"):
+        draft_linear_attention(q, kv, kv, torch.zeros_like(q), work, work.clone(), torch.zeros(2, dtype=torch.int32),
+                               [0, 1], [3, 32], scale=0.125, workspace=torch.zeros(16, dtype=torch.uint8))

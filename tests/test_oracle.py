@@ -327,3 +327,108 @@ def test_committed_query_rows(counts, graph_padding):
     assert rows == expected_rows
     assert q_index == [i * 4 + counts[i] - 1 for i in expected_rows]
     assert lengths == [seq_lens[i] - 4 + counts[i] for i in expected_rows]
+
+
+# -- linear draft attention (runtime.py:2024-2077) ----------------------------------------------
+def _attention_case(hkv, head_dim, budget, slots_total, dtype=torch.float32):
+    work_k = torch.full((slots_total, hkv, budget, head_dim), float("nan"), dtype=dtype)
+    return work_k, work_k.clone(), [0] * slots_total
+
+
+def test_draft_attention_reference_kat():
+    """The dense case of test_runtime.py:405-442 (one KV head, two query heads,
+    positions 0..2), against its softmax evaluated in closed form."""
+    work_k, work_v, lens = _attention_case(1, 2, 8, 1)
+    work_k[0, 0, :2] = torch.tensor([[1.0, 0.0], [0.0, 1.0]])
+    work_v[0, 0, :2] = torch.tensor([[2.0, 0.0], [0.0, 4.0]])
+    query = torch.tensor([[[1.0, 1.0], [1.0, -1.0]]])
+    out = torch.empty_like(query)
+    O.draft_linear_attention(query, torch.tensor([[[1.0, 1.0]]]), torch.tensor([[[6.0, 8.0]]]), 2 ** -0.5, out,
+                             work_k, work_v, lens, [0], [2])
+    expected = torch.tensor([[[3.51744921742277, 5.020939060907324], [2.8559231488782837, 2.8320802581035918]]])
+    torch.testing.assert_close(out, expected, rtol=1e-6, atol=1e-6)
+    assert lens == [3]
+    assert torch.equal(work_k[0, 0, 2], torch.tensor([1.0, 1.0]))
+    assert torch.isnan(work_k[0, 0, 3:]).all()
+
+
+def test_draft_attention_closed_forms():
+    """Position 0 returns the new value row exactly; a zero query averages the
+    values; rows past the batch are zero; NaN past each position is never read."""
+    g = torch.Generator().manual_seed(5)
+    hkv, d, budget = 2, 16, 32
+    work_k, work_v, lens = _attention_case(hkv, d, budget, 3)
+    work_k[1, :, :5] = torch.randn((hkv, 5, d), generator=g)
+    work_v[1, :, :5] = torch.randn((hkv, 5, d), generator=g)
+    query = torch.randn((4, 4 * hkv, d), generator=g)
+    query[1] = 0.0
+    key = torch.randn((4, hkv, d), generator=g)
+    value = torch.randn((4, hkv, d), generator=g)
+    out = torch.full_like(query, 7.0)
+    O.draft_linear_attention(query, key, value, 0.25, out, work_k, work_v, lens, [2, 1], [0, 5])
+    assert torch.equal(out[0], value[0].repeat_interleave(4, dim=0))
+    mean = torch.cat([work_v[1, :, :5], value[1][:, None]], dim=1).mean(dim=1)
+    torch.testing.assert_close(out[1], mean.repeat_interleave(4, dim=0), rtol=1e-6, atol=1e-6)
+    assert not torch.isnan(out).any()
+    assert out[2:].count_nonzero() == 0
+    assert lens == [0, 6, 1]
+
+
+def _planted_modulo_heads(query, key, value, scale, output, work_k, work_v, lens, slots, positions):
+    """The oracle with a plausible slip: query head h reads KV head h % Hkv."""
+    output.zero_()
+    hkv = work_k.shape[1]
+    for r, (slot, pos) in enumerate(zip(slots, positions)):
+        work_k[slot, :, pos] = key[r]
+        work_v[slot, :, pos] = value[r]
+        lens[slot] = pos + 1
+        heads = torch.arange(query.shape[1]) % hkv
+        k = work_k[slot, heads, : pos + 1].float()
+        v = work_v[slot, heads, : pos + 1].float()
+        w = torch.softmax(torch.einsum("hd,hnd->hn", query[r].float(), k) * scale, dim=-1)
+        output[r] = torch.einsum("hn,hnd->hd", w, v)
+    return output
+
+
+def test_draft_attention_group_map_is_repeat_interleave():
+    """KV head j serves query heads j*G .. j*G+G-1: with constant values per KV
+    head the output of head h is head h // G's value; the h % Hkv slip fails."""
+    hkv, group, d = 2, 3, 8
+    work_k, work_v, lens = _attention_case(hkv, d, 8, 1)
+    work_k[0, :, :3] = 0.5
+    work_v[0, 0, :3] = 1.0
+    work_v[0, 1, :3] = 2.0
+    query = torch.ones((1, hkv * group, d))
+    key = torch.full((1, hkv, d), 0.5)
+    value = torch.tensor([1.0, 2.0])[None, :, None].expand(1, hkv, d).clone()
+    out = torch.empty_like(query)
+    O.draft_linear_attention(query, key, value, 1.0, out, work_k.clone(), work_v.clone(), list(lens), [0], [3])
+    assert torch.equal(out[0, :, 0], torch.tensor([1.0, 1.0, 1.0, 2.0, 2.0, 2.0]))
+    slip = torch.empty_like(query)
+    _planted_modulo_heads(query, key, value, 1.0, slip, work_k.clone(), work_v.clone(), list(lens), [0], [3])
+    assert not torch.equal(slip[0, :, 0], out[0, :, 0])
+
+
+def test_draft_attention_matches_float64_softmax():
+    """Random GQA rows against a float64 softmax over the same prefix (bf16 output within one rounding)."""
+    g = torch.Generator().manual_seed(9)
+    hkv, group, d, budget = 2, 4, 32, 64
+    work_k, work_v, lens = _attention_case(hkv, d, budget, 4, torch.bfloat16)
+    positions, slots = [10, 0, 63], [3, 0, 2]
+    for s, p in zip(slots, positions):
+        work_k[s, :, :p] = torch.randn((hkv, p, d), generator=g).bfloat16()
+        work_v[s, :, :p] = torch.randn((hkv, p, d), generator=g).bfloat16()
+    query = torch.randn((3, hkv * group, d), generator=g).bfloat16()
+    key = torch.randn((3, hkv, d), generator=g).bfloat16()
+    value = torch.randn((3, hkv, d), generator=g).bfloat16()
+    out = torch.empty_like(query)
+    O.draft_linear_attention(query, key, value, d ** -0.5, out, work_k, work_v, lens, slots, positions)
+    for r, (s, p) in enumerate(zip(slots, positions)):
+        for h in range(hkv * group):
+            k = work_k[s, h // group, : p + 1].double()
+            v = work_v[s, h // group, : p + 1].double()
+            logits = [float(query[r, h].double() @ k[t]) * d ** -0.5 for t in range(p + 1)]
+            top = max(logits)
+            w = torch.tensor([math.exp(x - top) for x in logits], dtype=torch.float64)
+            ref = (w[:, None] * v).sum(0) / w.sum()
+            torch.testing.assert_close(out[r, h].double(), ref, rtol=8e-3, atol=1e-5)

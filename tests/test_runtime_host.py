@@ -183,3 +183,52 @@ def test_tensor_parallel_scoring_is_refused(launches):
         cache.accept_target_queries(torch.ones(1), is_prefill=False)
     with pytest.raises(ValueError, match="positive"):
         _cache(target_tensor_parallel_size=0)
+
+
+@pytest.fixture
+def attention_calls(monkeypatch):
+    from ds355 import attention
+
+    calls = []
+
+    def record(query, key, value, output, working_key, working_value, working_lens, slots, positions=None, *,
+               scale, workspace):
+        calls.append(dict(slots=slots.tolist() if isinstance(slots, torch.Tensor) else list(slots),
+                          positions=positions.tolist() if isinstance(positions, torch.Tensor) else positions,
+                          scale=scale, rows=output.shape[0]))
+        return output
+
+    monkeypatch.setattr(attention, "draft_linear_attention", record)
+    monkeypatch.setattr(attention, "attention_workspace_bytes", lambda *a: 64)
+    monkeypatch.setattr(attention, "new_attention_workspace",
+                        lambda *a: torch.zeros(64, dtype=torch.uint8))
+    return calls
+
+
+def test_draft_attention_pending_state(launches, attention_calls):
+    """Compact prefill arms the root step at the slots' working lengths
+    (runtime.py:1366-1369); later steps re-arm (runtime.py:1862-1871); the
+    pending state is consumed by one forward_attention (runtime.py:2075-2076)."""
+    cache = _cache()
+    q = torch.zeros((3, 2, 2))
+    kv = torch.zeros((3, 1, 2))
+    with pytest.raises(RuntimeError, match="called without prepared state"):
+        cache.forward_attention(q, kv, kv, 0.5, torch.zeros_like(q))
+    cache.set_active_requests(["a", "b"])
+    cache.set_active_requests(["b", "c"])  # slots 1, 0 after the reorder
+    cache.prepare_compact_prefill(None, 2, committed_seq_lens=[9, 5])
+    assert cache.has_pending_attention()
+    cache.forward_attention(q, kv, kv, 0.5, torch.zeros_like(q))
+    assert attention_calls[-1] == dict(slots=[1, 0], positions=None, scale=0.5, rows=3)
+    assert not cache.has_pending_attention()
+    cache.prepare_draft_step()
+    cache.forward_attention(q, kv, kv, 0.25, torch.zeros_like(q))
+    assert attention_calls[-1]["slots"] == [1, 0] and attention_calls[-1]["positions"] is None
+    cache._pending_request_indices = [0, 1]
+    cache._pending_local_positions = [3, 7]
+    cache.forward_attention(q, kv, kv, 0.25, torch.zeros_like(q))
+    assert attention_calls[-1]["slots"] == [0, 1] and attention_calls[-1]["positions"] == [3, 7]
+    cache._pending_request_indices = [0]
+    cache._pending_local_positions = [8]
+    with pytest.raises(RuntimeError, match="DiffSpec working cache exhausted"):
+        cache.forward_attention(q, kv, kv, 0.25, torch.zeros_like(q))

@@ -10,8 +10,9 @@ chain of ``ds355.step``; host metadata that the reference already holds as
 Python lists (query ends, verifier lengths, slots) is uploaded through a
 small ring of pinned staging buffers with non-blocking copies.
 
-Tree drafting, draft attention, raw-KV capture and the adaptive controller
-are outside this module.
+Linear draft attention over the working cache (``forward_attention``) runs
+as one launch of ``ds355.attention``.  Tree drafting, raw-KV capture and the
+adaptive controller are outside this module.
 """
 
 from __future__ import annotations
@@ -22,6 +23,7 @@ from typing import Any
 
 import torch
 
+from . import attention as _attention
 from . import step as _step
 from .plan import history_budget as _history_budget
 from .plan import plan_width as _plan_width
@@ -96,6 +98,9 @@ class _Staging:
         return self.device
 
 
+WORKING_LENS = "working_lens"  # pending positions = the slots' device working lengths
+
+
 class DiffSpecDraftCache:
     """Canonical raw KV, bounded working cache and retrieval state.
 
@@ -159,6 +164,7 @@ class DiffSpecDraftCache:
                                 dtype=torch.int64, device=self.device)
         self._rows_staging = _Staging(5, rows, self.device)
         self._plan_staging = _Staging(2, rows, self.device)
+        self._attention_staging = _Staging(2, max_num_reqs, self.device)
 
         self.retrieval_interval = settings.retrieval_interval
         self.metrics = DiffSpecRuntimeMetrics()
@@ -174,6 +180,12 @@ class DiffSpecDraftCache:
         self._target_scale = 0.0
         self.target_is_prefill = True
         self.local_positions: torch.Tensor | None = None  # root positions of the last rebuild (device)
+        # Pending linear draft attention (runtime.py:680-681): slots in row
+        # order, and per-row local positions (a host list, a device tensor, or
+        # WORKING_LENS = each slot's working length, read on the device).
+        self._pending_request_indices: list[int] | None = None
+        self._pending_local_positions: Any = None
+        self._attention_workspace: torch.Tensor | None = None
 
     # -- slots (runtime.py:755-793) --------------------------------------------------------------
     def set_active_requests(self, request_ids: list[str]) -> None:
@@ -346,7 +358,75 @@ class DiffSpecDraftCache:
             staged = self._plan_staging.upload([slots, list(seq_lens[:rows])])
         self._launch(_step.PLAN, rows, slots=staged[0, :rows], committed=staged[1, :rows])
         self.local_positions = self.plan[:rows, 1]
+        # The root token attends at its history length (runtime.py:1366-1369),
+        # which the plan launch also stored as the slot's working length.
+        self._pending_request_indices = list(slots)
+        self._pending_local_positions = WORKING_LENS
         return self.local_positions
+
+    # -- linear draft attention (runtime.py:1853-1885, 2024-2134) ---------------------------------
+    def prepare_draft_step(self, num_tokens: int | None = None) -> None:
+        """Arm the next linear draft step: every active row attends at its
+        slot's current working length (the non-root branch of runtime.py:1862-1871)."""
+        if not self._active_slots:
+            raise RuntimeError("DiffSpec request slots have not been initialized")
+        rows = len(self._active_slots) if num_tokens is None else num_tokens
+        if rows > len(self._active_slots):
+            raise RuntimeError("DiffSpec draft tensors omit active request rows")
+        self._pending_request_indices = self._active_slots[:rows]
+        self._pending_local_positions = WORKING_LENS
+
+    def has_pending_attention(self) -> bool:
+        return self._pending_request_indices is not None and self._pending_local_positions is not None
+
+    def forward_attention(
+        self,
+        query: torch.Tensor,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        scale: float,
+        output: torch.Tensor,
+    ) -> torch.Tensor:
+        """Attend each pending row over its working cache; one launch, no host sync.
+
+        Writes the new key/value at each row's local position, sets the
+        slot's working length to position + 1 and zeroes output rows past the
+        pending rows (graph padding), as runtime.py:2024-2134 does.
+        """
+        if not self.has_pending_attention():
+            raise RuntimeError("DiffSpec attention called without prepared state")
+        slots = self._pending_request_indices
+        positions = self._pending_local_positions
+        if isinstance(positions, str):
+            positions = None
+        rows = len(slots)
+        heads = query.shape[1] if query.dim() == 3 else query.shape[1] // self.head_dim
+        workspace = self._attention_workspace
+        need = _attention.attention_workspace_bytes(max(self.max_batch_rows, rows), heads, self.num_kv_heads,
+                                                    self.head_dim, self.settings.token_budget)
+        if workspace is None or workspace.numel() < need:
+            workspace = _attention.new_attention_workspace(max(self.max_batch_rows, rows), heads,
+                                                           self.num_kv_heads, self.head_dim,
+                                                           self.settings.token_budget, self.device)
+            self._attention_workspace = workspace
+        if isinstance(positions, list):
+            if len(positions) != rows:
+                raise ValueError("one local position per pending row is required")
+            if positions and max(positions) >= self.settings.token_budget:
+                raise RuntimeError("DiffSpec working cache exhausted")
+        slot_rows: Any = []
+        if rows:
+            staged = self._attention_staging.upload([list(slots), positions if isinstance(positions, list) else []])
+            slot_rows = staged[0, :rows]
+            if isinstance(positions, list):
+                positions = staged[1, :rows]
+        _attention.draft_linear_attention(
+            query, key, value, output, self.working_key, self.working_value, self.working_lens,
+            slot_rows, positions, scale=scale, workspace=workspace,
+        )
+        self._pending_request_indices = None
+        self._pending_local_positions = None
+        return output
 
     def _launch(
         self,

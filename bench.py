@@ -303,6 +303,8 @@ def run(args):
         roof_kernel, roof_bytes, roof_us = "chunk_score_kernel", score_bytes, score_us
     roof_gbps = roof_bytes / (roof_us * 1e-6) / 1e9
 
+    attention_leg = draft_attention_leg(spec, states, rows, hb, device, reps, args.seed, not args.no_cpu_baseline)
+
     cpu = None if args.no_cpu_baseline else cpu_baseline(spec, copies[0], cos_sin, hb, rows_t, active, reuse)
     if cpu is not None:
         cpu["gpu_speedup"] = round(cpu["value"] / (chain_ms * 1e3), 1)
@@ -354,9 +356,101 @@ def run(args):
         "chain": {"algorithmic_bytes": chain_bytes, "achieved_gbps": round(chain_gbps, 1),
                   "frac": round(chain_gbps / HBM_PEAK_GBPS, 4), "wall_ms_total": round(wall_ms, 3)},
         "copy_gbps": round(copy_gbps, 1),
+        "draft_attention": attention_leg,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result, ensure_ascii=False), flush=True)
+
+
+ATTENTION_COPIES = 6  # working caches rotated per launch: 6 x 67 MB exceeds the 256 MB MALL
+
+
+def draft_attention_leg(spec, states, rows, hb, device, reps, seed, with_cpu):
+    """Linear draft attention (one launch of draft_attention_kernel) over the
+    working caches the step just gathered: every row at the K draft steps'
+    local positions hb, hb + 1, ... in turn (the root token attends at the
+    history length, each draft token one further)."""
+    import torch
+
+    from ds355 import _lib, attention
+
+    hq, hkv, d, budget = spec["hq"], spec["hkv"], spec["d"], spec["budget"]
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    g = torch.Generator().manual_seed(seed + 11)
+    slots = torch.arange(rows, dtype=torch.int32, device=device)
+    positions = [torch.full((rows,), hb + s, dtype=torch.int32, device=device) for s in range(DRAFT_TOKENS)]
+    sets = []
+    for i in range(ATTENTION_COPIES):
+        st = states[i % len(states)]
+        wk = st["work_k"] if i < len(states) else st["work_k"].clone()
+        wv = st["work_v"] if i < len(states) else st["work_v"].clone()
+        q = torch.randn((rows, hq, d), generator=g).to(torch.bfloat16).to(device)
+        k = torch.randn((rows, hkv, d), generator=g).to(torch.bfloat16).to(device)
+        v = torch.randn((rows, hkv, d), generator=g).to(torch.bfloat16).to(device)
+        sets.append(dict(q=q, k=k, v=v, out=torch.empty_like(q), wk=wk, wv=wv,
+                         lens=torch.zeros((rows,), dtype=torch.int32, device=device),
+                         ws=attention.new_attention_workspace(rows, hq, hkv, d, budget, device)))
+    calls = []
+    for i in range(ATTENTION_COPIES * DRAFT_TOKENS):
+        t = sets[i % ATTENTION_COPIES]
+        calls.append((stream, _lib.DS_BF16, t["q"].data_ptr(), hq * d, d, t["k"].data_ptr(), hkv * d, d,
+                      t["v"].data_ptr(), hkv * d, d, t["out"].data_ptr(), hq * d, d, t["wk"].data_ptr(),
+                      t["wv"].data_ptr(), t["lens"].data_ptr(), slots.data_ptr(),
+                      positions[(i // ATTENTION_COPIES) % DRAFT_TOKENS].data_ptr(), rows, rows, rows, hq, hkv, d,
+                      budget, d ** -0.5, t["ws"].data_ptr(), t["ws"].numel()))
+    for c in calls:
+        _lib.check(lib.ds_draft_attention(*c))
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for i in range(reps):
+        ev[i][0].record()
+        _lib.check(lib.ds_draft_attention(*calls[i % len(calls)]))
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    avg_us = statistics.mean(a.elapsed_time(b) for a, b in ev) * 1e3
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(reps):
+        _lib.check(lib.ds_draft_attention(*calls[i % len(calls)]))
+    b.record()
+    torch.cuda.synchronize()
+    back_to_back_us = a.elapsed_time(b) * 1e3 / reps
+    status = [attention.attention_status(t["ws"]) for t in sets]
+    if any(status):
+        raise RuntimeError(f"draft attention status words {status}")
+    mean_n = hb + (DRAFT_TOKENS + 1) / 2  # positions hb .. hb + K - 1 -> lengths hb + 1 .. hb + K
+    kv_bytes = rows * mean_n * hkv * d * 2 * 2
+    io_bytes = rows * hq * d * 2 * 2 + rows * hkv * d * 2 * 2  # q in, out, new K/V rows written
+    algo = int(kv_bytes + io_bytes)
+    gbps = algo / (avg_us * 1e-6) / 1e9
+    leg = {
+        "workload": f"{rows} rows at local positions {hb}..{hb + DRAFT_TOKENS - 1} over the gathered working "
+                    f"caches [rows, {hkv}, {budget}, {d}] bf16, Hq {hq}, {ATTENTION_COPIES} rotated copies",
+        "kernel": "draft_attention_kernel",
+        "avg_us": round(avg_us, 2),
+        "back_to_back_us": round(back_to_back_us, 2),
+        "algorithmic_bytes": algo,
+        "achieved": round(gbps, 1),
+        "frac": round(gbps / HBM_PEAK_GBPS, 4),
+    }
+    if with_cpu:  # the oracle timed on the host cores, as the step's cpu_baseline is
+        from oracle import diffspec_oracle as oracle
+
+        t = sets[0]
+        cpu_q, cpu_k, cpu_v = t["q"].cpu(), t["k"].cpu(), t["v"].cpu()
+        cpu_wk, cpu_wv = t["wk"].cpu(), t["wv"].cpu()
+        out = torch.empty_like(cpu_q)
+        times = []
+        for _ in range(4):
+            lens = [0] * rows
+            started = time.perf_counter()
+            oracle.draft_linear_attention(cpu_q, cpu_k, cpu_v, d ** -0.5, out, cpu_wk, cpu_wv, lens,
+                                          list(range(rows)), [hb] * rows)
+            times.append(time.perf_counter() - started)
+        leg["cpu_oracle_us"] = round(statistics.median(times[1:]) * 1e6, 1)
+        leg["cpu_threads"] = torch.get_num_threads()
+    return leg
 
 
 def cpu_baseline(spec, inp, cos_sin, hb, rows_t, active, reuse):

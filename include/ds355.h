@@ -279,10 +279,11 @@ int ds_draft_attention(ds_stream_t stream, int dtype,
 /*
  * Workspace bytes of ds_draft_attention for up to batch_rows rows (0 when
  * an argument is not positive or Hq is not a multiple of Hkv).  No reference
- * counterpart: 256 header bytes, 4 KiB of per-row counters, 512 KiB of
- * per-(row, KV head, query block) counters, then tagged per-span partial
- * results: batch_rows x Hkv x ceil(G / 16) x ceil(token_budget / span) x 16
- * x (head_dim + 2) x 8 bytes, span = 256 tokens (128 for head_dim 256).
+ * counterpart.  With W = batch_rows x Hkv x ceil(G / 16) x
+ * ceil(token_budget / span) workgroups (span = 256 tokens, 128 for head_dim
+ * 256): 256 header bytes (word 0 the epoch, word 2 the status), W 8-byte
+ * tagged "seen" words rounded up to 256 bytes, then W x 16 x (head_dim + 2)
+ * 8-byte tagged partial results.
  */
 size_t ds_draft_attention_workspace_bytes(int batch_rows, int num_q_heads, int num_kv_heads, int head_dim,
                                           int token_budget);

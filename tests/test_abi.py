@@ -168,16 +168,20 @@ def test_step_workspace_size():
 
 
 def test_attention_workspace_size():
-    """256 header bytes, 4 KiB row counters, 512 KiB unit counters, then tagged
-    partials: rows x Hkv x ceil(G / 16) x spans x 16 x (D + 2) x 8 bytes."""
+    """256 header bytes, one 8-byte seen word per workgroup of the pending rows
+    (rows x Hkv x ceil(G / 16) x spans, rounded up to 256 bytes), then tagged
+    partials: 16 x (D + 2) x 8 bytes per workgroup."""
     from ds355 import _lib
 
     lib = _lib.load()
-    fixed = 256 + 4 * 1024 + 4 * 1024 * 128
-    assert lib.ds_draft_attention_workspace_bytes(16, 32, 4, 128, 2048) == fixed + 16 * 4 * 1 * 8 * 16 * 130 * 8
-    # G = 32 -> two query blocks; head_dim 256 -> 128-token spans; 100 tokens -> one span
-    assert lib.ds_draft_attention_workspace_bytes(3, 64, 2, 256, 2048) == fixed + 3 * 2 * 2 * 16 * 16 * 258 * 8
-    assert lib.ds_draft_attention_workspace_bytes(2, 8, 8, 64, 100) == fixed + 2 * 8 * 1 * 1 * 16 * 66 * 8
+
+    def expected(units, d):
+        return 256 + (units * 8 + 255) // 256 * 256 + units * 16 * (d + 2) * 8
+
+    assert lib.ds_draft_attention_workspace_bytes(16, 32, 4, 128, 2048) == expected(16 * 4 * 1 * 8, 128)
+    # G = 32 -> two query blocks; head_dim 256 -> 128-token spans
+    assert lib.ds_draft_attention_workspace_bytes(3, 64, 2, 256, 2048) == expected(3 * 2 * 2 * 16, 256)
+    assert lib.ds_draft_attention_workspace_bytes(2, 8, 8, 64, 100) == expected(2 * 8 * 1 * 1, 64)
     assert lib.ds_draft_attention_workspace_bytes(0, 32, 4, 128, 2048) == 0
     assert lib.ds_draft_attention_workspace_bytes(4, 6, 4, 128, 2048) == 0  # 6 query heads over 4 KV heads
 

@@ -31,19 +31,23 @@
 //                                     of query g.
 // Probabilities stay fp32 (the reference's softmax is fp32 and multiplies
 // fp32 V).  The four waves merge in LDS.  A row that fits one span writes its
-// output directly; longer rows write per-span partials (running max, sum and
-// unnormalised output), and the last span workgroup to finish merges them.
+// output directly; in a longer row every span but the last writes its
+// partial (running max, sum and unnormalised output) and exits, and the last
+// span's workgroup merges them with its own.
 //
-// Hand-over between workgroups needs no waiting on other workgroups' progress
-// and no cache flushes: partial values are stored as 64-bit words
-// (tag << 32 | fp32 bits) with device-scope stores, tag = launch epoch + 1;
-// the merging workgroup reads them with device-scope loads and re-reads any
-// word whose tag is not yet the launch's (its writer has already counted
-// itself, so the store is in flight).  The last merging workgroup advances the
-// epoch, which keeps graph replays and workspace reuse safe.  The new token's
-// K/V is read from the input rows (its working-cache slot is written by the
-// same launch), and working_lens[slot] is written by the last workgroup of
-// the row to read it, so positions may come from working_lens itself.
+// Hand-over between workgroups needs no cache flushes and no counting:
+// partial values are stored as 64-bit words (tag << 32 | fp32 bits) with
+// device-scope stores, tag = launch epoch + 1, and the merging workgroup
+// re-reads (device-scope loads) any word whose tag is not yet the launch's.
+// It only waits for workgroups of lower index (the row's earlier spans),
+// which are dispatched before it, so the wait ends whether or not the grid is
+// resident at once; it is bounded all the same.  The last merging workgroup
+// advances the epoch, which keeps graph replays and workspace reuse safe.
+// The new token's K/V is read from the input rows (its working-cache slot is
+// written by the same launch), and working_lens[slot] is written by the last
+// workgroup of the row to read it, so positions may come from working_lens
+// itself.  Waits in this kernel are LDS-only barriers and the merge's tag
+// checks: the row count and the epoch load stay in flight behind the loads.
 #include "ds355_common.h"
 
 namespace ds355 {
@@ -59,16 +63,16 @@ constexpr int kThreadsA = 256;
 constexpr int kWavesA = kThreadsA / 64;
 constexpr int kTileT = 16;        // tokens per MFMA tile
 constexpr int kGroupQ = 16;       // query heads per workgroup (MFMA N)
-constexpr int kMaxUnitsPerRow = 128;  // KV heads x query blocks
+constexpr int kGroupS = 8;      // other spans merged per round trip
 constexpr uint32_t kSpinA = 1u << 20;
 constexpr float kLog2e = 1.44269504088896340736f;
 
-// Workspace layout (bytes): header, row counters, unit counters, partials.
-enum { kHdrEpoch = 0, kHdrCombined = 1, kHdrStatus = 2 };
+// Workspace layout (bytes): a 256-byte header (epoch, status), then one
+// tagged "seen" word per workgroup of the pending rows, then the tagged
+// partials.  Past the header every word is a 64-bit (tag << 32 | value) word,
+// so a launch of another shape finds only older tags wherever it looks.
+enum { kHdrEpoch = 0, kHdrStatus = 2 };
 constexpr size_t kHeaderBytes = 256;
-constexpr size_t kRowCountOffset = kHeaderBytes;
-constexpr size_t kUnitCountOffset = kRowCountOffset + sizeof(uint32_t) * kMaxRows;
-constexpr size_t kPartialOffset = kUnitCountOffset + sizeof(uint32_t) * kMaxRows * kMaxUnitsPerRow;
 constexpr uint32_t kStatusPosition = 1;  // a row's slot or position was out of range
 constexpr uint32_t kStatusPartials = 2;  // a merge stopped waiting for a partial
 
@@ -98,8 +102,7 @@ struct AttnArgs {
   int rows, out_rows, num_slots, hq, hkv, group, qblocks, budget, splits;
   float scale;
   uint32_t* header;
-  uint32_t* row_count;
-  uint32_t* unit_count;
+  uint64_t* seen;
   uint64_t* partials;
 };
 
@@ -124,6 +127,24 @@ __device__ __forceinline__ float unpack(uint32_t w, int half) {
 }
 
 __device__ __forceinline__ u32x4 load16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// p = hi + lo in the cache dtype (16-bit words).  bf16: hi is p cut to its
+// top 16 bits (exact), lo the remainder p - hi (exact in fp32) cut the same
+// way, so |p - hi - lo| < 2^-14 |p|.  fp16: hi is p rounded to fp16, lo the
+// fp16 rounding of p - hi.
+template <int DT>
+__device__ __forceinline__ void split_prob(float p, uint32_t& hi, uint32_t& lo) {
+  if constexpr (DT == DS_BF16) {
+    const uint32_t bits = __float_as_uint(p);
+    const float h = __uint_as_float(bits & 0xffff0000u);
+    hi = bits >> 16;
+    lo = __float_as_uint(p - h) >> 16;
+  } else {
+    const _Float16 h = static_cast<_Float16>(p);
+    hi = __builtin_bit_cast(uint16_t, h);
+    lo = __builtin_bit_cast(uint16_t, static_cast<_Float16>(p - static_cast<float>(h)));
+  }
+}
 
 // J consecutive 16-bit elements (J = 4, 8 or 16) as J / 2 words.
 template <int J>
@@ -180,6 +201,27 @@ __device__ __forceinline__ void zero_heads(const AttnArgs& a, int row, int head0
   }
 }
 
+// Run by the grid's last workgroup at its end: once every workgroup of the
+// pending rows has stored its seen word (all of them have lower indices and
+// were dispatched before this one), each row's working length becomes
+// position + 1 and the epoch advances.
+__device__ __forceinline__ void publish(const AttnArgs& a, uint32_t tag) {
+  bool expired = false;
+  const int seen_words = a.rows * a.hkv * a.qblocks * a.splits;
+  for (int b = threadIdx.x; b < seen_words; b += kThreadsA) {
+    if (b != static_cast<int>(blockIdx.x)) settle(a, a.seen + b, coherent_load(a.seen + b), tag, expired);
+  }
+  lds_barrier();
+  for (int r = threadIdx.x; r < a.rows; r += kThreadsA) {
+    const int slot = a.slots[r];
+    int pos = -1;
+    if (slot >= 0 && slot < a.num_slots) pos = a.positions ? a.positions[r] : a.working_lens[slot];
+    if (pos >= 0 && pos < a.budget) a.working_lens[slot] = pos + 1;
+    else raise_status(a, kStatusPosition);
+  }
+  if (threadIdx.x == 0 && a.rows > 0) coherent_store(a.header + kHdrEpoch, tag);
+}
+
 template <int DT, int D>
 __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs a) {
   using S = AttnShape<D>;
@@ -187,9 +229,10 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
   __shared__ float s_m[kWavesA][kGroupQ];
   __shared__ float s_l[kWavesA][kGroupQ];
   __shared__ float s_acc[kWavesA - 1][kGroupQ][D + 4];
+  __shared__ float s_gm[kGroupS][kGroupQ];  // merge: other spans' max and sum
+  __shared__ float s_gl[kGroupS][kGroupQ];
   __shared__ int s_pos;
   __shared__ uint32_t s_tag;
-  __shared__ int s_last;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -206,62 +249,46 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
   const int gcount = min(kGroupQ, a.group - g0);
   const int head0 = kvh * a.group + g0;
 
-  if (row >= a.rows) {  // padding row: zero once
-    if (split == 0) zero_heads<D>(a, row, head0, gcount);
-    return;
-  }
-
-  // Thread 0 reads the row's position, then counts this workgroup as one of
-  // the row's readers; the waitcnt makes the read complete before the count,
-  // so the last reader may overwrite working_lens[slot].
-  const int slot = scalar_load(a.slots + row);
-  uint32_t row_old = 0;
+  // Thread 0 reads the launch epoch (tag = epoch + 1) and, for a pending
+  // row, the row's position (scalar loads), then stores this workgroup's
+  // tagged "seen" word.  The grid's last workgroup waits for every seen word
+  // before it advances working_lens and the epoch, so no workgroup reads
+  // either after they change.  No atomics: every word has one writer.
+  const bool real = row < a.rows;
+  const int slot = real ? scalar_load(a.slots + row) : -1;
   if (threadIdx.x == 0) {
+    const uint32_t epoch = static_cast<uint32_t>(scalar_load(reinterpret_cast<const int32_t*>(a.header + kHdrEpoch)));
     int pos = -1;
-    if (slot >= 0 && slot < a.num_slots) pos = a.positions ? a.positions[row] : a.working_lens[slot];
-    const uint32_t epoch = coherent_load(a.header + kHdrEpoch);
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    if (real && slot >= 0 && slot < a.num_slots) {
+      pos = a.positions ? scalar_load(a.positions + row) : scalar_load(a.working_lens + slot);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     s_pos = (pos >= 0 && pos < a.budget) ? pos : -1;
     s_tag = epoch + 1;
-    row_old = __hip_atomic_fetch_add(a.row_count + row, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (real) coherent_store(a.seen + blockIdx.x, tagged(epoch + 1, 0.f));
   }
-  __syncthreads();
+  lds_barrier();
   const int pos = s_pos;
   const uint32_t tag = s_tag;
   const bool valid = pos >= 0;
   const int n = valid ? pos + 1 : 0;
   const int active = valid ? (n + S::kSpan - 1) / S::kSpan : 1;
-
-  // The last of the row's workgroups to read the position publishes p + 1.
-  auto finish_row = [&]() {
-    if (threadIdx.x == 0 && row_old == static_cast<uint32_t>(a.hkv * a.qblocks * a.splits - 1)) {
-      coherent_store(a.row_count + row, 0u);
-      if (valid) a.working_lens[slot] = pos + 1;
-      else raise_status(a, kStatusPosition);
-    }
-  };
-  // Every (row, KV head, query block) has one merging workgroup; the last of
-  // them advances the epoch.
-  auto finish_unit = [&]() {
-    if (threadIdx.x == 0) {
-      const uint32_t total = static_cast<uint32_t>(a.rows * a.hkv * a.qblocks);
-      const uint32_t old = __hip_atomic_fetch_add(a.header + kHdrCombined, 1u, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-      if (old == total - 1) {
-        coherent_store(a.header + kHdrCombined, 0u);
-        coherent_store(a.header + kHdrEpoch, tag);
-      }
-    }
+  auto finish = [&]() {
+    if (blockIdx.x == gridDim.x - 1) publish(a, tag);
   };
 
+  if (!real) {  // padding row: zero once
+    if (split == 0) zero_heads<D>(a, row, head0, gcount);
+    finish();
+    return;
+  }
   if (split >= active) {
-    finish_row();
+    finish();
     return;
   }
   if (!valid) {  // bad slot or position: zero output, touch nothing else
     zero_heads<D>(a, row, head0, gcount);
-    finish_unit();
-    finish_row();
+    finish();
     return;
   }
 
@@ -271,21 +298,20 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
   const uint16_t* kin = static_cast<const uint16_t*>(a.k_in) + row * a.k_row + kvh * a.k_head;
   const uint16_t* vin = static_cast<const uint16_t*>(a.v_in) + row * a.v_row + kvh * a.v_head;
 
-  // The new token goes into the working cache (nobody reads that slot here).
-  if (qb == 0 && split == pos / S::kSpan && threadIdx.x < D / 4) {
-    const int e = threadIdx.x % (D / 8);
-    const bool is_v = threadIdx.x >= D / 8;
-    uint16_t* dst = static_cast<uint16_t*>(is_v ? a.work_v : a.work_k) + work_base + static_cast<int64_t>(pos) * D;
-    *reinterpret_cast<u32x4*>(dst + 8 * e) = load16((is_v ? vin : kin) + 8 * e);
-  }
-
   // Query block as the B operand of the score MFMAs: lane (quad, col) holds
-  // q[head0 + col][32 i + 8 quad .. + 8].
+  // q[head0 + col][32 i + 8 quad .. + 8]; columns past the group are zero.
+  // Every load of the main loop is unconditional (addresses clamped to valid
+  // rows, results masked by value), so the compiler can keep the next tile's
+  // loads in flight while the current tile is computed.
   u32x4 qv[S::kSteps];
   {
-    const uint16_t* qp = static_cast<const uint16_t*>(a.q) + row * a.q_row + (head0 + col) * a.q_head + 8 * quad;
+    const int qcol = min(col, gcount - 1);
+    const uint16_t* qp = static_cast<const uint16_t*>(a.q) + row * a.q_row + (head0 + qcol) * a.q_head + 8 * quad;
 #pragma unroll
-    for (int i = 0; i < S::kSteps; ++i) qv[i] = col < gcount ? load16(qp + 32 * i) : u32x4{0, 0, 0, 0};
+    for (int i = 0; i < S::kSteps; ++i) {
+      const u32x4 v = load16(qp + 32 * i);
+      qv[i] = col < gcount ? v : u32x4{0, 0, 0, 0};
+    }
   }
 
   f32x4 acc[J];
@@ -296,81 +322,118 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
   const int t0 = split * S::kSpan + wave * S::kTiles * kTileT;
 
   // One tile's operands: K rows for the score MFMAs, V rows for the output.
+  // Rows at or past n read row n - 1 = pos (the new token's input row): a
+  // valid, finite row whose scores are masked to -inf below.
   struct Tile {
     u32x4 k[S::kSteps];
     uint32_t v[4][J / 2];
   };
-  auto load_tile = [&](Tile& T, int tb) {
-    const int tk = tb + col;
-    const uint16_t* p = (tk == pos ? kin : kw + static_cast<int64_t>(tk) * D) + 8 * quad;
-#pragma unroll
-    for (int i = 0; i < S::kSteps; ++i) T.k[i] = tk < n ? load16(p + 32 * i) : u32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = tb + 4 * quad + r;
-      if (t < n) {
-        load_words<J>((t == pos ? vin : vw + static_cast<int64_t>(t) * D) + J * col, T.v[r]);
-      } else {
-#pragma unroll
-        for (int w = 0; w < J / 2; ++w) T.v[r][w] = 0;
-      }
-    }
+  auto row_ptr = [&](const uint16_t* work, const uint16_t* in, int t) {
+    return t >= pos ? in : work + static_cast<int64_t>(t) * D;
   };
-  auto compute_tile = [&](const Tile& T, int tb) {
-    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto load_tile = [&](Tile& T, int tb) {
+    const uint16_t* pk = row_ptr(kw, kin, tb + col) + 8 * quad;
 #pragma unroll
-    for (int i = 0; i < S::kSteps; ++i) s = mfma_scores<DT>(T.k[i], qv[i], s);
-    float x[4];
+    for (int i = 0; i < S::kSteps; ++i) T.k[i] = load16(pk + 32 * i);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = (tb + 4 * quad + i < n) ? s[i] * c : -INFINITY;
-    float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+    for (int r = 0; r < 4; ++r) load_words<J>(row_ptr(vw, vin, tb + 4 * quad + r) + J * col, T.v[r]);
+  };
+  // Scores, online softmax and output for the 32 tokens tb .. tb + 31 held in
+  // tiles T0 and T1.  The output MFMAs are 16x16x32 in the cache dtype with
+  // A = V^T and B = P^T: k-slot (lane / 16, e) is token 4 * (lane / 16) +
+  // (e & 3) of tile e / 4, i.e. the rows of the lane's own score tiles, and
+  // head_dim column m of block j is d = J * m + j, so both operands are in the
+  // lane's registers.  P is split into an upper part (its fp32 value cut to
+  // the dtype) and the dtype rounding of the exact remainder; two MFMAs per
+  // block keep the products within ~2^-16 of fp32 probabilities.
+  auto compute_pair = [&](const Tile& T0, const Tile& T1, int tb) {
+    f32x4 s0 = f32x4{0.f, 0.f, 0.f, 0.f}, s1 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < S::kSteps; ++i) {
+      s0 = mfma_scores<DT>(T0.k[i], qv[i], s0);
+      s1 = mfma_scores<DT>(T1.k[i], qv[i], s1);
+    }
+    float x[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[i] = (tb + 4 * quad + i < n) ? s0[i] * c : -INFINITY;
+      x[4 + i] = (tb + kTileT + 4 * quad + i < n) ? s1[i] * c : -INFINITY;
+    }
+    float tmax = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, 64));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
     const float mn = fmaxf(m, tmax);
     const float alpha = fast_exp2(m - mn);
-    float p[4];
+    float p[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = fast_exp2(x[i] - mn);
-    lsum = lsum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    for (int e = 0; e < 8; ++e) p[e] = fast_exp2(x[e] - mn);
+    lsum = lsum * alpha + (((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7])));
     m = mn;
 #pragma unroll
     for (int j = 0; j < J; ++j) acc[j] *= alpha;
+    u32x4 phi, plo;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int w = 0; w < 4; ++w) {
+      uint32_t h0, h1, l0, l1;
+      split_prob<DT>(p[2 * w], h0, l0);
+      split_prob<DT>(p[2 * w + 1], h1, l1);
+      phi[w] = h0 | (h1 << 16);
+      plo[w] = l0 | (l1 << 16);
+    }
 #pragma unroll
-      for (int j = 0; j < J; ++j) {
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(unpack<DT>(T.v[r][j >> 1], j & 1), p[r], acc[j], 0, 0, 0);
-      }
+    for (int j = 0; j < J; ++j) {
+      const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;  // high or low halves
+      const int w = j >> 1;
+      u32x4 av;
+      av[0] = __builtin_amdgcn_perm(T0.v[1][w], T0.v[0][w], sel);
+      av[1] = __builtin_amdgcn_perm(T0.v[3][w], T0.v[2][w], sel);
+      av[2] = __builtin_amdgcn_perm(T1.v[1][w], T1.v[0][w], sel);
+      av[3] = __builtin_amdgcn_perm(T1.v[3][w], T1.v[2][w], sel);
+      acc[j] = mfma_scores<DT>(av, phi, acc[j]);
+      acc[j] = mfma_scores<DT>(av, plo, acc[j]);
     }
   };
 
-  // Two tiles in flight: the next tile's loads are issued before the current
-  // tile is computed.
+  // All of the wave's tiles are in flight before the first pair is computed
+  // (the scheduling barrier keeps the compiler from sinking the loads next to
+  // their use); pairs wholly past n are loaded (cache hits on row pos) but
+  // not computed.
   if (t0 < n) {
-    Tile cur, nxt;
-    load_tile(cur, t0);
-#pragma unroll 1
-    for (int k = 0; k < S::kTiles; k += 2) {
-      const int tb = t0 + k * kTileT;
-      const bool more = k + 1 < S::kTiles && tb + kTileT < n;
-      if (more) load_tile(nxt, tb + kTileT);
-      compute_tile(cur, tb);
-      if (!more) break;
-      const bool more2 = k + 2 < S::kTiles && tb + 2 * kTileT < n;
-      if (more2) load_tile(cur, tb + 2 * kTileT);
-      compute_tile(nxt, tb + kTileT);
-      if (!more2) break;
+    if constexpr (S::kTiles == 4) {
+      Tile ta, tb, tc, td;
+      load_tile(ta, t0);
+      load_tile(tb, t0 + kTileT);
+      load_tile(tc, t0 + 2 * kTileT);
+      load_tile(td, t0 + 3 * kTileT);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_pair(ta, tb, t0);
+      if (t0 + 2 * kTileT < n) compute_pair(tc, td, t0 + 2 * kTileT);
+    } else {
+      Tile ta, tb;
+      load_tile(ta, t0);
+      load_tile(tb, t0 + kTileT);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_pair(ta, tb, t0);
     }
   }
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
+
+  // The new token goes into the working cache (no workgroup of this launch
+  // reads that row of the cache: rows >= pos come from the input).
+  if (qb == 0 && split == pos / S::kSpan && threadIdx.x < D / 4) {
+    const int e = threadIdx.x % (D / 8);
+    const bool is_v = threadIdx.x >= D / 8;
+    uint16_t* dst = static_cast<uint16_t*>(is_v ? a.work_v : a.work_k) + work_base + static_cast<int64_t>(pos) * D;
+    *reinterpret_cast<u32x4*>(dst + 8 * e) = load16((is_v ? vin : kin) + 8 * e);
+  }
 
   // Merge the four waves: common max, rescale, sum in wave order.
   if (quad == 0) {
     s_m[wave][col] = m;
     s_l[wave][col] = lsum;
   }
-  __syncthreads();
+  lds_barrier();
   float mx = s_m[0][col];
 #pragma unroll
   for (int w = 1; w < kWavesA; ++w) mx = fmaxf(mx, s_m[w][col]);
@@ -386,7 +449,20 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
       for (int j = 0; j < J; ++j) s_acc[wave - 1][col][d0 + J * i + j] = acc[j][i] * f;
     }
   }
-  __syncthreads();
+  lds_barrier();
+  // Wave 0 holds the span's result: unnormalised sums in acc, max mx, sum total_l.
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        float v = acc[j][i] * f;
+#pragma unroll
+        for (int ww = 0; ww < kWavesA - 1; ++ww) v += s_acc[ww][col][d0 + J * i + j];
+        acc[j][i] = v;
+      }
+    }
+  }
 
   if (active == 1) {
     if (wave == 0 && col < gcount) {
@@ -397,14 +473,8 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
         uint32_t w[J / 2];
 #pragma unroll
         for (int j = 0; j < J; j += 2) {
-          float v0 = acc[j][i] * f, v1 = acc[j + 1][i] * f;
-#pragma unroll
-          for (int ww = 0; ww < kWavesA - 1; ++ww) {
-            v0 += s_acc[ww][col][d0 + J * i + j];
-            v1 += s_acc[ww][col][d0 + J * i + j + 1];
-          }
-          w[j / 2] = static_cast<uint32_t>(Elem<DT>::store(v0 * inv)) |
-                     (static_cast<uint32_t>(Elem<DT>::store(v1 * inv)) << 16);
+          w[j / 2] = static_cast<uint32_t>(Elem<DT>::store(acc[j][i] * inv)) |
+                     (static_cast<uint32_t>(Elem<DT>::store(acc[j + 1][i] * inv)) << 16);
         }
         if constexpr (J == 4) {
           *reinterpret_cast<u32x2*>(o + J * i) = u32x2{w[0], w[1]};
@@ -416,107 +486,148 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
         }
       }
     }
-    finish_unit();
-    finish_row();
+    finish();
     return;
   }
 
-  // Several spans: publish this span's partial, the last one merges.
+  // Several spans.  Every span's result goes to LDS ([g][d] in s_acc[0], max
+  // and sum in s_m[0] / s_l[0]).  Every span but the last then publishes it
+  // as tagged words, written by all threads in address order (whole lines of
+  // device-scope writes), and is done; the last span's workgroup, which has
+  // the highest index of the row's spans, merges: it waits only for
+  // workgroups dispatched before it.
   const int unit = (row * a.hkv + kvh) * a.qblocks + qb;
   uint64_t* part_base = a.partials + static_cast<int64_t>(unit) * a.splits * kGroupQ * S::kRow;
+  lds_barrier();  // every wave is done reading s_acc
   if (wave == 0) {
-    if (col < gcount) {
-      uint64_t* pr = part_base + (static_cast<int64_t>(split) * kGroupQ + col) * S::kRow;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
-          float v = acc[j][i] * f;
-#pragma unroll
-          for (int ww = 0; ww < kWavesA - 1; ++ww) v += s_acc[ww][col][d0 + J * i + j];
-          coherent_store(pr + d0 + J * i + j, tagged(tag, v));
-        }
-      }
-      if (quad == 0) {
-        coherent_store(pr + D, tagged(tag, mx));
-        coherent_store(pr + D + 1, tagged(tag, total_l));
-      }
+      for (int j = 0; j < J; ++j) s_acc[0][col][d0 + J * i + j] = acc[j][i];
     }
-    if (lane == 0) {
-      const uint32_t old = __hip_atomic_fetch_add(a.unit_count + static_cast<int64_t>(row) * kMaxUnitsPerRow +
-                                                      kvh * a.qblocks + qb,
-                                                  1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = old == static_cast<uint32_t>(active - 1);
+    if (quad == 0) {
+      s_m[0][col] = mx;
+      s_l[0][col] = total_l;
     }
   }
-  __syncthreads();
-  if (!s_last) {
-    finish_row();
+  lds_barrier();
+  if (split < active - 1) {
+    uint64_t* pr = part_base + static_cast<int64_t>(split) * kGroupQ * S::kRow;
+    for (int w = threadIdx.x; w < gcount * S::kRow; w += kThreadsA) {
+      const int g = w / S::kRow, d = w % S::kRow;
+      const float v = d < D ? s_acc[0][g][d] : (d == D ? s_m[0][g] : s_l[0][g]);
+      coherent_store(pr + w, tagged(tag, v));
+    }
+    finish();
     return;
   }
 
-  // Merge: thread -> (query g, 4 consecutive outputs), spans in order, in
-  // groups of kGroupS spans whose words are all requested before any is used.
+  // Merge: thread -> (query g, 4 consecutive outputs), spans in index order.
+  // Per group of up to kGroupS other spans, one thread per (span, query)
+  // fetches that span's max and sum into LDS while every thread fetches its
+  // own output words, all in one round trip.
   constexpr int kChunks = D / 4;
-  constexpr int kGroupS = 4;
   bool expired = false;
-  for (int item = threadIdx.x; item < gcount * kChunks; item += kThreadsA) {
-    const int g = item / kChunks;
-    const int e = 4 * (item % kChunks);
+  const int others = active - 1;
+  const int items = gcount * kChunks;
+  for (int base = 0; base < items; base += kThreadsA) {
+    const int item = base + static_cast<int>(threadIdx.x);
+    const bool has_item = item < items;
+    const int g = has_item ? item / kChunks : 0;
+    const int e = has_item ? 4 * (item % kChunks) : 0;
     float run_m = -INFINITY, run_l = 0.f;
     float run[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < active; s0 += kGroupS) {
-      const int cnt = min(kGroupS, active - s0);
-      uint64_t wm[kGroupS], wl[kGroupS], wv[kGroupS][4];
+    for (int s0 = 0; s0 < others; s0 += kGroupS) {
+      const int cnt = min(kGroupS, others - s0);
+      const int ml = static_cast<int>(threadIdx.x);
+      const bool has_ml = ml < cnt * gcount;
+      const uint64_t* pml = part_base + (static_cast<int64_t>(s0 + ml / gcount) * kGroupQ + ml % gcount) * S::kRow;
+      const uint64_t* pi = part_base + (static_cast<int64_t>(s0) * kGroupQ + g) * S::kRow + e;
+      // Until every word of the group carries this launch's tag, all of them
+      // are requested again at once (one round trip per round).
+      uint64_t wm = 0, wl = 0;
+      uint64_t wv[kGroupS][4];
+      for (uint32_t spins = 0;; ++spins) {
+        if (spins > 0) __builtin_amdgcn_s_sleep(2);
+        if (has_ml) {
+          wm = coherent_load(pml + D);
+          wl = coherent_load(pml + D + 1);
+        }
+        if (has_item) {
 #pragma unroll
-      for (int u = 0; u < kGroupS; ++u) {
-        if (u < cnt) {
-          const uint64_t* pr = part_base + (static_cast<int64_t>(s0 + u) * kGroupQ + g) * S::kRow;
-          wm[u] = coherent_load(pr + D);
-          wl[u] = coherent_load(pr + D + 1);
+          for (int u = 0; u < kGroupS; ++u) {
 #pragma unroll
-          for (int v = 0; v < 4; ++v) wv[u][v] = coherent_load(pr + e + v);
+            for (int v = 0; v < 4; ++v) wv[u][v] = u < cnt ? coherent_load(pi + u * kGroupQ * S::kRow + v) : tagged(tag, 0.f);
+          }
+        }
+        uint32_t bad = 0u;
+        if (has_ml) bad = (static_cast<uint32_t>(wm >> 32) ^ tag) | (static_cast<uint32_t>(wl >> 32) ^ tag);
+        if (has_item) {
+#pragma unroll
+          for (int u = 0; u < kGroupS; ++u) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) bad |= static_cast<uint32_t>(wv[u][v] >> 32) ^ tag;
+          }
+        }
+        if (bad == 0u) break;
+        if (expired || spins >= kSpinA) {
+          if (!expired) raise_status(a, kStatusPartials);
+          expired = true;
+          break;
         }
       }
-      float gm = run_m;
-      float vm[kGroupS];
-#pragma unroll
-      for (int u = 0; u < kGroupS; ++u) {
-        if (u < cnt) {
-          const uint64_t* pr = part_base + (static_cast<int64_t>(s0 + u) * kGroupQ + g) * S::kRow;
-          vm[u] = settle(a, pr + D, wm[u], tag, expired);
-          gm = fmaxf(gm, vm[u]);
-        }
+      auto stale = [&](uint64_t w) { return static_cast<uint32_t>(w >> 32) != tag; };
+      auto value = [&](uint64_t w) {
+        return expired && stale(w) ? __uint_as_float(0x7fc00000u) : __uint_as_float(static_cast<uint32_t>(w));
+      };
+      if (has_ml) {
+        s_gm[ml / gcount][ml % gcount] = value(wm);
+        s_gl[ml / gcount][ml % gcount] = value(wl);
       }
-      const float rescale = fast_exp2(run_m - gm);
-      run_l *= rescale;
+      lds_barrier();
+      if (has_item) {
+        float gm = run_m;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) run[v] *= rescale;
-#pragma unroll
-      for (int u = 0; u < kGroupS; ++u) {
-        if (u < cnt) {
-          const uint64_t* pr = part_base + (static_cast<int64_t>(s0 + u) * kGroupQ + g) * S::kRow;
-          const float w = fast_exp2(vm[u] - gm);
-          run_l += settle(a, pr + D + 1, wl[u], tag, expired) * w;
-#pragma unroll
-          for (int v = 0; v < 4; ++v) run[v] += settle(a, pr + e + v, wv[u][v], tag, expired) * w;
+        for (int u = 0; u < kGroupS; ++u) {
+          if (u < cnt) gm = fmaxf(gm, s_gm[u][g]);
         }
+        const float rescale = fast_exp2(run_m - gm);
+        run_l *= rescale;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) run[v] *= rescale;
+#pragma unroll
+        for (int u = 0; u < kGroupS; ++u) {
+          if (u < cnt) {
+            const float w = fast_exp2(s_gm[u][g] - gm);
+            run_l += s_gl[u][g] * w;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) run[v] += value(wv[u][v]) * w;
+          }
+        }
+        run_m = gm;
       }
-      run_m = gm;
+      lds_barrier();  // s_gm / s_gl are refilled by the next group
     }
-    const float inv = 1.f / run_l;
-    uint16_t* o = static_cast<uint16_t*>(a.out) + row * a.o_row + (head0 + g) * a.o_head + e;
-    const uint32_t w0 = static_cast<uint32_t>(Elem<DT>::store(run[0] * inv)) |
-                        (static_cast<uint32_t>(Elem<DT>::store(run[1] * inv)) << 16);
-    const uint32_t w1 = static_cast<uint32_t>(Elem<DT>::store(run[2] * inv)) |
-                        (static_cast<uint32_t>(Elem<DT>::store(run[3] * inv)) << 16);
-    *reinterpret_cast<u32x2*>(o) = u32x2{w0, w1};
+    if (has_item) {
+      {  // the merging workgroup's own span, last in index order
+        const float om = s_m[0][g];
+        const float gm = fmaxf(run_m, om);
+        const float rescale = fast_exp2(run_m - gm);
+        const float w = fast_exp2(om - gm);
+        run_l = run_l * rescale + s_l[0][g] * w;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) run[v] = run[v] * rescale + s_acc[0][g][e + v] * w;
+      }
+      const float inv = 1.f / run_l;
+      uint16_t* o = static_cast<uint16_t*>(a.out) + row * a.o_row + (head0 + g) * a.o_head + e;
+      const uint32_t w0 = static_cast<uint32_t>(Elem<DT>::store(run[0] * inv)) |
+                          (static_cast<uint32_t>(Elem<DT>::store(run[1] * inv)) << 16);
+      const uint32_t w1 = static_cast<uint32_t>(Elem<DT>::store(run[2] * inv)) |
+                          (static_cast<uint32_t>(Elem<DT>::store(run[3] * inv)) << 16);
+      *reinterpret_cast<u32x2*>(o) = u32x2{w0, w1};
+    }
   }
-  if (threadIdx.x == 0) {
-    coherent_store(a.unit_count + static_cast<int64_t>(row) * kMaxUnitsPerRow + kvh * a.qblocks + qb, 0u);
-  }
-  finish_unit();
-  finish_row();
+  finish();
 }
 
 template <int DT, int D>
@@ -534,9 +645,9 @@ size_t attention_workspace_bytes(int rows, int num_q_heads, int num_kv_heads, in
   const int group = num_q_heads / num_kv_heads;
   const int qblocks = (group + kGroupQ - 1) / kGroupQ;
   const int splits = (token_budget + span_for(head_dim) - 1) / span_for(head_dim);
-  const size_t partial = static_cast<size_t>(rows) * num_kv_heads * qblocks * splits * kGroupQ * (head_dim + 2) *
-                         sizeof(uint64_t);
-  return kPartialOffset + partial;
+  const size_t units = static_cast<size_t>(rows) * num_kv_heads * qblocks * splits;
+  const size_t seen = (units * sizeof(uint64_t) + 255) / 256 * 256;
+  return kHeaderBytes + seen + units * kGroupQ * (head_dim + 2) * sizeof(uint64_t);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -558,8 +669,6 @@ int draft_attention_impl(hipStream_t stream, int dtype, const void* query, int64
   DS_SUPPORTED(out_rows <= kMaxRows, "at most %d output rows per launch (got %d)", kMaxRows, out_rows);
   const int group = num_q_heads / num_kv_heads;
   const int qblocks = (group + kGroupQ - 1) / kGroupQ;
-  DS_SUPPORTED(num_kv_heads * qblocks <= kMaxUnitsPerRow, "too many KV heads x query blocks (%d > %d)",
-               num_kv_heads * qblocks, kMaxUnitsPerRow);
   if (out_rows == 0) return clear_error();
   DS_REQUIRE(query && out && (rows == 0 || (key && value && working_key && working_value && working_lens && slots)),
              "null tensor pointer");
@@ -591,9 +700,10 @@ int draft_attention_impl(hipStream_t stream, int dtype, const void* query, int64
   a.scale = scale;
   char* ws = static_cast<char*>(workspace);
   a.header = reinterpret_cast<uint32_t*>(ws);
-  a.row_count = reinterpret_cast<uint32_t*>(ws + kRowCountOffset);
-  a.unit_count = reinterpret_cast<uint32_t*>(ws + kUnitCountOffset);
-  a.partials = reinterpret_cast<uint64_t*>(ws + kPartialOffset);
+  const size_t seen_bytes = (static_cast<size_t>(rows) * num_kv_heads * qblocks * a.splits * sizeof(uint64_t) + 255) /
+                            256 * 256;
+  a.seen = reinterpret_cast<uint64_t*>(ws + kHeaderBytes);
+  a.partials = reinterpret_cast<uint64_t*>(ws + kHeaderBytes + seen_bytes);
 
 #define DS_ATTN_CASE(DTV, DV) \
   if (dtype == DTV && head_dim == DV) return launch_attention<DTV, DV>(stream, a);

@@ -52,15 +52,6 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Workgroup barrier for LDS hand-offs only.  Unlike __syncthreads it does
-// not wait for this wave's outstanding global stores (the score row), which
-// other kernels read and this workgroup does not.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // Exclusive scan over the 256 threads through LDS; `total` gets the sum.
 __device__ __forceinline__ int lds_exclusive_scan(int v, int* scratch, int& total) {
   const int lane = threadIdx.x & 63;

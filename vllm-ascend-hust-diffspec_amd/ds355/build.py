@@ -2,8 +2,8 @@
 
 ``python -m ds355.build`` (or ``build()``) compiles every ``csrc/*.hip`` into
 ``ds355/libds355.so``.  The GPU code is built for gfx950 only, with fp
-contraction off (the RoPE rotate must round each product separately) and
-packed-fp32 instructions disabled.
+contraction off (the RoPE rotate must round each product separately),
+packed-fp32 instructions disabled and the wave-level atomic aggregation off.
 """
 
 from __future__ import annotations
@@ -41,6 +41,10 @@ def command(output: Path) -> list[str]:
         "-shared",
         "-ffp-contract=off",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # Keep single-lane atomics as written: the optimizer's wave-wide
+        # aggregation reads the result back at once, which stalls a wave on
+        # a device-scope round trip that the kernels hide behind their loads.
+        "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
         "-Wall",
         "-Wno-unused-function",
         "-o", str(output),

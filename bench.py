@@ -365,6 +365,13 @@ def run(args):
 ATTENTION_COPIES = 6  # working caches rotated per launch: 6 x 67 MB exceeds the 256 MB MALL
 
 
+def traffic_of(key, spec):
+    """HBM bytes per launch measured with rocprofv3 PMC counters for this workload, if recorded."""
+    name = next((k for k, v in WORKLOADS.items() if v is spec), None)
+    path = ROOT / "profiles" / f"traffic_{name}.json"
+    return json.loads(path.read_text()).get(key) if path.exists() else None
+
+
 def draft_attention_leg(spec, states, rows, hb, device, reps, seed, with_cpu):
     """Linear draft attention (one launch of draft_attention_kernel) over the
     working caches the step just gathered: every row at the K draft steps'
@@ -423,16 +430,20 @@ def draft_attention_leg(spec, states, rows, hb, device, reps, seed, with_cpu):
     kv_bytes = rows * mean_n * hkv * d * 2 * 2
     io_bytes = rows * hq * d * 2 * 2 + rows * hkv * d * 2 * 2  # q in, out, new K/V rows written
     algo = int(kv_bytes + io_bytes)
-    gbps = algo / (avg_us * 1e-6) / 1e9
+    # Back-to-back launches give the kernel's own duration (what a kernel
+    # trace reports); events around each launch add the launch latency.
+    gbps = algo / (back_to_back_us * 1e-6) / 1e9
     leg = {
         "workload": f"{rows} rows at local positions {hb}..{hb + DRAFT_TOKENS - 1} over the gathered working "
                     f"caches [rows, {hkv}, {budget}, {d}] bf16, Hq {hq}, {ATTENTION_COPIES} rotated copies",
         "kernel": "draft_attention_kernel",
-        "avg_us": round(avg_us, 2),
-        "back_to_back_us": round(back_to_back_us, 2),
+        "avg_us": round(back_to_back_us, 2),
+        "single_launch_event_us": round(avg_us, 2),
         "algorithmic_bytes": algo,
         "achieved": round(gbps, 1),
+        "peak": HBM_PEAK_GBPS,
         "frac": round(gbps / HBM_PEAK_GBPS, 4),
+        "traffic": traffic_of("attention_kernel_hbm_bytes_per_launch", spec),
     }
     if with_cpu:  # the oracle timed on the host cores, as the step's cpu_baseline is
         from oracle import diffspec_oracle as oracle

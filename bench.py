@@ -304,6 +304,7 @@ def run(args):
     roof_gbps = roof_bytes / (roof_us * 1e-6) / 1e9
 
     attention_leg = draft_attention_leg(spec, states, rows, hb, device, reps, args.seed, not args.no_cpu_baseline)
+    capture_leg = draft_capture_leg(spec, copies, states, rows, device, reps, args.seed)
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(spec, copies[0], cos_sin, hb, rows_t, active, reuse)
     if cpu is not None:
@@ -357,6 +358,7 @@ def run(args):
                   "frac": round(chain_gbps / HBM_PEAK_GBPS, 4), "wall_ms_total": round(wall_ms, 3)},
         "copy_gbps": round(copy_gbps, 1),
         "draft_attention": attention_leg,
+        "draft_capture": capture_leg,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result, ensure_ascii=False), flush=True)
@@ -462,6 +464,53 @@ def draft_attention_leg(spec, states, rows, hb, device, reps, seed, with_cpu):
         leg["cpu_oracle_us"] = round(statistics.median(times[1:]) * 1e6, 1)
         leg["cpu_threads"] = torch.get_num_threads()
     return leg
+
+
+def draft_capture_leg(spec, copies, states, rows, device, reps, seed):
+    """Raw pre-RoPE K/V capture of one draft token per row plus the RoPE input
+    (one launch of capture_kernel): each row's token at its last committed
+    position, local positions from the working lengths the step just wrote."""
+    import torch
+
+    from ds355 import _lib
+
+    hkv, d = spec["hkv"], spec["d"]
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    g = torch.Generator().manual_seed(seed + 13)
+    slots = torch.arange(rows, dtype=torch.int32, device=device)
+    rope = torch.zeros((rows * 64,), dtype=torch.int64, device=device)
+    calls = []
+    keep = []
+    for inp, st in zip(copies, states):
+        key = torch.randn((rows, hkv * d), generator=g).to(torch.bfloat16).to(device)
+        value = torch.randn((rows, hkv * d), generator=g).to(torch.bfloat16).to(device)
+        # the last committed position of each row (always inside the raw cache)
+        positions = torch.tensor([max(c - 1, 0) for c in inp["committed"][:rows]], dtype=torch.int64, device=device)
+        keep += [key, value, positions]
+        calls.append((stream, _lib.DS_BF16, key.data_ptr(), hkv * d, d, value.data_ptr(), hkv * d, d,
+                      positions.data_ptr(), 1, slots.data_ptr(), rows, inp["raw_k"].data_ptr(),
+                      inp["raw_v"].data_ptr(), inp["raw_k"].shape[0], inp["raw_k"].shape[1], hkv, d,
+                      st["working_lens"].data_ptr(), None, rope.data_ptr(), rows, rows, None))
+    for c in calls:
+        _lib.check(lib.ds_capture_raw_kv(*c))
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(reps):
+        _lib.check(lib.ds_capture_raw_kv(*calls[i % len(calls)]))
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / reps
+    moved = rows * hkv * d * 2 * 2 * 2 + rows * (4 + 8 + 4 + 8)  # K/V rows in and out; slots, positions, lens, RoPE
+    return {
+        "workload": f"{rows} rows, one draft token each, K/V [{rows}, {hkv}x{d}] bf16 into the raw caches, "
+                    f"int64 positions, local positions from working_lens",
+        "kernel": "capture_kernel",
+        "avg_us": round(us, 2),
+        "algorithmic_bytes": moved,
+        "note": "one launch per draft step; the reference builds index tensors on the host and runs torch index ops",
+    }
 
 
 def cpu_baseline(spec, inp, cos_sin, hb, rows_t, active, reuse):

@@ -288,6 +288,44 @@ int ds_draft_attention(ds_stream_t stream, int dtype,
 size_t ds_draft_attention_workspace_bytes(int batch_rows, int num_q_heads, int num_kv_heads, int head_dim,
                                           int token_budget);
 
+/*
+ * Raw pre-RoPE K/V capture of draft tokens and the graph-safe RoPE input,
+ * in one launch.
+ * Replaces DiffSpecDraftCache._write_raw (diffspec/runtime.py:1602-1618), the
+ * local positions of capture_raw_kv (diffspec/runtime.py:1797-1877) and
+ * graph_safe_rope_positions (diffspec/runtime.py:1767-1794), which the
+ * reference runs as torch index ops over index tensors built on the host
+ * (the vllm::diffspec_capture_raw_kv op, diffspec/vllm_patch.py:132-178).
+ *
+ *   token t < tokens:  raw_key[token_slots[t], positions[t], h, :] = key[t, h, :]
+ *                      raw_value likewise, every KV head h;
+ *   rope_positions[t], t < count:
+ *       working_lens given   : t < tokens ? working_lens[token_slots[t]] : 0
+ *                              (draft rows at their local positions, graph
+ *                              padding 0);
+ *       local_positions given: local_positions[t];
+ *       neither              : positions[t];
+ *   rope_positions[t] = 0 for count <= t < prev_count (the previous call's
+ *                              stale tail).
+ * positions, local_positions and rope_positions are int32, or int64 when
+ * positions_int64 != 0.  key/value rows: element (t, h, d) at
+ * t * row_stride + h * head_stride + d.  raw caches: [num_slots,
+ * max_model_len, heads, head_dim] contiguous.  dtype: DS_BF16/FP16/FP32
+ * (rows that are whole, aligned 16-byte vectors move as vectors, others
+ * element by element).
+ * A token whose slot or position is out of range is not written and sets
+ * bit 0 of *status (status may be NULL).  One launch.
+ */
+int ds_capture_raw_kv(ds_stream_t stream, int dtype,
+                      const void* key, int64_t k_row_stride, int64_t k_head_stride,
+                      const void* value, int64_t v_row_stride, int64_t v_head_stride,
+                      const void* positions, int positions_int64,
+                      const int32_t* token_slots, int tokens,
+                      void* raw_key, void* raw_value,
+                      int num_slots, int max_model_len, int heads, int head_dim,
+                      const int32_t* working_lens, const void* local_positions,
+                      void* rope_positions, int count, int prev_count, int32_t* status);
+
 #ifdef __cplusplus
 }
 #endif

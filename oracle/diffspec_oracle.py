@@ -50,6 +50,8 @@ __all__ = [
     "retrieval_rows",
     "retrieval_step",
     "draft_linear_attention",
+    "write_raw",
+    "graph_safe_rope_positions",
     "to_bf16_rne",
 ]
 
@@ -563,6 +565,46 @@ def draft_linear_attention(
     return output
 
 
+def write_raw(
+    raw_key: torch.Tensor,
+    raw_value: torch.Tensor,
+    slots: list[int],
+    positions: list[int],
+    key: torch.Tensor,
+    value: torch.Tensor,
+) -> None:
+    """Token ``t`` of ``key``/``value`` goes to ``raw[slots[t], positions[t]]``
+    (``DiffSpecDraftCache._write_raw``, diffspec/runtime.py:1602-1618), every KV
+    head at once; the rows are copies."""
+    heads, head_dim = raw_key.shape[2], raw_key.shape[3]
+    for t, (slot, pos) in enumerate(zip(slots, positions)):
+        raw_key[slot, pos] = key[t].reshape(heads, head_dim)
+        raw_value[slot, pos] = value[t].reshape(heads, head_dim)
+
+
+def graph_safe_rope_positions(
+    buffer: torch.Tensor,
+    written: int,
+    absolute_positions: torch.Tensor,
+    local_positions: torch.Tensor | None,
+) -> tuple[torch.Tensor, int]:
+    """The cache-owned RoPE input (diffspec/runtime.py:1767-1794).
+
+    ``buffer[:count]`` receives the local positions (or the absolute ones when
+    there are none) and ``buffer[count:written]``, the previous call's stale
+    prefix, is zeroed.  Returns the view, shaped like the absolute positions,
+    and the new written count.
+    """
+    count = absolute_positions.numel()
+    if count > buffer.numel():
+        raise RuntimeError("DiffSpec RoPE input exceeds its persistent buffer")
+    if count < written:
+        buffer[count:written] = 0
+    view = buffer[:count].view_as(absolute_positions)
+    view.copy_(absolute_positions if local_positions is None else local_positions)
+    return view, count
+
+
 def to_bf16_rne(x: torch.Tensor) -> torch.Tensor:
     """fp32 -> bf16 with round-to-nearest-even, done on the bit pattern.
 
@@ -597,6 +639,10 @@ PINNING = {
     "retrieval_rows": "committed-query matrix test_runtime.py:72-142 and 532-605",
     "to_bf16_rne": "equals torch's fp32->bf16 cast on random and tie-heavy inputs",
     "retrieval_step": "composition of the pinned functions above; checked against them row by row",
+    "write_raw": "value KAT of test_kv_graph_replay.py:59-73 (each step's row lands at its absolute position, "
+                 "padding tokens are never written) and the exact-copy invariant on random rows",
+    "graph_safe_rope_positions": "KATs test_kv_graph_replay.py:89-108 (dummy capture, replay, "
+                                 "counts 8, 2, 7, 1, 0, 4 against a zero-tailed buffer)",
     "draft_linear_attention": "KAT of test_runtime.py:405-442 evaluated in closed form; single position -> "
                                "the new value row; zero query -> mean of values; GQA head map h // G (planted "
                                "h % Hkv map fails); NaN past each position never read "

@@ -224,3 +224,42 @@ def test_attention_refuses_cpu_tensors():
     with pytest.raises(RuntimeError, match="DiffSpec working cache exhausted"):
         draft_linear_attention(q, kv, kv, torch.zeros_like(q), work, work.clone(), torch.zeros(2, dtype=torch.int32),
                                [0, 1], [3, 32], scale=0.125, workspace=torch.zeros(16, dtype=torch.uint8))
+
+
+def test_capture_validation_without_gpu():
+    """The capture entry point checks its arguments before any HIP call."""
+    from ds355 import _lib
+
+    lib = _lib.load()
+
+    def call(**kw):
+        args = dict(dtype=_lib.DS_BF16, tokens=1, count=1, prev=0, slots=4, lmax=16, heads=2, d=64, wl=None,
+                    local=None, rope=None)
+        args.update(kw)
+        return lib.ds_capture_raw_kv(None, args["dtype"], None, 128, 64, None, 128, 64, None, 0, None,
+                                     args["tokens"], None, None, args["slots"], args["lmax"], args["heads"],
+                                     args["d"], args["wl"], args["local"], args["rope"], args["count"], args["prev"],
+                                     None)
+
+    assert call(tokens=2, count=1) == _lib.DS_ERR_INVALID
+    assert "exceed the position count" in lib.ds_last_error().decode()
+    assert call(tokens=-1) == _lib.DS_ERR_INVALID
+    assert call(dtype=7) == _lib.DS_ERR_INVALID
+    assert call(wl=8, local=8) == _lib.DS_ERR_INVALID
+    assert "not both" in lib.ds_last_error().decode()
+    assert call() == _lib.DS_ERR_INVALID
+    assert "null tensor pointer" in lib.ds_last_error().decode()
+    assert call(tokens=0, count=0, prev=0) == _lib.DS_OK
+
+
+def test_capture_refuses_cpu_tensors():
+    from ds355.capture import capture_raw_kv_rows
+
+    raw = torch.zeros((2, 8, 1, 64), dtype=torch.bfloat16)
+    key = torch.zeros((1, 64), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU only"):
+        capture_raw_kv_rows(key, key, raw, raw.clone(), torch.zeros(1, dtype=torch.int32),
+                            torch.zeros(1, dtype=torch.int64), torch.zeros(4, dtype=torch.int64), tokens=1)
+    with pytest.raises(RuntimeError, match="exceeds its persistent buffer"):
+        capture_raw_kv_rows(key, key, raw, raw.clone(), torch.zeros(1, dtype=torch.int32),
+                            torch.zeros(5, dtype=torch.int64), torch.zeros(4, dtype=torch.int64), tokens=1)

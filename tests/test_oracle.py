@@ -432,3 +432,43 @@ def test_draft_attention_matches_float64_softmax():
             w = torch.tensor([math.exp(x - top) for x in logits], dtype=torch.float64)
             ref = (w[:, None] * v).sum(0) / w.sum()
             torch.testing.assert_close(out[r, h].double(), ref, rtol=8e-3, atol=1e-5)
+
+
+# -- raw KV capture and the RoPE input (runtime.py:1602-1618, 1767-1794) --------------------------
+@pytest.mark.parametrize("dtype", [torch.int32, torch.int64])
+def test_graph_safe_rope_positions_reference_kats(dtype):
+    """tests/test_kv_graph_replay.py:89-108: one 12-entry buffer keeps its address, the
+    replay's positions land first and every entry a previous call wrote beyond them is zero."""
+    buffer = torch.zeros(12, dtype=dtype)
+    captured, written = O.graph_safe_rope_positions(buffer, 0, torch.tensor([7, 8, 9, 10], dtype=dtype), None)
+    assert captured.tolist() == [7, 8, 9, 10]
+    replay, written = O.graph_safe_rope_positions(buffer, written, torch.tensor([7], dtype=dtype),
+                                                  torch.tensor([4], dtype=dtype))
+    assert replay.data_ptr() == captured.data_ptr()
+    assert captured.tolist() == [4, 0, 0, 0]
+    _, written = O.graph_safe_rope_positions(buffer, written, torch.tensor([7, 8, 9, 10], dtype=dtype),
+                                             torch.tensor([5, 0, 0, 0], dtype=dtype))
+    assert captured.tolist() == [5, 0, 0, 0]
+    for count in [8, 2, 7, 1, 0, 4]:
+        positions = torch.arange(count, dtype=dtype)
+        _, written = O.graph_safe_rope_positions(buffer, written, positions, positions)
+        expected = torch.zeros(12, dtype=dtype)
+        expected[:count] = positions
+        assert torch.equal(buffer, expected)
+    with pytest.raises(RuntimeError, match="exceeds its persistent buffer"):
+        O.graph_safe_rope_positions(buffer, written, torch.arange(13, dtype=dtype), None)
+
+
+def test_write_raw_reference_kat():
+    """tests/test_kv_graph_replay.py:59-73, 87: step s writes key (s+1, s+2), value +10 at
+    absolute position 5+s of the one request; the padding tokens (position 11) are never written."""
+    raw_k = torch.zeros((1, 12, 1, 2))
+    raw_v = torch.zeros((1, 12, 1, 2))
+    for step in range(3):
+        key = torch.full((4, 2), 999.0)
+        key[0] = torch.tensor([step + 1.0, step + 2.0])
+        O.write_raw(raw_k, raw_v, [0], [5 + step], key[:1], key[:1] + 10)  # active rows only
+        assert torch.equal(raw_k[0, 5 + step, 0], key[0])
+        assert torch.equal(raw_v[0, 5 + step, 0], key[0] + 10)
+    assert raw_k[0, 11].count_nonzero() == 0
+    assert raw_k[0, :5].count_nonzero() == 0 and raw_k[0, 8:].count_nonzero() == 0

@@ -18,7 +18,7 @@ DS_OK, DS_ERR_INVALID, DS_ERR_UNSUPPORTED, DS_ERR_HIP = 0, 1, 2, 3
 DS_BF16, DS_FP16, DS_FP32 = 0, 1, 2
 DS_HEAD_MEAN, DS_HEAD_MAX = 0, 1
 DS_STAGE_SCORE, DS_STAGE_SELECT, DS_STAGE_PLAN, DS_STAGE_ALL = 1, 2, 4, 7
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 EXPORTED_SYMBOLS = (
     "ds_last_error",
@@ -31,6 +31,7 @@ EXPORTED_SYMBOLS = (
     "ds_step_workspace_bytes",
     "ds_draft_attention",
     "ds_draft_attention_workspace_bytes",
+    "ds_capture_raw_kv",
 )
 
 _DTYPES = {torch.bfloat16: DS_BF16, torch.float16: DS_FP16, torch.float32: DS_FP32}
@@ -97,6 +98,10 @@ _SIGNATURES = {
         _p, _p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _p, ctypes.c_size_t,
     ]),
     "ds_draft_attention_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32, _i32, _i32]),
+    "ds_capture_raw_kv": (_i32, [
+        _p, _i32, _p, _i64, _i64, _p, _i64, _i64, _p, _i32, _p, _i32, _p, _p,
+        _i32, _i32, _i32, _i32, _p, _p, _p, _i32, _i32, _p,
+    ]),
 }
 
 _lib: ctypes.CDLL | None = None

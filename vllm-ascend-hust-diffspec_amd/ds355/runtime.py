@@ -11,8 +11,10 @@ Python lists (query ends, verifier lengths, slots) is uploaded through a
 small ring of pinned staging buffers with non-blocking copies.
 
 Linear draft attention over the working cache (``forward_attention``) runs
-as one launch of ``ds355.attention``.  Tree drafting, raw-KV capture and the
-adaptive controller are outside this module.
+as one launch of ``ds355.attention``; the raw pre-RoPE K/V capture of draft
+tokens and the graph-safe RoPE input (``capture_raw_kv``,
+``graph_safe_rope_positions``) as one launch of ``ds355.capture``.  Tree
+drafting and the adaptive controller are outside this module.
 """
 
 from __future__ import annotations
@@ -24,6 +26,7 @@ from typing import Any
 import torch
 
 from . import attention as _attention
+from . import capture as _capture
 from . import step as _step
 from .plan import history_budget as _history_budget
 from .plan import plan_width as _plan_width
@@ -186,6 +189,27 @@ class DiffSpecDraftCache:
         self._pending_request_indices: list[int] | None = None
         self._pending_local_positions: Any = None
         self._attention_workspace: torch.Tensor | None = None
+        # Draft cycle and capture state (runtime.py:677-699, 731-753, 1767-1794).
+        self._cycle_open = False
+        self._draft_step = 0
+        self._compact_prefill = False
+        self._rope_position_buffers: dict[torch.dtype, torch.Tensor] = {}
+        self._rope_position_written: dict[torch.dtype, int] = {}
+        self._capture_status = torch.zeros((1,), dtype=torch.int32, device=self.device)
+
+    # -- draft cycle (runtime.py:731-753) -----------------------------------------------------------
+    def begin_cycle(self, request_ids: list[str]) -> None:
+        self.set_active_requests(request_ids)
+        self._cycle_open = True
+        self._draft_step = 0
+        self._pending_request_indices = None
+        self._pending_local_positions = None
+
+    def end_cycle(self) -> None:
+        self._cycle_open = False
+        self._pending_request_indices = None
+        self._pending_local_positions = None
+        self._compact_prefill = False
 
     # -- slots (runtime.py:755-793) --------------------------------------------------------------
     def set_active_requests(self, request_ids: list[str]) -> None:
@@ -362,7 +386,133 @@ class DiffSpecDraftCache:
         # which the plan launch also stored as the slot's working length.
         self._pending_request_indices = list(slots)
         self._pending_local_positions = WORKING_LENS
+        self._compact_prefill = True
+        self._draft_step += 1
         return self.local_positions
+
+    # -- raw KV capture and RoPE input (runtime.py:1580-1618, 1767-1877) -------------------------
+    @staticmethod
+    def _request_indices(metadata: Any, num_tokens: int) -> list[int]:
+        """Token -> batch row from the query ends (runtime.py:1580-1594)."""
+        query_ends = getattr(metadata, "actual_seq_lengths_q", None)
+        starts = [0, *query_ends] if query_ends else metadata.query_start_loc.to("cpu").tolist()
+        rows, row = [], 0
+        for token in range(num_tokens):
+            while row + 1 < len(starts) - 1 and token >= starts[row + 1]:
+                row += 1
+            rows.append(row)
+        return rows
+
+    def _rope_buffer(self, dtype: torch.dtype) -> torch.Tensor:
+        buffer = self._rope_position_buffers.get(dtype)
+        if buffer is None:
+            buffer = torch.zeros((self.max_num_reqs * self.max_model_len,), dtype=dtype, device=self.device)
+            self._rope_position_buffers[dtype] = buffer
+        return buffer
+
+    def capture_status(self) -> int:
+        """Bit 0: a captured token's slot or absolute position was out of range (reads the device)."""
+        return int(self._capture_status.item())
+
+    def capture_raw_kv(
+        self,
+        layer_index: int,
+        absolute_positions: torch.Tensor,
+        key: torch.Tensor,
+        value: torch.Tensor,
+        metadata: Any = None,
+    ) -> torch.Tensor | None:
+        """Write the draft tokens' pre-RoPE K/V to the raw cache and, inside a
+        draft cycle, arm the next attention and return the RoPE input.
+
+        Linear drafting path of runtime.py:1797-1877: inside a cycle the rows
+        are the active requests (graph padding beyond them is neither written
+        nor given a position), their local positions are the slots' working
+        lengths (the rebuilt history length for the root token) and the
+        result is the cache-owned RoPE input that graph_safe_rope_positions
+        would return, written by the same launch.  Outside a cycle every token
+        goes to its request's slot (rows from ``metadata``'s query ends) and
+        None is returned, as in the reference.  The "working cache exhausted"
+        check the reference makes on host positions happens on the device
+        (the attention's status word), since the positions never reach the
+        host here.
+        """
+        if layer_index != 0:
+            raise ValueError("DiffSpec draft cache only supports one layer")
+        if not self._active_slots:
+            raise RuntimeError("DiffSpec request slots have not been initialized")
+        num_tokens = key.shape[0]
+        prepared_root = self._compact_prefill
+        if self._cycle_open:
+            num_tokens = len(self._active_slots)
+            if key.shape[0] < num_tokens or absolute_positions.numel() < num_tokens:
+                raise RuntimeError("DiffSpec draft tensors omit active request rows")
+            slots = self._active_slots[:num_tokens]
+        else:
+            if metadata is None:
+                return None
+            slots = [self._active_slots[r] for r in self._request_indices(metadata, num_tokens)]
+        if prepared_root:
+            self._compact_prefill = False
+        if self._cycle_open and not prepared_root and self._draft_step == 0:
+            # First draft step without a prepared root: rebuild first
+            # (runtime.py:1857-1861); the plan leaves the root positions in
+            # working_lens.
+            seq_lens = list(getattr(metadata, "seq_lens_list", ())) if metadata is not None else []
+            if not seq_lens:
+                return None
+            self.prepare_compact_prefill(metadata, num_tokens, committed_seq_lens=seq_lens)
+            self._compact_prefill = False
+            self._draft_step -= 1
+        staged = self._attention_staging.upload([slots, []]) if len(slots) <= self.max_num_reqs else None
+        token_slots = staged[0, : len(slots)] if staged is not None else torch.tensor(
+            slots, dtype=torch.int32, device=self.device)
+        dtype = absolute_positions.dtype
+        buffer = self._rope_buffer(dtype)
+        prev = self._rope_position_written.get(dtype, 0)
+        if self._cycle_open:
+            rope = _capture.capture_raw_kv_rows(
+                key, value, self.raw_key, self.raw_value, token_slots, absolute_positions, buffer,
+                tokens=num_tokens, working_lens=self.working_lens, prev_count=prev, status=self._capture_status)
+            self._rope_position_written[dtype] = absolute_positions.numel()
+            self._pending_request_indices = list(slots)
+            self._pending_local_positions = WORKING_LENS
+            self._draft_step += 1
+            return rope
+        _capture.capture_raw_kv_rows(
+            key, value, self.raw_key, self.raw_value, token_slots, absolute_positions[:num_tokens].contiguous(),
+            buffer, tokens=num_tokens, prev_count=0, status=self._capture_status)
+        # The launch wrote absolute positions into the RoPE buffer; its extent
+        # is what graph_safe_rope_positions must clear next.
+        self._rope_position_written[dtype] = max(prev, num_tokens)
+        return None
+
+    def graph_safe_rope_positions(
+        self, absolute_positions: torch.Tensor, local_positions: torch.Tensor | None,
+    ) -> torch.Tensor:
+        """Cache-owned, stable RoPE input (runtime.py:1767-1794).
+
+        The view capture_raw_kv returns is already this buffer and is returned
+        as is; otherwise one launch copies the positions and zeroes the
+        previous call's stale tail.
+        """
+        dtype = absolute_positions.dtype
+        buffer = self._rope_buffer(dtype)
+        count = absolute_positions.numel()
+        if count > buffer.numel():
+            raise RuntimeError("DiffSpec RoPE input exceeds its persistent buffer")
+        if (local_positions is not None and local_positions.data_ptr() == buffer.data_ptr()
+                and local_positions.numel() == count and self._rope_position_written.get(dtype, 0) == count):
+            return local_positions.view(absolute_positions.shape)
+        prev = self._rope_position_written.get(dtype, 0)
+        local = None if local_positions is None else local_positions.to(dtype).contiguous()
+        empty = self.raw_key.new_empty((0, self.num_kv_heads, self.head_dim))
+        rope = _capture.capture_raw_kv_rows(
+            empty, empty, self.raw_key, self.raw_value,
+            torch.empty((0,), dtype=torch.int32, device=self.device), absolute_positions.contiguous(), buffer,
+            tokens=0, local_positions=local, prev_count=prev)
+        self._rope_position_written[dtype] = count
+        return rope
 
     # -- linear draft attention (runtime.py:1853-1885, 2024-2134) ---------------------------------
     def prepare_draft_step(self, num_tokens: int | None = None) -> None:

@@ -303,6 +303,55 @@ def run(args):
         roof_kernel, roof_bytes, roof_us = "chunk_score_kernel", score_bytes, score_us
     roof_gbps = roof_bytes / (roof_us * 1e-6) / 1e9
 
+    # Scoring without a supplied LSE: the same pass keeps (max, sum) pairs and
+    # a second small kernel merges them; such a step always runs the chain.
+    free_descs = []
+    for inp, st in zip(copies, states):
+        st["lse_partials"] = torch.zeros((total_rows, spec["hq"], max_chunks, 2), dtype=torch.float32, device=device)
+        st["lse_out"] = torch.zeros((total_rows, spec["hq"]), dtype=torch.float32, device=device)
+        desc, _ = step.build_step_desc(
+            snapshot=step.VerifierSnapshot(inp["query"], None, inp["key_cache"], inp["table"], inp["scale"]),
+            rows=step.VerifierRows(rows_t["counts"], rows_t["starts"], rows_t["qlens"], rows_t["tlens"], rows),
+            scores=st["scores"], score_partials=st["partials"], sel_ids=st["sel_ids"], sel_count=st["sel_count"],
+            slots=rows_t["slots"], committed_lens=rows_t["committed"], plan=st["plan"],
+            working_lens=st["working_lens"], raw_key=inp["raw_k"], raw_value=inp["raw_v"], working_key=st["work_k"],
+            working_value=st["work_v"], cos_sin_cache=cos_sin, rotary_dim=d, is_neox_style=True, chunk_size=chunk,
+            history_budget=hb, recent_window=spec.get("window", RECENT_WINDOW), row_active=row_active,
+            lse_partials=st["lse_partials"], lse_out=st["lse_out"],
+        )
+        free_descs.append(desc)
+
+    def time_free(stages, reps):
+        def go(i):
+            desc = free_descs[i % len(free_descs)]
+            desc.stages = stages
+            _lib.check(lib.ds_retrieval_step(stream, desc))
+        for i in range(3):
+            go(i)
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for i in range(reps):
+            ev[i][0].record()
+            go(i)
+            ev[i][1].record()
+        torch.cuda.synchronize()
+        return statistics.mean(a.elapsed_time(b) for a, b in ev) * 1e3  # µs
+
+    free_score_us = time_free(step.SCORE, reps)
+    free_step_us = time_free(step.ALL, reps)
+    free_gbps = score_bytes / (free_score_us * 1e-6) / 1e9
+    lse_free_leg = {
+        "what": "scores without a supplied softmax LSE: chunk_score_kernel keeps (max, sum) pairs, "
+                "lse_finalize_kernel merges them into each head's LSE and the per-KV-head partials",
+        "score_us": round(free_score_us, 2), "step_us": round(free_step_us, 2),
+        "score_us_with_lse": round(score_us, 2),
+        "achieved_gbps": round(free_gbps, 1), "frac": round(free_gbps / HBM_PEAK_GBPS, 4),
+        "algorithmic_bytes": score_bytes,
+    }
+    del free_descs
+    for st in states:
+        del st["lse_partials"], st["lse_out"]
+
     attention_leg = draft_attention_leg(spec, states, rows, hb, device, reps, args.seed, not args.no_cpu_baseline)
     capture_leg = draft_capture_leg(spec, copies, states, rows, device, reps, args.seed)
 
@@ -357,6 +406,7 @@ def run(args):
         "chain": {"algorithmic_bytes": chain_bytes, "achieved_gbps": round(chain_gbps, 1),
                   "frac": round(chain_gbps / HBM_PEAK_GBPS, 4), "wall_ms_total": round(wall_ms, 3)},
         "copy_gbps": round(copy_gbps, 1),
+        "lse_free_scoring": lse_free_leg,
         "draft_attention": attention_leg,
         "draft_capture": capture_leg,
         "cpu_baseline": cpu,

@@ -56,13 +56,19 @@ int ds_abi_version(void);
  * chunk) are written as 0, as the reference does.
  *
  * query   : [batch, Hq, head_dim], token stride q_stride, head stride head_dim.
- * lse     : fp32, element (b, h) at lse[b * lse_row_stride + h * lse_head_stride].
+ * lse     : fp32, element (b, h) at lse[b * lse_row_stride + h * lse_head_stride];
+ *           NULL computes it: each query head's logsumexp over the row's
+ *           scored tokens, in the same pass over the keys (the reference's
+ *           chunk_attention_scores with softmax_lse=None,
+ *           diffspec/runtime.py:321-322); head mean only.
  * key_cache: element (block, i, kvh, d) at
  *            k[block * k_block_stride + i * k_token_stride + kvh * k_head_stride + d].
  * dtype   : DS_BF16 or DS_FP16 (query and key_cache share it).
  * workspace: caller-owned device scratch of batch * max_chunks * Hkv floats
- *           (per-KV-head partial sums; unused with DS_HEAD_MAX).  Two
- *           kernels: the streaming pass and a small finalize pass.
+ *           (per-KV-head partial sums; unused with DS_HEAD_MAX), plus
+ *           batch * max_chunks * Hq * 2 floats when lse is NULL.  Two
+ *           kernels (three without an LSE): the streaming pass, the LSE
+ *           merge and a small finalize pass.
  * Limits  : head_dim % 32 == 0 and <= 256, Hq % Hkv == 0, Hq / Hkv <= 16,
  *           batch <= 1024; DS_HEAD_MAX needs chunk <= 128 or a chunk that
  *           divides 64.
@@ -210,6 +216,12 @@ typedef struct ds_step_desc {
    * 64-byte aligned; NULL runs the kernel chain */
   void* workspace;
   size_t workspace_bytes;
+  /* scoring without a supplied LSE (lse == NULL): the pass computes each
+   * query head's LSE over the row's scored tokens (the reference's
+   * chunk_attention_scores with softmax_lse=None, diffspec/runtime.py:321-322) */
+  float* lse_partials;               /* [batch_rows, Hq, max_chunks, 2] fp32 scratch; required when lse == NULL */
+  float* lse_out;                    /* [batch_rows, Hq] natural-log LSE of each scored row, or NULL */
+  int64_t lse_out_stride;            /* elements between rows of lse_out */
 } ds_step_desc;
 
 int ds_retrieval_step(ds_stream_t stream, const ds_step_desc* desc);

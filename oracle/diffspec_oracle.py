@@ -140,7 +140,7 @@ def chunk_attention_scores(
 def paged_chunk_attention_scores(
     query: torch.Tensor,
     key_cache: torch.Tensor,
-    softmax_lse: torch.Tensor,
+    softmax_lse: torch.Tensor | None,
     block_table: torch.Tensor,
     seq_lens: torch.Tensor,
     *,
@@ -156,11 +156,12 @@ def paged_chunk_attention_scores(
     the output is ``[B, ceil(max_seq_len / chunk)]`` fp32 and chunks beyond a
     row's length are 0 (``valid_count = 0`` -> ``0 / max(0, 1)``,
     kernels.py:80-82).  The maths per row is ``chunk_attention_scores`` with
-    the supplied LSE.
+    the supplied LSE, or, for ``softmax_lse=None``, with each head's
+    ``logsumexp`` over the row's own tokens (runtime.py:321-322).
     """
     batch, num_query_heads, head_dim = query.shape
     _, block_size, num_kv_heads, _ = key_cache.shape
-    lse = softmax_lse.float().reshape(batch, num_query_heads)
+    lse = None if softmax_lse is None else softmax_lse.float().reshape(batch, num_query_heads)
     max_chunks = (max_seq_len + chunk_size - 1) // chunk_size
     out = torch.zeros((batch, max_chunks), dtype=torch.float32)
     for b in range(batch):
@@ -171,7 +172,7 @@ def paged_chunk_attention_scores(
         table = block_table[b, :pages].long()
         dense = key_cache[table].reshape(-1, num_kv_heads, head_dim)[:length]
         row = chunk_attention_scores(
-            query[b], dense, chunk_size, softmax_lse=lse[b], scale=scale,
+            query[b], dense, chunk_size, softmax_lse=None if lse is None else lse[b], scale=scale,
             head_reduce=head_reduce,
         )
         out[b, : row.numel()] = row
@@ -465,7 +466,7 @@ def retrieval_rows(
 
 def retrieval_step(
     query: torch.Tensor,
-    lse: torch.Tensor,
+    lse: torch.Tensor | None,
     key_cache: torch.Tensor,
     block_table: torch.Tensor,
     seq_lens: list[int],
@@ -625,7 +626,8 @@ PINNING = {
     "chunk_attention_scores": "dense softmax formulation test_runtime.py:270-298; zero-K -> 1/L "
                               "(test_retrieval_dynamic_npu.py:39-42); planted missing partial-chunk divide",
     "paged_chunk_attention_scores": "dense GQA softmax reference with reordered pages "
-                                    "(test_retrieval_npu.py:36-85); zero tail beyond a row",
+                                    "(test_retrieval_npu.py:36-85), with a supplied LSE and without one "
+                                    "(test_runtime.py:270-298); zero tail beyond a row",
     "select_context_chunks": "KATs test_runtime.py:301-310, 41-69, 532-605; brute force over subsets; "
                              "torch.topk on tie-free inputs",
     "history_indices": "KATs test_runtime.py:616-634, 781-799",

@@ -110,6 +110,75 @@ def test_c_side_validation_reports_reference_messages():
     assert "unknown stage bits" in lib.ds_last_error().decode()
 
 
+def test_lse_free_validation_without_gpu():
+    """Scoring without an LSE: workspace sizing, the head-mean restriction and the step's pair buffer.
+
+    The pointers are placeholders: every call fails its argument checks before
+    any HIP call or launch.
+    """
+    from ds355 import _lib
+
+    lib = _lib.load()
+    fake = 1 << 12  # 16-byte aligned, never dereferenced
+    # batch 2, Hq 8, Hkv 2, 3 chunks: (2 + 2 * 8) floats per (row, chunk).
+    need = 2 * 3 * (2 + 2 * 8) * 4
+    args = [None, _lib.DS_BF16, fake, 8 * 128, fake, 16 * 2 * 128, 2 * 128, 128, None, 0, 0, fake, 4, fake,
+            2, 8, 2, 128, 16, 64, 3, 1.0, _lib.DS_HEAD_MEAN, fake, 3]
+    rc = lib.ds_chunk_scores(*args, fake, 2 * 3 * 2 * 4)  # room for the partials only
+    assert rc == _lib.DS_ERR_INVALID
+    assert lib.ds_last_error().decode() == (
+        f"workspace too small: need {need} bytes without an LSE (batch * max_chunks * (kv_heads + 2 * q_heads) * 4)")
+    args[22] = _lib.DS_HEAD_MAX
+    assert lib.ds_chunk_scores(*args, fake, need) == _lib.DS_ERR_UNSUPPORTED
+    assert lib.ds_last_error().decode() == "head_reduce=max needs a supplied softmax LSE"
+
+    desc = _lib.StepDesc()
+    desc.stages = _lib.DS_STAGE_SCORE
+    desc.batch_rows = desc.batch_size = 1
+    desc.chunk_size, desc.history_budget, desc.token_budget = 64, 128, 256
+    desc.plan_width, desc.sel_stride = 5 + 4, 4
+    desc.counts = desc.query_start = desc.query_len = desc.target_len = fake
+    desc.max_chunks, desc.scores, desc.score_partials = 4, fake, fake
+    desc.num_kv_heads, desc.num_q_heads = 2, 8
+    assert lib.ds_retrieval_step(None, desc) == _lib.DS_ERR_INVALID
+    assert lib.ds_last_error().decode() == (
+        "without a softmax LSE the step needs lse_partials ([batch_rows, Hq, max_chunks, 2] fp32)")
+
+
+def test_lse_free_host_checks():
+    """The Python wrappers refuse the LSE-free variant where it is not defined."""
+    from ds355 import step
+    from ds355.kernels import paged_chunk_attention_scores
+
+    q = torch.zeros((1, 4, 32), dtype=torch.bfloat16)
+    k = torch.zeros((2, 16, 1, 32), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="needs a supplied softmax_lse"):
+        paged_chunk_attention_scores(q, k, None, torch.zeros((1, 2), dtype=torch.int32),
+                                     torch.ones(1, dtype=torch.int32), chunk_size=4, max_seq_len=4, scale=1.0,
+                                     head_reduce="max")
+    with pytest.raises(ValueError, match="GPU only"):
+        paged_chunk_attention_scores(q, k, None, torch.zeros((1, 2), dtype=torch.int32),
+                                     torch.ones(1, dtype=torch.int32), chunk_size=4, max_seq_len=4, scale=1.0)
+    i32 = lambda *s: torch.zeros(s, dtype=torch.int32)  # noqa: E731
+    raw = torch.zeros((2, 64, 1, 32), dtype=torch.bfloat16)
+    work = torch.zeros((2, 1, 32, 32), dtype=torch.bfloat16)
+    common = dict(
+        snapshot=step.VerifierSnapshot(q, None, k, i32(1, 2), 1.0),
+        rows=step.VerifierRows(i32(1), i32(1), i32(1), i32(1), 1),
+        scores=torch.zeros((1, 4)), score_partials=torch.zeros((1, 4, 1)), sel_ids=i32(2, 4), sel_count=i32(2),
+        slots=i32(1), committed_lens=i32(1), plan=torch.zeros((1, 9), dtype=torch.int64), working_lens=None,
+        raw_key=raw, raw_value=raw, working_key=work, working_value=work,
+        cos_sin_cache=torch.zeros((64, 32), dtype=torch.bfloat16), rotary_dim=32, is_neox_style=True,
+        chunk_size=4, history_budget=16,
+    )
+    with pytest.raises(ValueError, match="lse_partials must be a contiguous fp32"):
+        step.build_step_desc(**common)
+    with pytest.raises(ValueError, match="lse_out must be fp32"):
+        step.build_step_desc(**common, lse_partials=torch.zeros((1, 4, 4, 2)), lse_out=torch.zeros((1, 3)))
+    with pytest.raises(ValueError, match="GPU only"):
+        step.build_step_desc(**common, lse_partials=torch.zeros((1, 4, 4, 2)), lse_out=torch.zeros((1, 4)))
+
+
 def test_no_cpu_fallback():
     """Every product entry point refuses CPU tensors instead of computing on the host."""
     from ds355.compact_kv import rebuild_compact_kv_from_plan

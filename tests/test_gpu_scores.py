@@ -3,7 +3,10 @@
 Mirrors the reference's device tests (tests/test_retrieval_npu.py:36-85 and
 tests/test_retrieval_dynamic_npu.py:15-45): a dense GQA softmax reference with
 reordered pages and partial chunks (rtol 1e-3, atol 1e-6), and zero keys,
-whose uniform softmax gives exactly 1/L per chunk.
+whose uniform softmax gives exactly 1/L per chunk.  Without a supplied LSE
+(softmax_lse=None, the reference's chunk_attention_scores default,
+diffspec/runtime.py:321-322) the same checks run against the oracle's
+per-row logsumexp.
 """
 
 import pytest
@@ -18,7 +21,7 @@ def _gpu_scores(query, key_cache, lse, table, lengths, chunk, scale, device, hea
     from ds355.kernels import paged_chunk_attention_scores
 
     return paged_chunk_attention_scores(
-        query.to(device), key_cache.to(device), lse.to(device), table.to(device),
+        query.to(device), key_cache.to(device), None if lse is None else lse.to(device), table.to(device),
         torch.tensor(lengths, dtype=torch.int32, device=device),
         chunk_size=chunk, max_seq_len=max(lengths), scale=scale, head_reduce=head_reduce,
     ).cpu()
@@ -134,3 +137,68 @@ def test_reference_validation_messages(cuda):
                                      scale=1.0)
     with pytest.raises(ValueError, match=r"query must have shape"):
         paged_chunk_attention_scores(q[0], k, torch.zeros(8, device=cuda), bt, sl, chunk_size=4, max_seq_len=4, scale=1.0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim,chunk,block_size", [(128, 64, 128), (64, 32, 16), (128, 128, 256), (96, 48, 64),
+                                                       (256, 16, 1024)])
+@pytest.mark.parametrize("hq,hkv", [(32, 4), (12, 2), (16, 1)])
+def test_lse_free_ragged_batch_matches_oracle(cuda, dtype, head_dim, chunk, block_size, hq, hkv):
+    g = gen(11)
+    lengths = uniform_lengths(7, 1, 5000, g) + [0, 1, chunk, chunk + 1]
+    query = randn((len(lengths), hq, head_dim), dtype, g)
+    key_cache, table = paged_keys(lengths, hkv, head_dim, block_size, dtype, g)
+    scale = default_scale(head_dim)
+    actual = _gpu_scores(query, key_cache, None, table, lengths, chunk, scale, cuda)
+    expected = O.paged_chunk_attention_scores(query, key_cache, None, table, torch.tensor(lengths), chunk_size=chunk,
+                                              max_seq_len=max(lengths), scale=scale)
+    torch.testing.assert_close(actual, expected, rtol=1e-3, atol=1e-6)
+    # The same scores as with the exact LSE supplied.
+    lse = lse_for(query, key_cache, table, lengths, scale)
+    supplied = _gpu_scores(query, key_cache, lse, table, lengths, chunk, scale, cuda)
+    torch.testing.assert_close(actual, supplied, rtol=1e-3, atol=1e-6)
+
+
+def test_lse_free_zero_keys_give_uniform_mass(cuda):
+    query = torch.ones((2, 4, 256), dtype=torch.bfloat16)
+    keys = torch.zeros((9, 1024, 1, 256), dtype=torch.bfloat16)
+    table = torch.tensor([[4, 1, 7], [8, 2, 5]], dtype=torch.int32)
+    for chunks in [1, 9, 64, 192]:
+        lengths = [16 * chunks - 3, min(100, 16 * chunks - 3)]
+        actual = _gpu_scores(query, keys, None, table, lengths, 16, 256 ** -0.5, cuda)
+        expected = torch.zeros((2, chunks))
+        for row, length in enumerate(lengths):
+            expected[row, : (length + 15) // 16] = 1.0 / length
+        torch.testing.assert_close(actual, expected, rtol=1e-3, atol=1e-6)
+
+
+def test_lse_free_large_logits_stay_finite(cuda):
+    """Logits in the hundreds: the running max keeps every 2^(x - m) in range."""
+    g = gen(12)
+    lengths = [4000, 333, 64]
+    query = (randn((3, 32, 128), torch.bfloat16, g).float() * 4).to(torch.bfloat16)
+    key_cache, table = paged_keys(lengths, 4, 128, 64, torch.bfloat16, g)
+    scale = 1.0
+    actual = _gpu_scores(query, key_cache, None, table, lengths, 64, scale, cuda)
+    assert torch.isfinite(actual).all()
+    expected = O.paged_chunk_attention_scores(query, key_cache, None, table, torch.tensor(lengths), chunk_size=64,
+                                              max_seq_len=max(lengths), scale=scale)
+    torch.testing.assert_close(actual, expected, rtol=1e-3, atol=1e-6)
+
+
+def test_lse_free_headline_shape_scores(cuda):
+    """16 requests, L ~ U[4096, 40960], 32 q heads / 4 KV heads x 128, chunk 64, no LSE."""
+    g = gen(0)
+    lengths = uniform_lengths(16, 4096, 40960, g)
+    query = randn((16, 32, 128), torch.bfloat16, g)
+    key_cache, table = paged_keys(lengths, 4, 128, 128, torch.bfloat16, g)
+    scale = default_scale(128)
+    actual = _gpu_scores(query, key_cache, None, table, lengths, 64, scale, cuda)
+    expected = O.paged_chunk_attention_scores(query, key_cache, None, table, torch.tensor(lengths), chunk_size=64,
+                                              max_seq_len=max(lengths), scale=scale)
+    torch.testing.assert_close(actual, expected, rtol=1e-3, atol=1e-6)
+    for b, n in enumerate(lengths):
+        c = (n + 63) // 64
+        sizes = torch.full((c,), 64.0)
+        sizes[-1] = n - (c - 1) * 64
+        assert abs(float((actual[b, :c].double() * sizes.double()).sum()) - 1.0) < 2e-3

@@ -58,7 +58,8 @@ def path(request):
     return request.param
 
 
-def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="chain", single_launch=None):
+def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="chain", single_launch=None,
+            lse_free=False):
     from ds355 import step
 
     i32 = lambda xs: torch.tensor(xs, dtype=torch.int32, device=device)  # noqa: E731
@@ -80,6 +81,9 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="cha
             table=case["table"].to(device), cos_sin=case["cos_sin"].to(device),
         )
         state["work_v"] = torch.full_like(state["work_k"], float("nan"))
+    if lse_free and "lse_partials" not in state:
+        state["lse_partials"] = torch.zeros((rows, case["hq"], max_chunks, 2), dtype=torch.float32, device=device)
+        state["lse_out"] = torch.full((rows, case["hq"]), float("nan"), dtype=torch.float32, device=device)
     fused = path == "fused" and (stages is None or stages == step.ALL)
     if fused and "workspace" not in state:
         state["workspace"] = step.new_workspace(rows, state["scores"].shape[1], case["hkv"], case["token_budget"],
@@ -87,8 +91,8 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="cha
     epoch = step.workspace_epoch(state["workspace"]) if fused else None
     step.retrieval_step(
         stages=step.ALL if stages is None else stages,
-        snapshot=step.VerifierSnapshot(state["query"], state["lse"], state["key_cache"], state["table"],
-                                       case["scale"]),
+        snapshot=step.VerifierSnapshot(state["query"], None if lse_free else state["lse"], state["key_cache"],
+                                       state["table"], case["scale"]),
         rows=step.VerifierRows(i32(case["counts"]), i32(case["starts"]), i32(case["qlens"]), i32(case["tlens"]),
                                case["real_rows"]),
         scores=state["scores"], score_partials=state["partials"], sel_ids=state["sel_ids"], sel_count=state["sel_count"], slots=i32(case["slots"]),
@@ -98,11 +102,14 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="cha
         is_neox_style=case["neox"], chunk_size=case["chunk"], history_budget=case["budget"],
         row_active=None if row_active is None else i32(row_active),
         workspace=state.get("workspace") if fused else None,
+        lse_partials=state.get("lse_partials") if lse_free else None,
+        lse_out=state.get("lse_out") if lse_free else None,
     )
     torch.cuda.synchronize()
     if fused:  # the single launch ran (epoch + 1) or, for other shapes, the chain did
         if single_launch is None:
-            single_launch = rows >= 8  # batches of fewer rows run the chain
+            # Batches of fewer rows, and steps without a supplied LSE, run the chain.
+            single_launch = rows >= 8 and not lse_free
         assert step.workspace_epoch(state["workspace"]) == epoch + (1 if single_launch else 0)
         assert step.workspace_status(state["workspace"]) == 0
     return state
@@ -251,3 +258,26 @@ def test_stage_split_equals_full_chain(cuda, path):
     run_gpu(case, cuda, stages=step.PLAN, state=split)
     for key in ("scores", "sel_ids", "sel_count", "plan", "working_lens", "work_k", "work_v"):
         assert torch.equal(torch.nan_to_num(split[key]), torch.nan_to_num(full[key])), key
+
+
+@pytest.mark.parametrize("seed,hq,hkv,head_dim,chunk,block_size", [(4, 32, 4, 128, 64, 128), (6, 16, 2, 64, 32, 64)])
+def test_lse_free_step_equals_supplied_lse(cuda, path, seed, hq, hkv, head_dim, chunk, block_size):
+    """Without a snapshot LSE the step computes each committed query's LSE over its
+    scored tokens: the same normaliser the verifier's attention returns, so
+    scores, selection, plans and working cache match the oracle with the exact
+    LSE, and lse_out equals that LSE."""
+    g = gen(seed)
+    lens = [int(x) for x in torch.randint(3000, 30000, (12,), generator=g)]
+    counts = [int(x) for x in torch.randint(0, 6, (12,), generator=g)]
+    counts[0] = 5
+    slots = [int(x) for x in torch.randperm(12, generator=g)]
+    case = build_case(seed, real_rows=12, pad_rows=4, target_lens=lens, query_len=5, counts=counts, hq=hq, hkv=hkv,
+                      head_dim=head_dim, chunk=chunk, token_budget=2048, block_size=block_size, lmax=30000,
+                      slots=slots, num_slots=12)
+    state = run_gpu(case, cuda, path=path, lse_free=True)
+    check_step(case, state)
+    rows_idx, q_index, _ = O.retrieval_rows(case["counts"], case["ends"], case["tlens"], case["real_rows"])
+    lse_out = state["lse_out"].cpu()
+    torch.testing.assert_close(lse_out[rows_idx], case["lse"][q_index], rtol=1e-5, atol=1e-4)
+    unscored = [b for b in range(case["rows"]) if b not in rows_idx]
+    assert torch.isnan(lse_out[unscored]).all()  # rows that are not scored are left alone

@@ -91,6 +91,15 @@ def test_paged_scores_equal_dense_with_reordered_pages(hq, hkv):
     got = O.paged_chunk_attention_scores(query, keys, torch.stack(lse), tables, torch.tensor(lengths),
                                          chunk_size=chunk, max_seq_len=max(lengths), scale=scale)
     torch.testing.assert_close(got, torch.stack(refs), rtol=1e-5, atol=1e-7)
+    # Without an LSE each row normalises over its own tokens (runtime.py:321-322),
+    # the softmax of the dense reference.
+    free = O.paged_chunk_attention_scores(query, keys, None, tables, torch.tensor(lengths),
+                                          chunk_size=chunk, max_seq_len=max(lengths), scale=scale)
+    torch.testing.assert_close(free, torch.stack(refs), rtol=1e-5, atol=1e-7)
+    # A planted LSE off by log 2 halves every score and is caught.
+    off = O.paged_chunk_attention_scores(query, keys, torch.stack(lse) + math.log(2), tables, torch.tensor(lengths),
+                                         chunk_size=chunk, max_seq_len=max(lengths), scale=scale)
+    assert not torch.allclose(off, torch.stack(refs), rtol=1e-3)
 
 
 def test_head_reduce_max_closed_form():

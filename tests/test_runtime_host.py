@@ -113,6 +113,32 @@ def test_retrieval_skips_prefill_snapshot_and_interval(launches):
     assert len(launches) == 1
 
 
+def test_snapshot_without_lse(launches):
+    """A backend that returns no LSE: dropped as the reference does (runtime.py:850-851),
+    or, with lse_free_scoring, kept and scored with per-row LSE buffers."""
+    q = torch.zeros((2, 2, 2))
+    meta = _metadata([1, 2], [6, 4], prefill=False)
+    reference = _cache(settings=dict(retrieval_interval=1))
+    reference.begin_target_forward(["a", "b"])
+    reference.capture_target_attention(q, None, torch.zeros((1, 2, 1, 2)), meta, 0.5)
+    reference.accept_target_queries(torch.ones(2), is_prefill=False)
+    assert launches == [] and reference.retrieval_status()["retrieval_skipped_no_snapshot"] == 1
+
+    cache = _cache(settings=dict(retrieval_interval=1), lse_free_scoring=True)
+    cache.begin_target_forward(["a", "b"])
+    cache.capture_target_attention(q, None, torch.zeros((1, 2, 1, 2)), meta, 0.5)
+    cache.accept_target_queries(torch.ones(2), is_prefill=False)
+    call = launches[-1]
+    assert call["snapshot"].lse is None
+    assert call["lse_partials"].shape == (2, 2, cache.max_chunks, 2)
+    assert call["lse_out"].shape == (2, 2) and cache.scored_lse.shape == (cache.max_batch_rows, 2)
+    # A supplied LSE is still used when there is one; no pair buffers are passed.
+    cache.begin_target_forward(["a", "b"])
+    cache.capture_target_attention(q, torch.ones((2, 2)), torch.zeros((1, 2, 1, 2)), meta, 0.5)
+    cache.accept_target_queries(torch.ones(2), is_prefill=False)
+    assert launches[-1]["snapshot"].lse is not None and launches[-1]["lse_partials"] is None
+
+
 def test_speculative_rows_and_graph_padding(launches):
     """Linear verification: per-row query lengths, accepted counts and padded rows beyond the scheduler's."""
     cache = _cache(settings=dict(retrieval_interval=1), max_model_len=32)

@@ -67,7 +67,7 @@ int make_score_args(score::ScoreArgs& a, int64_t& upper_units, bool& uniform_pag
                     const int32_t* block_table, int64_t bt_stride, const RowSource& src, int batch, int num_q_heads,
                     int num_kv_heads, int head_dim, int block_size, int chunk_size, int max_chunks, float scale,
                     int head_reduce, float* partial, float* out, int64_t out_stride, int write_tail,
-                    size_t partial_bytes);
+                    size_t partial_bytes, float* mz);
 int make_select_args(select::SelectArgs& a, float* scores, int64_t score_stride, const float* partials,
                      int max_chunks, int hkv, int hq, const RowSource& src, int batch, int chunk, int budget,
                      int do_select, int do_plan, int32_t* ids, int64_t ids_stride, int32_t* counts,
@@ -500,7 +500,8 @@ size_t fused_workspace_bytes(int rows, int max_chunks, int num_kv_heads, int tok
 // kernel; `launched` stays false (and nothing is launched) otherwise.
 int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource& src, bool& launched) {
   launched = false;
-  if (d->workspace == nullptr || d->stages != DS_STAGE_ALL) return clear_error();
+  // Without a supplied LSE a row's scores need all of its chunks first: the chain runs.
+  if (d->workspace == nullptr || d->stages != DS_STAGE_ALL || d->lse == nullptr) return clear_error();
   const size_t need = fused_workspace_bytes(d->batch_rows, d->max_chunks, d->num_kv_heads, d->token_budget);
   DS_REQUIRE(need > 0 && d->workspace_bytes >= need,
              "step workspace too small: need %zu bytes for %d rows, %d chunks, %d KV heads, token budget %d", need,
@@ -514,7 +515,7 @@ int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource
                            d->k_block_stride, d->k_token_stride, d->k_head_stride, d->lse, d->lse_token_stride,
                            d->lse_head_stride, d->block_table, d->bt_stride, src, d->batch_rows, d->num_q_heads,
                            d->num_kv_heads, d->head_dim, d->block_size, d->chunk_size, d->max_chunks, d->scale,
-                           DS_HEAD_MEAN, d->score_partials, nullptr, 0, 0, SIZE_MAX);
+                           DS_HEAD_MEAN, d->score_partials, nullptr, 0, 0, SIZE_MAX, nullptr);
   if (rc != DS_OK) return rc;
   rc = make_select_args(f.p, d->scores, d->max_chunks, d->score_partials, d->max_chunks, d->num_kv_heads,
                         d->num_q_heads, src, d->batch_rows, d->chunk_size, d->history_budget, 1, 1, d->sel_ids,

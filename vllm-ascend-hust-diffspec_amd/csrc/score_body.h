@@ -10,6 +10,7 @@ namespace score {
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
 constexpr int kMaxNtu = 8;  // 16-token groups per unit with head_reduce = max (U <= 128)
+constexpr int kMaxGroup = 16;  // query heads per KV head (one 16-row MFMA A operand)
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
@@ -43,7 +44,56 @@ struct ScoreArgs {
   float* out;      // [batch, out_stride] final scores (head max; tail zeros)
   int64_t out_stride;
   int write_tail;
+  // Without a supplied LSE: per (row, query head, chunk) the chunk's largest
+  // scaled logit m (log2 units) and sum z = sum_t 2^(logit_t - m), as float
+  // pairs [batch, Hq, max_chunks, 2] (a head's chunks are contiguous).
+  float* mz;
 };
+
+// (m, z) pairs with m in log2 units: the merged pair of two parts of one sum.
+// m = -inf marks an empty part (z = 0).
+__device__ __forceinline__ void merge_mz(float& m, float& z, float m2, float z2) {
+  const float mn = fmaxf(m, m2);
+  const float a = m == -INFINITY ? 0.f : z * __builtin_amdgcn_exp2f(m - mn);
+  const float b = m2 == -INFINITY ? 0.f : z2 * __builtin_amdgcn_exp2f(m2 - mn);
+  m = mn;
+  z = a + b;
+}
+
+// Add one term 2^x to the pair (m, z), with one exp2: for x <= m the term is
+// 2^(x - m) on the current scale, else the sum is rescaled to x.  m starts at
+// kNoMax (finite, so x = -inf adds nothing and the first real x takes over);
+// lanes that saw no term keep z = 0.
+constexpr float kNoMax = -3.0e38f;
+__device__ __forceinline__ void add_term(float& m, float& z, float x) {
+  const float d = x - m;
+  const float e = __builtin_amdgcn_exp2f(-fabsf(d));
+  z = d <= 0.f ? z + e : fmaf(z, e, 1.f);
+  m = fmaxf(m, x);
+}
+
+// Merge the (m, z) pairs of the 16 lanes of each 16-lane row with DPP lane
+// permutes (quad xor 1, quad xor 2, half-row mirror, row mirror): the row's
+// max first, then every z rescaled to it once and summed; every lane of the
+// row ends with the row's pair.  A lane that saw no term has z = 0 and adds
+// nothing, whatever its m.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+__device__ __forceinline__ void merge_mz_row16(float& m, float& z) {
+  float mx = fmaxf(m, dpp_row<0xB1>(m));
+  mx = fmaxf(mx, dpp_row<0x4E>(mx));
+  mx = fmaxf(mx, dpp_row<0x141>(mx));
+  mx = fmaxf(mx, dpp_row<0x140>(mx));
+  float t = z > 0.f ? z * __builtin_amdgcn_exp2f(m - mx) : 0.f;
+  t += dpp_row<0xB1>(t);
+  t += dpp_row<0x4E>(t);
+  t += dpp_row<0x141>(t);
+  t += dpp_row<0x140>(t);
+  m = mx;
+  z = t;
+}
 
 template <int DT>
 __device__ __forceinline__ f32x4_t mfma16x16x32(const Raw16& a, const Raw16& b, f32x4_t c) {
@@ -86,12 +136,40 @@ struct Batch {
   BatchCtx c;
 };
 
+// LSEFREE: merge a chunk's running pairs (one per token group slot of a
+// batch, then the 16 token lanes), store each real head's pair at
+// mz[row, head, chunk] and reset for the next chunk.
+template <int KB>
+__device__ __forceinline__ void flush_pairs(const ScoreArgs& a, const BatchCtx& c, int cc, float (&m)[KB][4],
+                                            float (&z)[KB][4], int kgrp, int col) {
+  const int ch = c.c0 + cc;
+  const int chunks_row = (c.len + a.chunk - 1) / a.chunk;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float mt = m[0][e], zt = z[0][e];
+#pragma unroll
+    for (int i = 1; i < KB; ++i) merge_mz(mt, zt, m[i][e], z[i][e]);
+    merge_mz_row16(mt, zt);
+    const int h = 4 * kgrp + e;
+    if (col == 0 && h < a.G && ch < chunks_row) {
+      const int64_t at = ((static_cast<int64_t>(c.b) * a.Hq + c.g * a.G + h) * a.max_chunks + ch) * 2;
+      *reinterpret_cast<float2*>(a.mz + at) = make_float2(mt, zt);
+    }
+#pragma unroll
+    for (int i = 0; i < KB; ++i) {
+      m[i][e] = kNoMax;
+      z[i][e] = 0.f;
+    }
+  }
+}
+
 // One wave's walk over its strided unit list: units gw, gw + tw, ... of the
 // numbering in s_prefix (rows' unit counts, exclusive prefix) with s_len /
 // s_qrow the rows' scored lengths and query rows.  Head mean stores
 // per-KV-head chunk sums (partial, or tagged with `tag` when TAGGED); head
-// max stores final chunk scores.
-template <int DT, int STEPS, int KB, bool HMAX, bool UNIFORM_PAGE, bool TAGGED>
+// max stores final chunk scores.  LSEFREE (head mean only): no LSE is read;
+// each chunk's (max, sum) per query head goes to a.mz instead.
+template <int DT, int STEPS, int KB, bool HMAX, bool UNIFORM_PAGE, bool TAGGED, bool LSEFREE = false>
 __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_prefix, const int* s_len,
                                              const int* s_qrow, int total, int gw, int tw, uint32_t tag) {
   const int lane = threadIdx.x & 63;
@@ -183,10 +261,12 @@ __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_pr
     const uint16_t* qh = a.q + c.qbase + static_cast<int64_t>(q_head) * a.D + kgrp * 8;
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) out.q[s] = *reinterpret_cast<const Raw16*>(qh + 32 * s);
+    if constexpr (!LSEFREE) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = min(4 * kgrp + i, a.G - 1);
-      out.lse[i] = a.lse[c.lbase + static_cast<int64_t>(m) * a.lse_head_stride];
+      for (int i = 0; i < 4; ++i) {
+        const int m = min(4 * kgrp + i, a.G - 1);
+        out.lse[i] = a.lse[c.lbase + static_cast<int64_t>(m) * a.lse_head_stride];
+      }
     }
   };
 
@@ -194,6 +274,24 @@ __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_pr
   float tmax[kMaxNtu];                  // per 16-token group (head max)
 #pragma unroll
   for (int t = 0; t < kMaxNtu; ++t) tmax[t] = 0.f;
+  // LSEFREE: the lane's running (max, sum) of query head 4 * kgrp + e over
+  // its tokens of chunk `cur` of the unit, in log2 units.  A unit's token
+  // groups run in order, so its chunks finish one after another: the pairs
+  // are merged and stored when the chunk index moves on (registers only, no
+  // per-chunk arrays).
+  // One pair per token group slot of a batch keeps the slots' update chains
+  // independent.
+  float cm[KB][4], cz[KB][4];
+#pragma unroll
+  for (int i = 0; i < KB; ++i) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      cm[i][e] = kNoMax;
+      cz[i][e] = 0.f;
+    }
+  }
+  int cur = 0;  // wave-uniform
+  const float scale2 = a.scale * 1.44269504088896340736f;
 
   auto compute = [&](const Batch<KB, STEPS>& bt) {
     const BatchCtx& c = bt.c;
@@ -220,6 +318,15 @@ __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_pr
 #pragma unroll
         for (int t = 0; t < kMaxNtu; ++t) {
           if (t == tg) tmax[t] = fmaxf(tmax[t], m4);
+        }
+      } else if constexpr (LSEFREE) {
+        if (ci != cur) {  // wave-uniform
+          flush_pairs(a, c, cur, cm, cz, kgrp, col);
+          cur = ci;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          add_term(cm[i][e], cz[i][e], (4 * kgrp + e < a.G && tok_ok) ? logit[e] * scale2 : -INFINITY);
         }
       } else {
         float s = 0.f;
@@ -252,6 +359,9 @@ __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_pr
       }
 #pragma unroll
       for (int t = 0; t < kMaxNtu; ++t) tmax[t] = 0.f;
+    } else if constexpr (LSEFREE) {
+      flush_pairs(a, c, cur, cm, cz, kgrp, col);
+      cur = 0;
     } else {
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc) {

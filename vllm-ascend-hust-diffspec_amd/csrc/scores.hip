@@ -24,6 +24,15 @@
 // in the selection kernel for a retrieval step, or in finalize_kernel for
 // the drop-in entry point.  The per-token head max (head_reduce = max) keeps
 // all KV heads of a span in one wave and writes final scores directly.
+//
+// Without a supplied LSE (the reference's chunk_attention_scores with
+// softmax_lse=None, diffspec/runtime.py:321-322: the LSE of each query head
+// over the row's scored tokens) the same single pass keeps, per lane, a
+// running (max, sum of 2^(logit - max)) per chunk and query head, merges the
+// 16 token lanes with DPP permutes and stores the pairs; lse_finalize_kernel
+// then merges a row's chunks into each head's LSE and writes the usual
+// per-KV-head partials, sum over the group's heads of z * 2^(m - lse), so
+// selection and the drop-in finalize read them unchanged.
 #include "score_body.h"
 
 namespace ds355 {
@@ -36,7 +45,7 @@ using namespace score;
 // UNIFORM_PAGE = every 16-token group lies inside one block (block_size and
 // the unit start are multiples of 16), so its block-table entry is one
 // scalar load.
-template <int DT, int STEPS, int KB, int WGS, bool HMAX, bool UNIFORM_PAGE>
+template <int DT, int STEPS, int KB, int WGS, bool HMAX, bool UNIFORM_PAGE, bool LSEFREE>
 __global__ __launch_bounds__(kThreads, WGS) void chunk_score_kernel(ScoreArgs a) {
   __shared__ int s_prefix[kMaxRows + 1];
   __shared__ int s_len[kMaxRows];
@@ -54,8 +63,8 @@ __global__ __launch_bounds__(kThreads, WGS) void chunk_score_kernel(ScoreArgs a)
                    [&](int r) { return (s_len[r] + a.U - 1) / a.U * units_per_span; });
   const int total = s_prefix[a.batch];
   const int gw = uniform(blockIdx.x * kWaves + (threadIdx.x >> 6));
-  score_stream<DT, STEPS, KB, HMAX, UNIFORM_PAGE, false>(a, s_prefix, s_len, s_qrow, total, gw,
-                                                         gridDim.x * kWaves, 0u);
+  score_stream<DT, STEPS, KB, HMAX, UNIFORM_PAGE, false, LSEFREE>(a, s_prefix, s_len, s_qrow, total, gw,
+                                                                  gridDim.x * kWaves, 0u);
 
   if (a.write_tail) {
     // Head max writes final scores; chunks at or beyond a row's length are 0.
@@ -91,7 +100,82 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(const float* __restr
   }
 }
 
-template <int DT, int STEPS, bool HMAX>
+// One workgroup per (row, KV head, slice of chunks): the LSE of each query
+// head of the group from all of the row's (max, sum) pairs, then that KV
+// head's partial of every chunk of the slice, sum over the group's heads of
+// z * 2^(m - lse).  The slices of a row each recompute the group's LSEs (a
+// few KB of pairs, from L2) so that no second launch or grid-wide wait is
+// needed.  A head's pairs are contiguous: tph threads per head stream them
+// with eight loads in flight and merge by lane shuffles (and LDS when a head
+// spans several waves).
+constexpr int kFinalizeLoads = 8;
+constexpr int kFinalizeSlice = 128;  // chunks per slice
+__global__ __launch_bounds__(kThreads) void lse_finalize_kernel(const float* __restrict__ mz, RowSource src,
+                                                                int max_chunks, int hq, int hkv, int chunk,
+                                                                float* __restrict__ partial, float* __restrict__ lse_out,
+                                                                int64_t lse_stride) {
+  __shared__ float s_m[kThreads], s_z[kThreads];
+  __shared__ float s_lse2[kMaxGroup];
+  const int slices = (max_chunks + kFinalizeSlice - 1) / kFinalizeSlice;
+  const int s = blockIdx.x % slices;
+  const int g = (blockIdx.x / slices) % hkv;
+  const int b = blockIdx.x / slices / hkv;
+  const RowDesc d = row_desc(src, b);
+  const int len = d.active ? d.len : 0;
+  const int chunks = (len + chunk - 1) / chunk;
+  const int c_begin = s * kFinalizeSlice;
+  if (c_begin >= chunks) return;  // workgroup-uniform (also rows with nothing scored)
+  const int c_end = min(chunks, c_begin + kFinalizeSlice);
+  const int G = hq / hkv;
+  const int t = threadIdx.x;
+  const float2* pairs = reinterpret_cast<const float2*>(mz) + (static_cast<int64_t>(b) * hq + g * G) * max_chunks;
+
+  int tph = 1;  // threads per head: a power of two, tph * G <= kThreads
+  while (tph * 2 * G <= kThreads) tph *= 2;
+  const int hl = t / tph, j = t % tph;
+  float m = -INFINITY, z = 0.f;
+  if (hl < G) {
+    const float2* p = pairs + static_cast<int64_t>(hl) * max_chunks;
+    for (int c0 = j; c0 < chunks; c0 += kFinalizeLoads * tph) {
+      float2 v[kFinalizeLoads];
+#pragma unroll
+      for (int u = 0; u < kFinalizeLoads; ++u) {
+        const int c = c0 + u * tph;
+        v[u] = c < chunks ? p[c] : make_float2(-INFINITY, 0.f);
+      }
+#pragma unroll
+      for (int u = 0; u < kFinalizeLoads; ++u) merge_mz(m, z, v[u].x, v[u].y);
+    }
+  }
+  const int span = tph < 64 ? tph : 64;
+  for (int off = 1; off < span; off <<= 1) merge_mz(m, z, __shfl_xor(m, off, 64), __shfl_xor(z, off, 64));
+  s_m[t] = m;
+  s_z[t] = z;
+  __syncthreads();
+  if (t < G) {
+    float mh = -INFINITY, zh = 0.f;
+    for (int k = 0; k < tph; k += 64) merge_mz(mh, zh, s_m[t * tph + k], s_z[t * tph + k]);
+    const float lse2 = zh > 0.f ? mh + __log2f(zh) : -INFINITY;
+    s_lse2[t] = lse2;
+    if (lse_out && s == 0) lse_out[static_cast<int64_t>(b) * lse_stride + g * G + t] = lse2 * 0.69314718055994530942f;
+  }
+  __syncthreads();
+  for (int c = c_begin + t; c < c_end; c += kThreads) {
+    float2 v[kMaxGroup];
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; ++h) {
+      v[h] = h < G ? pairs[static_cast<int64_t>(h) * max_chunks + c] : make_float2(-INFINITY, 0.f);
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; ++h) {
+      if (v[h].x != -INFINITY) sum += v[h].y * __builtin_amdgcn_exp2f(v[h].x - s_lse2[h]);
+    }
+    partial[(static_cast<int64_t>(b) * max_chunks + c) * hkv + g] = sum;
+  }
+}
+
+template <int DT, int STEPS, bool HMAX, bool LSEFREE>
 void launch_kb(hipStream_t stream, const ScoreArgs& a, int64_t upper_blocks, bool uniform_page) {
   // Batch shape, measured on 16 x 40k-token rows: batches of about 8 KB of
   // keys per wave with three workgroups per CU stream faster than 16 KB
@@ -103,23 +187,23 @@ void launch_kb(hipStream_t stream, const ScoreArgs& a, int64_t upper_blocks, boo
   const int64_t cap = static_cast<int64_t>(device_cu_count()) * WGS;
   const int grid = static_cast<int>(std::max<int64_t>(1, std::min(upper_blocks, cap)));
   if (uniform_page) {
-    chunk_score_kernel<DT, STEPS, KB, WGS, HMAX, true><<<grid, kThreads, 0, stream>>>(a);
+    chunk_score_kernel<DT, STEPS, KB, WGS, HMAX, true, LSEFREE><<<grid, kThreads, 0, stream>>>(a);
   } else {
-    chunk_score_kernel<DT, STEPS, KB, WGS, HMAX, false><<<grid, kThreads, 0, stream>>>(a);
+    chunk_score_kernel<DT, STEPS, KB, WGS, HMAX, false, LSEFREE><<<grid, kThreads, 0, stream>>>(a);
   }
 }
 
-template <int DT, bool HMAX>
+template <int DT, bool HMAX, bool LSEFREE>
 void launch_steps(hipStream_t stream, const ScoreArgs& a, int64_t grid, bool uniform_page) {
   switch (a.D / 32) {
-    case 1: launch_kb<DT, 1, HMAX>(stream, a, grid, uniform_page); break;
-    case 2: launch_kb<DT, 2, HMAX>(stream, a, grid, uniform_page); break;
-    case 3: launch_kb<DT, 3, HMAX>(stream, a, grid, uniform_page); break;
-    case 4: launch_kb<DT, 4, HMAX>(stream, a, grid, uniform_page); break;
-    case 5: launch_kb<DT, 5, HMAX>(stream, a, grid, uniform_page); break;
-    case 6: launch_kb<DT, 6, HMAX>(stream, a, grid, uniform_page); break;
-    case 7: launch_kb<DT, 7, HMAX>(stream, a, grid, uniform_page); break;
-    default: launch_kb<DT, 8, HMAX>(stream, a, grid, uniform_page); break;
+    case 1: launch_kb<DT, 1, HMAX, LSEFREE>(stream, a, grid, uniform_page); break;
+    case 2: launch_kb<DT, 2, HMAX, LSEFREE>(stream, a, grid, uniform_page); break;
+    case 3: launch_kb<DT, 3, HMAX, LSEFREE>(stream, a, grid, uniform_page); break;
+    case 4: launch_kb<DT, 4, HMAX, LSEFREE>(stream, a, grid, uniform_page); break;
+    case 5: launch_kb<DT, 5, HMAX, LSEFREE>(stream, a, grid, uniform_page); break;
+    case 6: launch_kb<DT, 6, HMAX, LSEFREE>(stream, a, grid, uniform_page); break;
+    case 7: launch_kb<DT, 7, HMAX, LSEFREE>(stream, a, grid, uniform_page); break;
+    default: launch_kb<DT, 8, HMAX, LSEFREE>(stream, a, grid, uniform_page); break;
   }
 }
 
@@ -134,7 +218,7 @@ int make_score_args(ScoreArgs& a, int64_t& upper_units, bool& uniform_page, int 
                     const int32_t* block_table, int64_t bt_stride, const RowSource& src, int batch, int num_q_heads,
                     int num_kv_heads, int head_dim, int block_size, int chunk_size, int max_chunks, float scale,
                     int head_reduce, float* partial, float* out, int64_t out_stride, int write_tail,
-                    size_t partial_bytes) {
+                    size_t partial_bytes, float* mz) {
   upper_units = 0;
   DS_REQUIRE(dtype == DS_BF16 || dtype == DS_FP16, "chunk scores support BF16 or FP16 query/key caches");
   DS_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0,
@@ -145,7 +229,7 @@ int make_score_args(ScoreArgs& a, int64_t& upper_units, bool& uniform_page, int 
   DS_REQUIRE(head_reduce == DS_HEAD_MEAN || head_reduce == DS_HEAD_MAX, "head_reduce must be mean or max");
   DS_SUPPORTED(head_dim > 0 && head_dim % 32 == 0 && head_dim <= 256,
                "head_dim must be a multiple of 32 up to 256 (got %d)", head_dim);
-  DS_SUPPORTED(num_q_heads / num_kv_heads <= 16, "at most 16 query heads per KV head (got %d)",
+  DS_SUPPORTED(num_q_heads / num_kv_heads <= kMaxGroup, "at most %d query heads per KV head (got %d)", kMaxGroup,
                num_q_heads / num_kv_heads);
   DS_SUPPORTED(batch <= kMaxRows, "at most %d rows per launch (got %d)", kMaxRows, batch);
   DS_REQUIRE(q_stride % 8 == 0 && k_block_stride % 8 == 0 && k_token_stride % 8 == 0 && k_head_stride % 8 == 0,
@@ -160,7 +244,13 @@ int make_score_args(ScoreArgs& a, int64_t& upper_units, bool& uniform_page, int 
   const int ntu = (U + 15) / 16;
   DS_SUPPORTED(!hmax || ntu <= kMaxNtu, "head_reduce=max supports chunks of at most %d tokens", kMaxNtu * 16);
   if (batch == 0 || max_chunks == 0) return clear_error();
-  DS_REQUIRE(query && key_cache && lse && block_table, "null tensor pointer");
+  DS_REQUIRE(query && key_cache && block_table, "null tensor pointer");
+  // No LSE: the pass computes it (head mean only); the pairs need mz.
+  DS_SUPPORTED(lse || !hmax, "head_reduce=max needs a supplied softmax LSE");
+  DS_REQUIRE(lse || mz,
+             "workspace too small: need %zu bytes without an LSE (batch * max_chunks * (kv_heads + 2 * q_heads) * 4)",
+             static_cast<size_t>(batch) * max_chunks * (num_kv_heads + 2 * static_cast<size_t>(num_q_heads)) *
+                 sizeof(float));
   if (!hmax) {
     const size_t need = static_cast<size_t>(batch) * max_chunks * num_kv_heads * sizeof(float);
     DS_REQUIRE(partial != nullptr && partial_bytes >= need,
@@ -206,6 +296,7 @@ int make_score_args(ScoreArgs& a, int64_t& upper_units, bool& uniform_page, int 
   a.ci_shift = cpu > 1 ? log2_or_neg(chunk_size) : 31;
   a.scale = scale;
   a.partial = partial;
+  a.mz = lse ? nullptr : mz;
   a.out = out;
   a.out_stride = out_stride;
   a.write_tail = hmax ? write_tail : 0;
@@ -221,25 +312,37 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
                         int64_t lse_row_stride, int64_t lse_head_stride, const int32_t* block_table,
                         int64_t bt_stride, const RowSource& src, int batch, int num_q_heads, int num_kv_heads,
                         int head_dim, int block_size, int chunk_size, int max_chunks, float scale, int head_reduce,
-                        float* partial, float* out, int64_t out_stride, int write_tail, size_t partial_bytes) {
+                        float* partial, float* out, int64_t out_stride, int write_tail, size_t partial_bytes,
+                        float* mz, float* lse_out, int64_t lse_out_stride) {
   ScoreArgs a{};
   int64_t upper_units = 0;
   bool uniform_page = false;
   const int rc = make_score_args(a, upper_units, uniform_page, dtype, query, q_stride, key_cache, k_block_stride,
                                  k_token_stride, k_head_stride, lse, lse_row_stride, lse_head_stride, block_table,
                                  bt_stride, src, batch, num_q_heads, num_kv_heads, head_dim, block_size, chunk_size,
-                                 max_chunks, scale, head_reduce, partial, out, out_stride, write_tail, partial_bytes);
+                                 max_chunks, scale, head_reduce, partial, out, out_stride, write_tail, partial_bytes,
+                                 mz);
   if (rc != DS_OK || upper_units == 0) return rc;
   const bool hmax = head_reduce == DS_HEAD_MAX;
+  const bool lse_free = lse == nullptr;
   const int64_t upper_blocks = (upper_units + kWaves - 1) / kWaves;
   if (dtype == DS_BF16) {
-    if (hmax) launch_steps<DS_BF16, true>(stream, a, upper_blocks, uniform_page);
-    else launch_steps<DS_BF16, false>(stream, a, upper_blocks, uniform_page);
+    if (hmax) launch_steps<DS_BF16, true, false>(stream, a, upper_blocks, uniform_page);
+    else if (lse_free) launch_steps<DS_BF16, false, true>(stream, a, upper_blocks, uniform_page);
+    else launch_steps<DS_BF16, false, false>(stream, a, upper_blocks, uniform_page);
   } else {
-    if (hmax) launch_steps<DS_FP16, true>(stream, a, upper_blocks, uniform_page);
-    else launch_steps<DS_FP16, false>(stream, a, upper_blocks, uniform_page);
+    if (hmax) launch_steps<DS_FP16, true, false>(stream, a, upper_blocks, uniform_page);
+    else if (lse_free) launch_steps<DS_FP16, false, true>(stream, a, upper_blocks, uniform_page);
+    else launch_steps<DS_FP16, false, false>(stream, a, upper_blocks, uniform_page);
   }
-  return check_launch("ds_chunk_scores");
+  int rc2 = check_launch("ds_chunk_scores");
+  if (rc2 != DS_OK || !lse_free) return rc2;
+  const int64_t grid = static_cast<int64_t>(batch) * num_kv_heads * ((max_chunks + kFinalizeSlice - 1) / kFinalizeSlice);
+  DS_SUPPORTED(grid < (int64_t{1} << 31), "too many (row, KV head, chunk slice) workgroups");
+  lse_finalize_kernel<<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(a.mz, a.src, max_chunks, num_q_heads,
+                                                                            num_kv_heads, chunk_size, partial, lse_out,
+                                                                            lse_out_stride);
+  return check_launch("ds_chunk_scores lse");
 }
 
 }  // namespace ds355
@@ -256,10 +359,19 @@ extern "C" int ds_chunk_scores(ds_stream_t stream, int dtype, const void* query,
   src.seq_lens = seq_lens;
   const bool hmax = head_reduce == DS_HEAD_MAX;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // Without an LSE the workspace also holds the (max, sum) pairs, after the
+  // per-KV-head partials (a workspace too small for them is reported with
+  // the other argument checks).
+  float* mz = nullptr;
+  if (lse == nullptr && !hmax && batch > 0 && max_chunks > 0 && num_q_heads > 0 && num_kv_heads > 0) {
+    const size_t parts = static_cast<size_t>(batch) * max_chunks * num_kv_heads;
+    const size_t need = (parts + static_cast<size_t>(batch) * max_chunks * num_q_heads * 2) * sizeof(float);
+    if (workspace != nullptr && workspace_bytes >= need) mz = workspace + parts;
+  }
   int rc = launch_chunk_scores(s, dtype, query, q_stride, key_cache, k_block_stride, k_token_stride, k_head_stride,
                                lse, lse_row_stride, lse_head_stride, block_table, bt_stride, src, batch, num_q_heads,
                                num_kv_heads, head_dim, block_size, chunk_size, max_chunks, scale, head_reduce,
-                               workspace, out, out_stride, 1, workspace_bytes);
+                               workspace, out, out_stride, 1, workspace_bytes, mz, nullptr, 0);
   if (rc != DS_OK || hmax || batch == 0 || max_chunks == 0) return rc;
   DS_REQUIRE(out != nullptr, "null score output pointer");
   const int64_t n = static_cast<int64_t>(batch) * max_chunks;

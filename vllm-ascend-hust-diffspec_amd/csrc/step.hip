@@ -1,8 +1,9 @@
 // One retrieval step on one stream: the single-launch kernel (fused.hip)
 // when the descriptor brings a workspace and fits it, otherwise a chain:
 //   chunk_score_kernel (rows with committed tokens; committed query; rejected
-//   suffix cut) -> select_plan_kernel (selection into the per-slot state,
-//   then a plan row for every real row) -> gather kernel over the plan.
+//   suffix cut; without a softmax LSE, plus lse_finalize_kernel) ->
+//   select_plan_kernel (selection into the per-slot state, then a plan row
+//   for every real row) -> gather kernel over the plan.
 // No host synchronisation; launch shapes depend only on the descriptor's
 // upper bounds, so the chain can be captured into a HIP graph.
 #include "rowdesc.h"
@@ -14,7 +15,8 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
                         int64_t lse_row_stride, int64_t lse_head_stride, const int32_t* block_table,
                         int64_t bt_stride, const RowSource& src, int batch, int num_q_heads, int num_kv_heads,
                         int head_dim, int block_size, int chunk_size, int max_chunks, float scale, int head_reduce,
-                        float* partial, float* out, int64_t out_stride, int write_tail, size_t partial_bytes);
+                        float* partial, float* out, int64_t out_stride, int write_tail, size_t partial_bytes,
+                        float* mz, float* lse_out, int64_t lse_out_stride);
 
 int launch_select_plan(hipStream_t stream, float* scores, int64_t score_stride, const float* partials,
                        int max_chunks, int hkv, int hq, const RowSource& src,
@@ -63,6 +65,10 @@ extern "C" int ds_retrieval_step(ds_stream_t stream_handle, const ds_step_desc* 
                "score and score-partial buffers are required");
     DS_REQUIRE(d->num_kv_heads > 0 && d->num_q_heads > 0, "head counts must be positive");
   }
+  if (score) {
+    DS_REQUIRE(d->lse != nullptr || d->lse_partials != nullptr,
+               "without a softmax LSE the step needs lse_partials ([batch_rows, Hq, max_chunks, 2] fp32)");
+  }
   src.max_len = static_cast<int>(std::min<int64_t>(static_cast<int64_t>(d->max_chunks) * d->chunk_size, INT32_MAX));
   bool launched = false;
   int rc = launch_fused_step(stream, d, src, launched);
@@ -72,7 +78,8 @@ extern "C" int ds_retrieval_step(ds_stream_t stream_handle, const ds_step_desc* 
                              d->k_token_stride, d->k_head_stride, d->lse, d->lse_token_stride, d->lse_head_stride,
                              d->block_table, d->bt_stride, src, d->batch_rows, d->num_q_heads, d->num_kv_heads,
                              d->head_dim, d->block_size, d->chunk_size, d->max_chunks, d->scale, DS_HEAD_MEAN,
-                             d->score_partials, nullptr, 0, 0, SIZE_MAX);
+                             d->score_partials, nullptr, 0, 0, SIZE_MAX, d->lse_partials, d->lse_out,
+                             d->lse_out_stride);
     if (rc != DS_OK) return rc;
   }
   if (select || rebuild) {

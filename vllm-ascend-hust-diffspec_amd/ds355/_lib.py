@@ -18,7 +18,7 @@ DS_OK, DS_ERR_INVALID, DS_ERR_UNSUPPORTED, DS_ERR_HIP = 0, 1, 2, 3
 DS_BF16, DS_FP16, DS_FP32 = 0, 1, 2
 DS_HEAD_MEAN, DS_HEAD_MAX = 0, 1
 DS_STAGE_SCORE, DS_STAGE_SELECT, DS_STAGE_PLAN, DS_STAGE_ALL = 1, 2, 4, 7
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 EXPORTED_SYMBOLS = (
     "ds_last_error",
@@ -75,6 +75,7 @@ class StepDesc(ctypes.Structure):
         ("row_active", _p),
         ("chunk_size", _i32), ("history_budget", _i32), ("recent_window", _i32),
         ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),
+        ("lse_partials", _p), ("lse_out", _p), ("lse_out_stride", _i64),
     ]
 
 

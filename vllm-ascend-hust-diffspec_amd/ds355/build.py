@@ -1,8 +1,9 @@
 """Build libds355.so in-tree with hipcc for gfx950.
 
 ``python -m ds355.build`` (or ``build()``) compiles every ``csrc/*.hip`` into
-``ds355/libds355.so``.  The GPU code is built for gfx950 only, with fp
-contraction off (the RoPE rotate must round each product separately),
+``ds355/libds355.so``: one hipcc process per source file, in parallel, into
+a temporary directory, then one link.  The GPU code is built for gfx950 only,
+with fp contraction off (the RoPE rotate must round each product separately),
 packed-fp32 instructions disabled and the wave-level atomic aggregation off.
 """
 
@@ -12,6 +13,8 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent
@@ -31,14 +34,12 @@ def sources() -> list[Path]:
     return sorted(SOURCE_DIR.glob("*.hip"))
 
 
-def command(output: Path) -> list[str]:
+def flags() -> list[str]:
     return [
-        hipcc(),
         f"--offload-arch={ARCH}",
         "-O3",
         "-std=c++17",
         "-fPIC",
-        "-shared",
         "-ffp-contract=off",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
         # Keep single-lane atomics as written: the optimizer's wave-wide
@@ -47,15 +48,10 @@ def command(output: Path) -> list[str]:
         "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
         "-Wall",
         "-Wno-unused-function",
-        "-o", str(output),
-        *[str(s) for s in sources()],
     ]
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile the library; raises CalledProcessError with hipcc's output on failure."""
-    tmp = LIBRARY.with_suffix(".so.tmp")
-    cmd = command(tmp)
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     result = subprocess.run(cmd, capture_output=True, text=True)
@@ -65,6 +61,20 @@ def build(verbose: bool = False) -> Path:
         raise subprocess.CalledProcessError(result.returncode, cmd, result.stdout, stderr)
     if verbose and stderr.strip():
         print(stderr, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile the library; raises CalledProcessError with hipcc's output on failure."""
+    tmp = LIBRARY.with_suffix(".so.tmp")
+    srcs = sources()
+    jobs = max(1, min(len(srcs), os.cpu_count() or 1, 16))
+    with tempfile.TemporaryDirectory(prefix="ds355-build-") as work:
+        objects = [Path(work) / (src.stem + ".o") for src in srcs]
+        compiles = [[hipcc(), *flags(), "-c", "-o", str(obj), str(src)] for src, obj in zip(srcs, objects)]
+        with ThreadPoolExecutor(max_workers=jobs) as pool:
+            for future in [pool.submit(_run, cmd, verbose) for cmd in compiles]:
+                future.result()
+        _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *[str(o) for o in objects]], verbose)
     os.replace(tmp, LIBRARY)
     return LIBRARY
 

@@ -4,7 +4,10 @@
 output and ``ValueError`` messages of diffspec/kernels.py:95-150; the Triton
 kernel is replaced by the HIP kernel ``ds_chunk_scores`` (one streaming pass
 over K that multiplies each key row by all query heads of its GQA group and
-fuses the head mean).
+fuses the head mean).  ``softmax_lse=None`` (not in the reference kernel)
+gives the reference's ``chunk_attention_scores`` without an LSE
+(diffspec/runtime.py:321-322): each head is normalised over the row's own
+scored tokens, computed in the same single pass over K.
 """
 
 from __future__ import annotations
@@ -17,7 +20,7 @@ from . import _lib
 def paged_chunk_attention_scores(
     query: torch.Tensor,
     key_cache: torch.Tensor,
-    softmax_lse: torch.Tensor,
+    softmax_lse: torch.Tensor | None,
     block_table: torch.Tensor,
     seq_lens: torch.Tensor,
     *,
@@ -33,7 +36,8 @@ def paged_chunk_attention_scores(
     and seq_lens ``[B]`` -> fp32 ``[B, ceil(max_seq_len / chunk_size)]``;
     chunks past a row's length are 0.  ``head_reduce="max"`` (not in the
     reference) takes the largest weight over heads per token instead of the
-    head mean.
+    head mean.  ``softmax_lse=None`` normalises each head over the row's own
+    tokens (head mean only).
     """
     if query.ndim != 3:
         raise ValueError("query must have shape [batch, query_heads, head_dim]")
@@ -45,8 +49,10 @@ def paged_chunk_attention_scores(
         raise ValueError("query and key head dimensions must match")
     if num_query_heads % num_kv_heads != 0:
         raise ValueError("query heads must be divisible by KV heads")
-    if softmax_lse.numel() != batch_size * num_query_heads:
+    if softmax_lse is not None and softmax_lse.numel() != batch_size * num_query_heads:
         raise ValueError("softmax_lse must contain one value per query head")
+    if softmax_lse is None and head_reduce != "mean":
+        raise ValueError("head_reduce='max' needs a supplied softmax_lse")
     if head_reduce not in ("mean", "max"):
         raise ValueError("head_reduce must be 'mean' or 'max'")
     if query.dtype != key_cache.dtype:
@@ -60,9 +66,11 @@ def paged_chunk_attention_scores(
         query = query.contiguous()
     if key_cache.stride(3) != 1:
         key_cache = key_cache.contiguous()
-    lse = softmax_lse.reshape(batch_size, num_query_heads)
-    if lse.dtype != torch.float32:
-        lse = lse.float()
+    lse = None
+    if softmax_lse is not None:
+        lse = softmax_lse.reshape(batch_size, num_query_heads)
+        if lse.dtype != torch.float32:
+            lse = lse.float()
     table = block_table if block_table.dtype == torch.int32 else block_table.to(torch.int32)
     if table.ndim != 2 or table.stride(1) != 1:
         table = table.reshape(batch_size, -1).contiguous()
@@ -71,12 +79,15 @@ def paged_chunk_attention_scores(
     mode = _lib.DS_HEAD_MAX if head_reduce == "max" else _lib.DS_HEAD_MEAN
     workspace = None
     if mode == _lib.DS_HEAD_MEAN:
-        workspace = torch.empty((batch_size, max_chunks, num_kv_heads), dtype=torch.float32, device=device)
+        # Per-KV-head partials; without an LSE, then a (max, sum) pair per
+        # (chunk, query head).
+        width = num_kv_heads + (2 * num_query_heads if lse is None else 0)
+        workspace = torch.empty((batch_size, max_chunks, width), dtype=torch.float32, device=device)
     _lib.check(lib.ds_chunk_scores(
         _lib.stream_handle(device), _lib.dtype_code(query.dtype),
         query.data_ptr(), query.stride(0),
         key_cache.data_ptr(), key_cache.stride(0), key_cache.stride(1), key_cache.stride(2),
-        lse.data_ptr(), lse.stride(0), lse.stride(1),
+        _lib.ptr(lse), 0 if lse is None else lse.stride(0), 0 if lse is None else lse.stride(1),
         table.data_ptr(), table.stride(0),
         lens.data_ptr(),
         batch_size, num_query_heads, num_kv_heads, head_dim, block_size, chunk_size, max_chunks,

@@ -110,6 +110,13 @@ class DiffSpecDraftCache:
     Constructor arguments follow diffspec/runtime.py:599-613.
     ``rotary_embedding`` supplies ``rotary_dim``, ``is_neox_style`` and
     either ``cos_sin_cache`` or ``_match_cos_sin_cache_dtype(x)``.
+    ``lse_free_scoring`` (not in the reference) keeps a verifier snapshot
+    whose attention backend returned no softmax LSE: scoring then computes
+    each query head's LSE over the row's scored tokens in the same pass over
+    K (the reference's ``chunk_attention_scores`` with ``softmax_lse=None``,
+    runtime.py:321-322) and leaves it in ``scored_lse``.  Without it a
+    snapshot with no LSE is dropped, as the reference does
+    (runtime.py:850-851).
     """
 
     def __init__(
@@ -127,6 +134,7 @@ class DiffSpecDraftCache:
         target_cos_sin_cache: torch.Tensor | None = None,
         target_tensor_parallel_size: int = 1,
         max_batch_rows: int | None = None,
+        lse_free_scoring: bool = False,
     ) -> None:
         if target_tensor_parallel_size < 1:
             raise ValueError("Target tensor parallel size must be positive")
@@ -163,6 +171,11 @@ class DiffSpecDraftCache:
         rows = self.max_batch_rows
         self.scores = torch.zeros((rows, self.max_chunks), dtype=torch.float32, device=self.device)
         self._score_partials: torch.Tensor | None = None  # [rows, max_chunks, target KV heads], on first use
+        self.lse_free_scoring = lse_free_scoring
+        # Without a snapshot LSE: (max, sum) pairs [rows, Hq, max_chunks, 2]
+        # and the computed natural-log LSE [rows, Hq], on first use.
+        self._lse_partials: torch.Tensor | None = None
+        self.scored_lse: torch.Tensor | None = None
         self.plan = torch.zeros((rows, _plan_width(settings.token_budget, settings.chunk_size)),
                                 dtype=torch.int64, device=self.device)
         self._rows_staging = _Staging(5, rows, self.device)
@@ -267,8 +280,11 @@ class DiffSpecDraftCache:
         metadata: Any,
         scale: float,
     ) -> None:
-        """Keep the last verifier layer's query, LSE and paged K (no copies of K)."""
-        if softmax_lse is None or key_cache is None:
+        """Keep the last verifier layer's query, LSE and paged K (no copies of K).
+
+        A missing LSE drops the snapshot unless ``lse_free_scoring`` is set.
+        """
+        if key_cache is None or (softmax_lse is None and not self.lse_free_scoring):
             return
         query_ends = list(getattr(metadata, "actual_seq_lengths_q", ()))
         seq_lens = list(getattr(metadata, "seq_lens_list", ()))
@@ -276,14 +292,14 @@ class DiffSpecDraftCache:
         if not query_ends or not seq_lens or block_tables is None:
             return
         is_prefill = bool(getattr(metadata, "num_prefills", 1))
-        lse = self._reshape_target_lse(query, softmax_lse)
+        lse = None if softmax_lse is None else self._reshape_target_lse(query, softmax_lse)
         if is_prefill:
             index = torch.tensor([end - 1 for end in query_ends], dtype=torch.long, device=query.device)
-            lse = lse.index_select(0, index)
+            lse = None if lse is None else lse.index_select(0, index)
             query = query.index_select(0, index)
             query_ends = list(range(1, len(query_ends) + 1))
         self._target_query = query.detach()
-        self._target_lse = lse.detach()
+        self._target_lse = None if lse is None else lse.detach()
         self._target_key_cache = key_cache
         self._target_block_tables = block_tables[: len(seq_lens)]
         self._target_query_ends = query_ends
@@ -597,6 +613,15 @@ class DiffSpecDraftCache:
                 self._score_partials = torch.zeros((self.max_batch_rows, self.max_chunks, kv_heads),
                                                    dtype=torch.float32, device=self.device)
             partials = self._score_partials[:batch_rows]
+        lse_partials = lse_out = None
+        if stages & _step.SCORE and snapshot.lse is None:
+            q_heads = snapshot.query.shape[1]
+            if self._lse_partials is None or self._lse_partials.shape[1] != q_heads:
+                self._lse_partials = torch.zeros((self.max_batch_rows, q_heads, self.max_chunks, 2),
+                                                 dtype=torch.float32, device=self.device)
+                self.scored_lse = torch.zeros((self.max_batch_rows, q_heads), dtype=torch.float32,
+                                              device=self.device)
+            lse_partials, lse_out = self._lse_partials[:batch_rows], self.scored_lse[:batch_rows]
         _step.retrieval_step(
             stages=stages, snapshot=snapshot, rows=rows,
             scores=self.scores[:batch_rows] if stages & (_step.SCORE | _step.SELECT) else None,
@@ -607,7 +632,7 @@ class DiffSpecDraftCache:
             working_key=self.working_key, working_value=self.working_value,
             cos_sin_cache=cos_sin, rotary_dim=rotary.rotary_dim, is_neox_style=rotary.is_neox_style,
             chunk_size=self.settings.chunk_size, history_budget=self.history_budget,
-            recent_window=self.recent_window,
+            recent_window=self.recent_window, lse_partials=lse_partials, lse_out=lse_out,
         )
 
     def _cos_sin_cache(self) -> torch.Tensor:

@@ -30,12 +30,15 @@ def _i32(name: str, t: torch.Tensor, n: int | None = None) -> torch.Tensor:
 class VerifierSnapshot:
     """Target last-layer state used for scoring (runtime.py:841-878).
 
-    query ``[tokens, Hq, D]``; lse viewed as ``[tokens, Hq]`` (any strides);
-    key_cache ``[blocks, block_size, Hkv, D]``; block_table ``[rows, *]`` int32.
+    query ``[tokens, Hq, D]``; lse viewed as ``[tokens, Hq]`` (any strides),
+    or None: scoring then computes each query head's LSE over the row's
+    scored tokens (the reference's ``chunk_attention_scores`` with
+    ``softmax_lse=None``, runtime.py:321-322); key_cache ``[blocks,
+    block_size, Hkv, D]``; block_table ``[rows, *]`` int32.
     """
 
     query: torch.Tensor
-    lse: torch.Tensor
+    lse: torch.Tensor | None
     key_cache: torch.Tensor
     block_table: torch.Tensor
     scale: float
@@ -108,6 +111,8 @@ def build_step_desc(
     recent_window: int | None = None,
     row_active: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
+    lse_partials: torch.Tensor | None = None,
+    lse_out: torch.Tensor | None = None,
 ) -> tuple[_lib.StepDesc, torch.device]:
     """Validate and pack a step descriptor for ``stages`` (``SCORE | SELECT | PLAN``; ``ALL`` = one step).
 
@@ -118,6 +123,10 @@ def build_step_desc(
     per-KV-head sums SCORE writes and SELECT reads).  PLAN writes ``plan`` and
     gathers.  ``workspace`` (from ``new_workspace``) lets a full step run as
     one launch when its shapes allow it; the results are the same.
+
+    Without a snapshot LSE, SCORE needs ``lse_partials`` (``[batch_rows, Hq,
+    max_chunks, 2]`` fp32 scratch: each chunk's (max, sum) per query head) and may write ``lse_out`` (``[batch_rows, Hq]`` fp32, each
+    scored row's natural-log LSE); such a step runs as the kernel chain.
     """
     if stages & ~ALL:
         raise ValueError(f"unknown stage bits {stages:#x}")
@@ -186,8 +195,21 @@ def build_step_desc(
             raise ValueError("query heads must be divisible by KV heads")
         if q.stride(2) != 1 or q.stride(1) != q.shape[2] or kc.stride(3) != 1:
             raise ValueError("query and key cache rows must be contiguous")
-        if lse.dtype != torch.float32 or lse.ndim != 2 or lse.shape != q.shape[:2]:
+        if lse is not None and (lse.dtype != torch.float32 or lse.ndim != 2 or lse.shape != q.shape[:2]):
             raise ValueError("target softmax LSE does not match target query shape")
+        if lse is None and stages & SCORE:
+            hq = q.shape[1]
+            if (lse_partials is None or lse_partials.dtype != torch.float32 or not lse_partials.is_contiguous()
+                    or lse_partials.shape != (batch_rows, hq, scores.shape[1], 2)):
+                raise ValueError("without a softmax LSE, lse_partials must be a contiguous fp32 "
+                                 "[batch_rows, query_heads, max_chunks, 2] buffer")
+            if lse_out is not None and (lse_out.dtype != torch.float32 or lse_out.ndim != 2
+                                        or lse_out.shape != (batch_rows, hq) or lse_out.stride(1) != 1):
+                raise ValueError("lse_out must be fp32 [batch_rows, query_heads] with unit head stride")
+            tensors += [lse_partials, lse_out]
+            desc.lse_partials = lse_partials.data_ptr()
+            desc.lse_out = _lib.ptr(lse_out)
+            desc.lse_out_stride = 0 if lse_out is None else lse_out.stride(0)
         if bt.dtype != torch.int32 or bt.ndim != 2 or bt.stride(1) != 1 or bt.shape[0] < batch_rows:
             raise ValueError("block_table must be int32 [rows, blocks] with unit last stride")
         if q.dtype != kc.dtype:
@@ -197,7 +219,8 @@ def build_step_desc(
         tensors += [q, lse, kc, bt]
         desc.dtype = _lib.dtype_code(q.dtype)
         desc.query, desc.q_stride = q.data_ptr(), q.stride(0)
-        desc.lse, desc.lse_token_stride, desc.lse_head_stride = lse.data_ptr(), lse.stride(0), lse.stride(1)
+        if lse is not None:
+            desc.lse, desc.lse_token_stride, desc.lse_head_stride = lse.data_ptr(), lse.stride(0), lse.stride(1)
         desc.key_cache = kc.data_ptr()
         desc.k_block_stride, desc.k_token_stride, desc.k_head_stride = kc.stride(0), kc.stride(1), kc.stride(2)
         desc.block_size = kc.shape[1]

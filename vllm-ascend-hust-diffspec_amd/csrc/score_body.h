@@ -317,7 +317,7 @@ __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_pr
         m4 = fmaxf(m4, __shfl_xor(m4, 32, 64));
 #pragma unroll
         for (int t = 0; t < kMaxNtu; ++t) {
-          if (t == tg) tmax[t] = fmaxf(tmax[t], m4);
+          tmax[t] = t == tg ? fmaxf(tmax[t], m4) : tmax[t];  // a select: tmax stays in registers
         }
       } else if constexpr (LSEFREE) {
         if (ci != cur) {  // wave-uniform

@@ -22,6 +22,7 @@ import platform
 import statistics
 import sys
 import time
+import types
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
@@ -354,6 +355,7 @@ def run(args):
 
     attention_leg = draft_attention_leg(spec, states, rows, hb, device, reps, args.seed, not args.no_cpu_baseline)
     capture_leg = draft_capture_leg(spec, copies, states, rows, device, reps, args.seed)
+    host_leg = runtime_host_leg(spec, inp0, hb, device)
 
     cpu = None if args.no_cpu_baseline else cpu_baseline(spec, copies[0], cos_sin, hb, rows_t, active, reuse)
     if cpu is not None:
@@ -409,6 +411,7 @@ def run(args):
         "lse_free_scoring": lse_free_leg,
         "draft_attention": attention_leg,
         "draft_capture": capture_leg,
+        "runtime_host": host_leg,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result, ensure_ascii=False), flush=True)
@@ -560,6 +563,86 @@ def draft_capture_leg(spec, copies, states, rows, device, reps, seed):
         "avg_us": round(us, 2),
         "algorithmic_bytes": moved,
         "note": "one launch per draft step; the reference builds index tensors on the host and runs torch index ops",
+    }
+
+
+def runtime_host_leg(spec, inp, hb, device, cycles=40):
+    """Host time of DiffSpecDraftCache's calls over whole draft cycles.
+
+    One cycle: verifier snapshot, retrieval (SCORE | SELECT), draft cycle
+    start, compact prefill (PLAN), then K = 4 draft steps of raw-KV capture
+    and draft attention.  Each call is timed on the host without a
+    synchronisation (launches are asynchronous); the cycle time ends with
+    one.  Medians after 5 warm-up cycles, in µs.
+    """
+    import torch
+
+    from ds355 import runtime
+
+    rows, hkv, d, hq = inp["rows"], spec["hkv"], spec["d"], spec["hq"]
+
+    class Rotary:
+        rotary_dim = d
+        is_neox_style = True
+
+    inv = 1.0 / (ROPE_THETA ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    freqs = torch.outer(torch.arange(spec["budget"], dtype=torch.float32), inv)
+    rotary = Rotary()
+    rotary.cos_sin_cache = torch.cat((freqs.cos(), freqs.sin()), -1).to(torch.bfloat16).to(device)
+    settings = runtime.DiffSpecSettings(chunk_size=spec["chunk"], token_budget=spec["budget"], retrieval_interval=1,
+                                        max_tree_nodes=4, max_tree_depth=DRAFT_TOKENS, tree_threshold=0.7,
+                                        adaptive_profile=False, recent_window=spec.get("window", RECENT_WINDOW))
+    cache = runtime.DiffSpecDraftCache(settings, max_num_reqs=rows, max_model_len=inp["lmax"], num_kv_heads=hkv,
+                                       head_dim=d, target_num_layers=2, dtype=torch.bfloat16, device=device,
+                                       rotary_embedding=rotary)
+    ids = [f"request-{i}" for i in range(rows)]
+    ends = [s + q for s, q in zip(inp["starts"], inp["qlens"])][:rows]
+    meta = types.SimpleNamespace(actual_seq_lengths_q=ends, seq_lens_list=inp["tlens"][:rows],
+                                 block_tables=inp["table"][:rows], num_prefills=0)
+    counts = torch.tensor(inp["counts"][:rows], dtype=torch.int32, device=device)
+    g = torch.Generator(device=device).manual_seed(5)
+    q = torch.randn((rows, hq, d), generator=g, device=device).to(torch.bfloat16)
+    k = torch.randn((rows, hkv * d), generator=g, device=device).to(torch.bfloat16)
+    v = torch.randn((rows, hkv, d), generator=g, device=device).to(torch.bfloat16)
+    out = torch.empty((rows, hq * d), dtype=torch.bfloat16, device=device)
+    pos = torch.tensor([max(c - 1, 0) for c in inp["committed"][:rows]], dtype=torch.int64, device=device)
+    names = ("capture_target_attention", "accept_target_queries", "prepare_compact_prefill", "capture_raw_kv",
+             "forward_attention", "cycle")
+    times = {n: [] for n in names}
+
+    def timed(name, fn):
+        t = time.perf_counter()
+        fn()
+        times[name].append((time.perf_counter() - t) * 1e6)
+
+    for it in range(cycles + 5):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        cache.begin_target_forward(ids)
+        timed("capture_target_attention", lambda: cache.capture_target_attention(
+            inp["query"][: ends[-1]], inp["lse"][: ends[-1]], inp["key_cache"], meta, inp["scale"]))
+        timed("accept_target_queries", lambda: cache.accept_target_queries(counts, is_prefill=False))
+        cache.begin_cycle(ids)
+        timed("prepare_compact_prefill", lambda: cache.prepare_compact_prefill(
+            meta, rows, committed_seq_lens=inp["committed"][:rows]))
+        for step_i in range(DRAFT_TOKENS):
+            if step_i:
+                cache.prepare_draft_step()
+            timed("capture_raw_kv", lambda: cache.capture_raw_kv(0, pos + step_i, k, v))
+            timed("forward_attention", lambda: cache.forward_attention(q, k, v, inp["scale"], out))
+        cache.end_cycle()
+        torch.cuda.synchronize()
+        times["cycle"].append((time.perf_counter() - t0) * 1e6)
+        if it == 4:
+            for n in names:
+                times[n].clear()
+    result = {n: round(statistics.median(xs), 1) for n, xs in times.items()}
+    del cache
+    return {
+        "what": f"host µs per DiffSpecDraftCache call, median over {cycles} draft cycles of {rows} requests "
+                f"(retrieval, compact prefill, {DRAFT_TOKENS} draft steps); 'cycle' is the wall time of a "
+                f"whole cycle ending with one synchronisation",
+        **result,
     }
 
 

@@ -191,3 +191,21 @@ def test_retrieval_step_replayed_from_a_graph(cuda, path):
             assert step.workspace_epoch(graphed["workspace"]) == replay + 1
         if replay == 0:  # the captured inputs: the oracle's step
             check_step(case, graphed)
+
+
+def test_launches_use_torch_current_stream(cuda):
+    """Every entry point launches on torch's current stream: the default one, a side stream, a capture."""
+    from ds355 import _lib
+
+    assert _lib.stream_handle(cuda) == torch.cuda.current_stream(cuda).cuda_stream
+    side = torch.cuda.Stream(cuda)
+    with torch.cuda.stream(side):
+        assert _lib.stream_handle(cuda) == side.cuda_stream != torch.cuda.default_stream(cuda).cuda_stream
+    x = torch.zeros(4, device=cuda)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        assert _lib.stream_handle(cuda) == torch.cuda.current_stream(cuda).cuda_stream
+        x.add_(1)
+    graph.replay()
+    torch.cuda.synchronize()
+    assert x.tolist() == [1.0] * 4

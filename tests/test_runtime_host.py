@@ -113,6 +113,17 @@ def test_retrieval_skips_prefill_snapshot_and_interval(launches):
     assert len(launches) == 1
 
 
+def test_slot_map_is_uploaded_only_when_it_changes():
+    """Draft steps of one cycle reuse the device slot row; a new order re-uploads it."""
+    cache = _cache()
+    first = cache._device_slots([2, 0, 1])
+    uploads = cache._slot_map.index
+    again = cache._device_slots([2, 0, 1])
+    assert cache._slot_map.index == uploads and again.data_ptr() == first.data_ptr()
+    assert again.tolist() == [2, 0, 1]
+    assert cache._device_slots([0, 1]).tolist() == [0, 1] and cache._slot_map.index != uploads
+
+
 def test_snapshot_without_lse(launches):
     """A backend that returns no LSE: dropped as the reference does (runtime.py:850-851),
     or, with lse_free_scoring, kept and scored with per-row LSE buffers."""

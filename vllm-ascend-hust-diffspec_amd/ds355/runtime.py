@@ -80,24 +80,27 @@ class _Staging:
     def __init__(self, fields: int, rows: int, device: torch.device, depth: int = 4) -> None:
         pin = device.type == "cuda"
         self.host = [torch.zeros((fields, rows), dtype=torch.int32, pin_memory=pin) for _ in range(depth)]
-        self.events: list[torch.cuda.Event | None] = [None] * depth
+        self.host_np = [h.numpy() for h in self.host]  # list -> pinned buffer without a temporary tensor
+        self.events = [torch.cuda.Event() for _ in range(depth)] if pin else None
+        self.recorded = [False] * depth
+        self.device_index = device.index if device.index is not None else (torch.cuda.current_device() if pin else 0)
         self.device = torch.zeros((fields, rows), dtype=torch.int32, device=device)
         self.index = 0
 
     def upload(self, columns: list[list[int]]) -> torch.Tensor:
         i = self.index
         self.index = (i + 1) % len(self.host)
-        if self.events[i] is not None:
+        if self.recorded[i]:
             self.events[i].synchronize()  # only waits if the GPU is a full ring behind
-        buf = self.host[i]
+        buf = self.host_np[i]
         for f, values in enumerate(columns):
-            if values:
-                buf[f, : len(values)] = torch.tensor(values, dtype=torch.int32)
-        self.device.copy_(buf, non_blocking=True)
-        if self.device.device.type == "cuda":
-            event = torch.cuda.Event()
-            event.record()
-            self.events[i] = event
+            if len(values):
+                buf[f, : len(values)] = values
+        self.device.copy_(self.host[i], non_blocking=True)
+        if self.events is not None:
+            # An explicit stream: record() without one resolves the current device first.
+            self.events[i].record(torch.cuda.current_stream(self.device_index))
+            self.recorded[i] = True
         return self.device
 
 
@@ -181,6 +184,10 @@ class DiffSpecDraftCache:
         self._rows_staging = _Staging(5, rows, self.device)
         self._plan_staging = _Staging(2, rows, self.device)
         self._attention_staging = _Staging(2, max_num_reqs, self.device)
+        # Row order of slots as a device array, re-uploaded only when it changes
+        # (a draft cycle's steps all use the same one).
+        self._slot_map = _Staging(1, max_num_reqs, self.device)
+        self._slot_map_list: list[int] | None = None
 
         self.retrieval_interval = settings.retrieval_interval
         self.metrics = DiffSpecRuntimeMetrics()
@@ -419,6 +426,16 @@ class DiffSpecDraftCache:
             rows.append(row)
         return rows
 
+    def _device_slots(self, slots: list[int]) -> torch.Tensor:
+        """``slots`` as an int32 device row (at most max_num_reqs entries).
+
+        The copy is stream-ordered, so launches already queued keep reading
+        the previous contents."""
+        if self._slot_map_list != slots:
+            self._slot_map.upload([slots])
+            self._slot_map_list = list(slots)
+        return self._slot_map.device[0, : len(slots)]
+
     def _rope_buffer(self, dtype: torch.dtype) -> torch.Tensor:
         buffer = self._rope_position_buffers.get(dtype)
         if buffer is None:
@@ -480,8 +497,7 @@ class DiffSpecDraftCache:
             self.prepare_compact_prefill(metadata, num_tokens, committed_seq_lens=seq_lens)
             self._compact_prefill = False
             self._draft_step -= 1
-        staged = self._attention_staging.upload([slots, []]) if len(slots) <= self.max_num_reqs else None
-        token_slots = staged[0, : len(slots)] if staged is not None else torch.tensor(
+        token_slots = self._device_slots(slots) if len(slots) <= self.max_num_reqs else torch.tensor(
             slots, dtype=torch.int32, device=self.device)
         dtype = absolute_positions.dtype
         buffer = self._rope_buffer(dtype)
@@ -582,10 +598,9 @@ class DiffSpecDraftCache:
                 raise RuntimeError("DiffSpec working cache exhausted")
         slot_rows: Any = []
         if rows:
-            staged = self._attention_staging.upload([list(slots), positions if isinstance(positions, list) else []])
-            slot_rows = staged[0, :rows]
+            slot_rows = self._device_slots(list(slots))
             if isinstance(positions, list):
-                positions = staged[1, :rows]
+                positions = self._attention_staging.upload([[], positions])[1, :rows]
         _attention.draft_linear_attention(
             query, key, value, output, self.working_key, self.working_value, self.working_lens,
             slot_rows, positions, scale=scale, workspace=workspace,

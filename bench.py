@@ -248,6 +248,8 @@ def run(args):
     step_us = time_stage(step.ALL, reps)
     score_us = time_stage(step.SCORE, reps)
     select_us = time_stage(step.SELECT, reps)
+    # The runtime's retrieval call (SCORE | SELECT): one launch with a workspace.
+    score_select_us = time_stage(step.SCORE | step.SELECT, reps)
     plan_gather_us = time_stage(step.PLAN, reps)
 
     # Gather alone through its C entry point (prebuilt arguments, so host
@@ -400,6 +402,7 @@ def run(args):
         "path": ("single launch (fused_step_kernel)" if fused else
                  "three-kernel chain" + (" (batch below the single launch's 8 rows)" if args.path == "fused" else "")),
         "kernels_us": {"step": round(step_us, 2), "chunk_score": round(score_us, 2), "select": round(select_us, 2),
+                       "score_and_select": round(score_select_us, 2),
                        "plan_and_gather": round(plan_gather_us, 2), "gather": round(gather_us, 2)},
         "score_roofline": {"achieved": round(score_gbps, 1), "frac": round(score_gbps / HBM_PEAK_GBPS, 4),
                            "algorithmic_bytes": score_bytes},

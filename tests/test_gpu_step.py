@@ -281,3 +281,53 @@ def test_lse_free_step_equals_supplied_lse(cuda, path, seed, hq, hkv, head_dim, 
     torch.testing.assert_close(lse_out[rows_idx], case["lse"][q_index], rtol=1e-5, atol=1e-4)
     unscored = [b for b in range(case["rows"]) if b not in rows_idx]
     assert torch.isnan(lse_out[unscored]).all()  # rows that are not scored are left alone
+
+
+@pytest.mark.parametrize("lse_free", [False, True])
+def test_runtime_retrieval_and_rebuild_match_oracle(cuda, lse_free):
+    """DiffSpecDraftCache end to end: verifier snapshot -> accept_target_queries (score +
+    select) -> prepare_compact_prefill (plan + gather), against the oracle's step.  With
+    lse_free_scoring the snapshot carries no LSE."""
+    from types import SimpleNamespace
+
+    from ds355 import runtime
+
+    g = gen(21)
+    lens = [int(x) for x in torch.randint(3000, 20000, (12,), generator=g)]
+    counts = [int(x) for x in torch.randint(0, 6, (12,), generator=g)]
+    counts[0] = 3
+    case = build_case(21, real_rows=12, pad_rows=0, target_lens=lens, query_len=5, counts=counts, hq=32, hkv=4,
+                      head_dim=128, chunk=64, token_budget=2048, block_size=128, lmax=20000,
+                      slots=list(range(12)), num_slots=12)
+
+    class Rotary:
+        rotary_dim = 128
+        is_neox_style = True
+        cos_sin_cache = case["cos_sin"].to(cuda)
+
+    settings = runtime.DiffSpecSettings(chunk_size=64, token_budget=2048, retrieval_interval=1, max_tree_nodes=4,
+                                        max_tree_depth=4, tree_threshold=0.7, adaptive_profile=False)
+    cache = runtime.DiffSpecDraftCache(settings, max_num_reqs=12, max_model_len=20000, num_kv_heads=4, head_dim=128,
+                                       target_num_layers=2, dtype=torch.bfloat16, device=cuda,
+                                       rotary_embedding=Rotary(), lse_free_scoring=lse_free)
+    cache.raw_key.copy_(case["raw_k"])
+    cache.raw_value.copy_(case["raw_v"])
+    cache.working_key.fill_(float("nan"))
+    cache.working_value.fill_(float("nan"))
+    ids = [f"request-{i}" for i in range(12)]
+    meta = SimpleNamespace(actual_seq_lengths_q=case["ends"], seq_lens_list=case["tlens"],
+                           block_tables=case["table"].to(cuda), num_prefills=0)
+    cache.begin_target_forward(ids)
+    assert cache._active_slots == list(range(12))
+    cache.capture_target_attention(case["query"].to(cuda), None if lse_free else case["lse"].to(cuda),
+                                   case["key_cache"].to(cuda), meta, case["scale"])
+    cache.accept_target_queries(torch.tensor(counts, dtype=torch.int32, device=cuda), is_prefill=False)
+    cache.prepare_compact_prefill(meta, 12, committed_seq_lens=case["committed"])
+    torch.cuda.synchronize()
+    state = dict(scores=cache.scores[:12], sel_ids=cache.sel_ids, sel_count=cache.sel_count, plan=cache.plan[:12],
+                 work_k=cache.working_key, work_v=cache.working_value)
+    check_step(case, state)
+    assert cache.working_lens.cpu().tolist() == cache.plan[:12, 1].cpu().tolist()
+    if lse_free:
+        rows_idx, q_index, _ = O.retrieval_rows(case["counts"], case["ends"], case["tlens"], 12)
+        torch.testing.assert_close(cache.scored_lse[rows_idx].cpu(), case["lse"][q_index], rtol=1e-5, atol=1e-4)

@@ -66,7 +66,8 @@ int ds_abi_version(void);
  * dtype   : DS_BF16 or DS_FP16 (query and key_cache share it).
  * workspace: caller-owned device scratch of batch * max_chunks * Hkv floats
  *           (per-KV-head partial sums; unused with DS_HEAD_MAX), plus
- *           batch * max_chunks * Hq * 2 floats when lse is NULL.  Two
+ *           batch * max_chunks * Hq * 2 floats when lse is NULL (placed
+ *           first, so an 8-byte aligned workspace aligns them).  Two
  *           kernels (three without an LSE): the streaming pass, the LSE
  *           merge and a small finalize pass.
  * Limits  : head_dim % 32 == 0 and <= 256, Hq % Hkv == 0, Hq / Hkv <= 16,

@@ -359,25 +359,31 @@ extern "C" int ds_chunk_scores(ds_stream_t stream, int dtype, const void* query,
   src.seq_lens = seq_lens;
   const bool hmax = head_reduce == DS_HEAD_MAX;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  // Without an LSE the workspace also holds the (max, sum) pairs, after the
-  // per-KV-head partials (a workspace too small for them is reported with
-  // the other argument checks).
+  // Without an LSE the workspace starts with the (max, sum) pairs (8-byte
+  // aligned with the workspace), then the per-KV-head partials; a workspace
+  // too small for both is reported with the other argument checks.
   float* mz = nullptr;
+  float* partial = workspace;
+  size_t partial_bytes = workspace_bytes;
   if (lse == nullptr && !hmax && batch > 0 && max_chunks > 0 && num_q_heads > 0 && num_kv_heads > 0) {
-    const size_t parts = static_cast<size_t>(batch) * max_chunks * num_kv_heads;
-    const size_t need = (parts + static_cast<size_t>(batch) * max_chunks * num_q_heads * 2) * sizeof(float);
-    if (workspace != nullptr && workspace_bytes >= need) mz = workspace + parts;
+    const size_t pairs = static_cast<size_t>(batch) * max_chunks * num_q_heads * 2;
+    const size_t need = (static_cast<size_t>(batch) * max_chunks * num_kv_heads + pairs) * sizeof(float);
+    if (workspace != nullptr && workspace_bytes >= need) {
+      mz = workspace;
+      partial = workspace + pairs;
+      partial_bytes = workspace_bytes - pairs * sizeof(float);
+    }
   }
   int rc = launch_chunk_scores(s, dtype, query, q_stride, key_cache, k_block_stride, k_token_stride, k_head_stride,
                                lse, lse_row_stride, lse_head_stride, block_table, bt_stride, src, batch, num_q_heads,
                                num_kv_heads, head_dim, block_size, chunk_size, max_chunks, scale, head_reduce,
-                               workspace, out, out_stride, 1, workspace_bytes, mz, nullptr, 0);
+                               partial, out, out_stride, 1, partial_bytes, mz, nullptr, 0);
   if (rc != DS_OK || hmax || batch == 0 || max_chunks == 0) return rc;
   DS_REQUIRE(out != nullptr, "null score output pointer");
   const int64_t n = static_cast<int64_t>(batch) * max_chunks;
   const int grid = static_cast<int>(std::min<int64_t>((n + kThreads - 1) / kThreads, 4096));
   const int max_len = static_cast<int>(std::min<int64_t>(static_cast<int64_t>(max_chunks) * chunk_size, INT32_MAX));
-  finalize_kernel<<<grid, kThreads, 0, s>>>(workspace, seq_lens, batch, max_chunks, num_kv_heads, num_q_heads,
+  finalize_kernel<<<grid, kThreads, 0, s>>>(partial, seq_lens, batch, max_chunks, num_kv_heads, num_q_heads,
                                             chunk_size, max_len, out, out_stride);
   return check_launch("ds_chunk_scores finalize");
 }

@@ -79,8 +79,8 @@ def paged_chunk_attention_scores(
     mode = _lib.DS_HEAD_MAX if head_reduce == "max" else _lib.DS_HEAD_MEAN
     workspace = None
     if mode == _lib.DS_HEAD_MEAN:
-        # Per-KV-head partials; without an LSE, then a (max, sum) pair per
-        # (chunk, query head).
+        # Per-KV-head partials; without an LSE, preceded by a (max, sum) pair
+        # per (query head, chunk).
         width = num_kv_heads + (2 * num_query_heads if lse is None else 0)
         workspace = torch.empty((batch_size, max_chunks, width), dtype=torch.float32, device=device)
     _lib.check(lib.ds_chunk_scores(

@@ -65,11 +65,12 @@ int ds_abi_version(void);
  *            k[block * k_block_stride + i * k_token_stride + kvh * k_head_stride + d].
  * dtype   : DS_BF16 or DS_FP16 (query and key_cache share it).
  * workspace: caller-owned device scratch of batch * max_chunks * Hkv floats
- *           (per-KV-head partial sums; unused with DS_HEAD_MAX), plus
- *           batch * max_chunks * Hq * 2 floats when lse is NULL (placed
- *           first, so an 8-byte aligned workspace aligns them).  Two
- *           kernels (three without an LSE): the streaming pass, the LSE
- *           merge and a small finalize pass.
+ *           (per-KV-head partial sums; unused with DS_HEAD_MAX), plus,
+ *           when lse is NULL, batch * max_chunks * Hq * 2 floats of
+ *           (max, sum) pairs and batch * Hq floats of row LSEs (placed
+ *           first, so an 8-byte aligned workspace aligns the pairs).  Two
+ *           kernels (four without an LSE): the streaming pass, the head
+ *           LSEs, the partials and a small finalize pass.
  * Limits  : head_dim % 32 == 0 and <= 256, Hq % Hkv == 0, Hq / Hkv <= 16,
  *           batch <= 1024; DS_HEAD_MAX needs chunk <= 128 or a chunk that
  *           divides 64.
@@ -221,7 +222,7 @@ typedef struct ds_step_desc {
    * query head's LSE over the row's scored tokens (the reference's
    * chunk_attention_scores with softmax_lse=None, diffspec/runtime.py:321-322) */
   float* lse_partials;               /* [batch_rows, Hq, max_chunks, 2] fp32 scratch; required when lse == NULL */
-  float* lse_out;                    /* [batch_rows, Hq] natural-log LSE of each scored row, or NULL */
+  float* lse_out;                    /* [batch_rows, Hq] natural-log LSE of each scored row; required when lse == NULL */
   int64_t lse_out_stride;            /* elements between rows of lse_out */
 } ds_step_desc;
 

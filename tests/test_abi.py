@@ -120,14 +120,15 @@ def test_lse_free_validation_without_gpu():
 
     lib = _lib.load()
     fake = 1 << 12  # 16-byte aligned, never dereferenced
-    # batch 2, Hq 8, Hkv 2, 3 chunks: (2 + 2 * 8) floats per (row, chunk).
-    need = 2 * 3 * (2 + 2 * 8) * 4
+    # batch 2, Hq 8, Hkv 2, 3 chunks: (2 + 2 * 8) floats per (row, chunk) and 8 LSEs per row.
+    need = 2 * (3 * (2 + 2 * 8) + 8) * 4
     args = [None, _lib.DS_BF16, fake, 8 * 128, fake, 16 * 2 * 128, 2 * 128, 128, None, 0, 0, fake, 4, fake,
             2, 8, 2, 128, 16, 64, 3, 1.0, _lib.DS_HEAD_MEAN, fake, 3]
     rc = lib.ds_chunk_scores(*args, fake, 2 * 3 * 2 * 4)  # room for the partials only
     assert rc == _lib.DS_ERR_INVALID
     assert lib.ds_last_error().decode() == (
-        f"workspace too small: need {need} bytes without an LSE (batch * max_chunks * (kv_heads + 2 * q_heads) * 4)")
+        f"workspace too small: need {need} bytes without an LSE "
+        "(batch * (max_chunks * (kv_heads + 2 * q_heads) + q_heads) * 4)")
     args[22] = _lib.DS_HEAD_MAX
     assert lib.ds_chunk_scores(*args, fake, need) == _lib.DS_ERR_UNSUPPORTED
     assert lib.ds_last_error().decode() == "head_reduce=max needs a supplied softmax LSE"
@@ -141,8 +142,12 @@ def test_lse_free_validation_without_gpu():
     desc.max_chunks, desc.scores, desc.score_partials = 4, fake, fake
     desc.num_kv_heads, desc.num_q_heads = 2, 8
     assert lib.ds_retrieval_step(None, desc) == _lib.DS_ERR_INVALID
-    assert lib.ds_last_error().decode() == (
-        "without a softmax LSE the step needs lse_partials ([batch_rows, Hq, max_chunks, 2] fp32)")
+    msg = ("without a softmax LSE the step needs lse_partials ([batch_rows, Hq, max_chunks, 2] fp32) and "
+           "lse_out ([batch_rows, Hq] fp32)")
+    assert lib.ds_last_error().decode() == msg
+    desc.lse_partials = fake  # the LSE output is required too
+    assert lib.ds_retrieval_step(None, desc) == _lib.DS_ERR_INVALID
+    assert lib.ds_last_error().decode() == msg
 
 
 def test_lse_free_host_checks():
@@ -173,8 +178,9 @@ def test_lse_free_host_checks():
     )
     with pytest.raises(ValueError, match="lse_partials must be a contiguous fp32"):
         step.build_step_desc(**common)
-    with pytest.raises(ValueError, match="lse_out must be fp32"):
-        step.build_step_desc(**common, lse_partials=torch.zeros((1, 4, 4, 2)), lse_out=torch.zeros((1, 3)))
+    for bad in (None, torch.zeros((1, 3))):
+        with pytest.raises(ValueError, match="lse_out must be fp32"):
+            step.build_step_desc(**common, lse_partials=torch.zeros((1, 4, 4, 2)), lse_out=bad)
     with pytest.raises(ValueError, match="GPU only"):
         step.build_step_desc(**common, lse_partials=torch.zeros((1, 4, 4, 2)), lse_out=torch.zeros((1, 4)))
 

@@ -134,6 +134,7 @@ struct Batch {
   Raw16 q[STEPS];
   float lse[4];
   BatchCtx c;
+  int fresh;  // q and lse were loaded for this batch (else: the same as the batch before)
 };
 
 // LSEFREE: merge a chunk's running pairs (one per token group slot of a
@@ -208,11 +209,16 @@ __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_pr
     return c;
   };
 
-  // Every load below is issued unconditionally, from wave-uniform bases plus
-  // small per-lane offsets: lanes and batches with nothing to read use a
+  // Every key load below is issued unconditionally, from wave-uniform bases
+  // plus small per-lane offsets: lanes and batches with nothing to read use a
   // valid dummy address (row 0, or a clamped head / in-block row) and
-  // compute() masks them.  Each batch therefore adds a fixed number of loads,
-  // and the wait for the batch being computed never drains the next batch.
+  // compute() masks them.  Each batch therefore adds a fixed number of key
+  // loads, and the wait for the batch being computed never drains the next
+  // batch's keys.  q and the LSE are loaded only by a batch that starts a new
+  // (row, KV head), before its keys (so a wait that covers them is one the
+  // previous batch needed anyway); the other batches of the unit take them
+  // from the batch computed just before (re-loading them every batch cost
+  // about 5 us of a 57 us pass on 16 x 40k-token rows).
   //
   // kb[i] = element offset of token group i's first row for KV head g
   // (uniform: the group lies inside one block).  Reading lanes past the row
@@ -237,8 +243,24 @@ __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_pr
   const int64_t lane_k = static_cast<int64_t>(col) * a.k_token_stride + kgrp * 8;
   const int q_head = min(col, a.G - 1);  // rows >= G read a real head; masked later
 
+  int64_t last_qbase = -1, last_lbase = -1;  // q / LSE of the last loaded batch (wave-uniform)
   auto load = [&](const BatchCtx& c, const int64_t (&kb)[KB], Batch<KB, STEPS>& out) {
     out.c = c;
+    out.fresh = c.qbase != last_qbase || c.lbase != last_lbase;
+    last_qbase = c.qbase;
+    last_lbase = c.lbase;
+    if (out.fresh) {  // wave-uniform; issued before the keys
+      const uint16_t* qh = a.q + c.qbase + static_cast<int64_t>(q_head) * a.D + kgrp * 8;
+#pragma unroll
+      for (int s = 0; s < STEPS; ++s) out.q[s] = *reinterpret_cast<const Raw16*>(qh + 32 * s);
+      if constexpr (!LSEFREE) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = min(4 * kgrp + i, a.G - 1);
+          out.lse[i] = a.lse[c.lbase + static_cast<int64_t>(m) * a.lse_head_stride];
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
       const uint16_t* krow;
@@ -258,15 +280,15 @@ __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_pr
 #pragma unroll
       for (int s = 0; s < STEPS; ++s) out.k[i][s] = *reinterpret_cast<const Raw16*>(krow + 32 * s);
     }
-    const uint16_t* qh = a.q + c.qbase + static_cast<int64_t>(q_head) * a.D + kgrp * 8;
+  };
+  // A batch of the same unit as the one just computed takes its q and LSE
+  // from it (registers the computation has already waited for).
+  auto inherit = [&](Batch<KB, STEPS>& next, const Batch<KB, STEPS>& done) {
+    if (!next.fresh) {  // wave-uniform
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) out.q[s] = *reinterpret_cast<const Raw16*>(qh + 32 * s);
-    if constexpr (!LSEFREE) {
+      for (int s = 0; s < STEPS; ++s) next.q[s] = done.q[s];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = min(4 * kgrp + i, a.G - 1);
-        out.lse[i] = a.lse[c.lbase + static_cast<int64_t>(m) * a.lse_head_stride];
-      }
+      for (int i = 0; i < 4; ++i) next.lse[i] = done.lse[i];
     }
   };
 
@@ -402,11 +424,13 @@ __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_pr
     cx0 = ctx_of(n + 2);
     pages_of(cx0, pg0);
     compute(d0);
+    inherit(d1, d0);
     if (!d1.c.valid) break;
     load(cx0, pg0, d0);
     cx1 = ctx_of(n + 3);
     pages_of(cx1, pg1);
     compute(d1);
+    inherit(d0, d1);
   }
 }
 

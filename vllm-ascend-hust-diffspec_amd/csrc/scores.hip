@@ -29,10 +29,10 @@
 // softmax_lse=None, diffspec/runtime.py:321-322: the LSE of each query head
 // over the row's scored tokens) the same single pass keeps, per lane, a
 // running (max, sum of 2^(logit - max)) per chunk and query head, merges the
-// 16 token lanes with DPP permutes and stores the pairs; lse_finalize_kernel
-// then merges a row's chunks into each head's LSE and writes the usual
-// per-KV-head partials, sum over the group's heads of z * 2^(m - lse), so
-// selection and the drop-in finalize read them unchanged.
+// 16 token lanes with DPP permutes and stores the pairs; lse_heads_kernel
+// then merges a row's chunks into each head's LSE and lse_partials_kernel
+// writes the usual per-KV-head partials, sum over the group's heads of
+// z * 2^(m - lse), so selection and the drop-in finalize read them unchanged.
 #include "score_body.h"
 
 namespace ds355 {
@@ -100,21 +100,64 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(const float* __restr
   }
 }
 
-// One workgroup per (row, KV head, slice of chunks): the LSE of each query
-// head of the group from all of the row's (max, sum) pairs, then that KV
-// head's partial of every chunk of the slice, sum over the group's heads of
-// z * 2^(m - lse).  The slices of a row each recompute the group's LSEs (a
-// few KB of pairs, from L2) so that no second launch or grid-wide wait is
-// needed.  A head's pairs are contiguous: tph threads per head stream them
-// with eight loads in flight and merge by lane shuffles (and LDS when a head
-// spans several waves).
-constexpr int kFinalizeLoads = 8;
-constexpr int kFinalizeSlice = 128;  // chunks per slice
-__global__ __launch_bounds__(kThreads) void lse_finalize_kernel(const float* __restrict__ mz, RowSource src,
-                                                                int max_chunks, int hq, int hkv, int chunk,
-                                                                float* __restrict__ partial, float* __restrict__ lse_out,
-                                                                int64_t lse_stride) {
+// Scores without a supplied LSE, after the pass: two small kernels.
+//   lse_heads_kernel, one workgroup per (row, KV head): each query head of
+//     the group merges all of the row's (max, sum) pairs into its LSE and
+//     writes it (natural log) to lse_out.  A head's pairs are contiguous:
+//     tph threads per head stream them with kLseLoads loads in flight and
+//     merge by lane shuffles (and LDS when a head spans several waves).
+//   lse_partials_kernel, one workgroup per (row, KV head, slice of
+//     kFinalizeSlice chunks): the KV head's partial of every chunk of the
+//     slice, sum over the group's heads of z * 2^(m - lse), which selection
+//     and the drop-in finalize read as with a supplied LSE.
+// Every pair is read once by each kernel, however long the row.
+constexpr int kLseLoads = 16;
+constexpr int kFinalizeSlice = 128;  // chunks per partials workgroup
+__global__ __launch_bounds__(kThreads) void lse_heads_kernel(const float* __restrict__ mz, RowSource src,
+                                                             int max_chunks, int hq, int hkv, int chunk,
+                                                             float* __restrict__ lse_out, int64_t lse_stride) {
   __shared__ float s_m[kThreads], s_z[kThreads];
+  const int b = blockIdx.x / hkv, g = blockIdx.x % hkv;
+  const RowDesc d = row_desc(src, b);
+  const int len = d.active ? d.len : 0;
+  if (len <= 0) return;  // workgroup-uniform
+  const int chunks = (len + chunk - 1) / chunk;
+  const int G = hq / hkv;
+  const int t = threadIdx.x;
+  int tph = 1;  // threads per head: a power of two, tph * G <= kThreads
+  while (tph * 2 * G <= kThreads) tph *= 2;
+  const int hl = t / tph, j = t % tph;
+  float m = -INFINITY, z = 0.f;
+  if (hl < G) {
+    const float2* p = reinterpret_cast<const float2*>(mz) + (static_cast<int64_t>(b) * hq + g * G + hl) * max_chunks;
+    for (int c0 = j; c0 < chunks; c0 += kLseLoads * tph) {
+      float2 v[kLseLoads];
+#pragma unroll
+      for (int u = 0; u < kLseLoads; ++u) {
+        const int c = c0 + u * tph;
+        v[u] = c < chunks ? p[c] : make_float2(-INFINITY, 0.f);
+      }
+#pragma unroll
+      for (int u = 0; u < kLseLoads; ++u) merge_mz(m, z, v[u].x, v[u].y);
+    }
+  }
+  const int span = tph < 64 ? tph : 64;
+  for (int off = 1; off < span; off <<= 1) merge_mz(m, z, __shfl_xor(m, off, 64), __shfl_xor(z, off, 64));
+  s_m[t] = m;
+  s_z[t] = z;
+  __syncthreads();
+  if (t < G) {
+    float mh = -INFINITY, zh = 0.f;
+    for (int k = 0; k < tph; k += 64) merge_mz(mh, zh, s_m[t * tph + k], s_z[t * tph + k]);
+    const float lse2 = zh > 0.f ? mh + __log2f(zh) : -INFINITY;
+    lse_out[static_cast<int64_t>(b) * lse_stride + g * G + t] = lse2 * 0.69314718055994530942f;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void lse_partials_kernel(const float* __restrict__ mz, RowSource src,
+                                                                int max_chunks, int hq, int hkv, int chunk,
+                                                                const float* __restrict__ lse, int64_t lse_stride,
+                                                                float* __restrict__ partial) {
   __shared__ float s_lse2[kMaxGroup];
   const int slices = (max_chunks + kFinalizeSlice - 1) / kFinalizeSlice;
   const int s = blockIdx.x % slices;
@@ -128,38 +171,9 @@ __global__ __launch_bounds__(kThreads) void lse_finalize_kernel(const float* __r
   const int c_end = min(chunks, c_begin + kFinalizeSlice);
   const int G = hq / hkv;
   const int t = threadIdx.x;
+  if (t < G) s_lse2[t] = lse[static_cast<int64_t>(b) * lse_stride + g * G + t] * 1.44269504088896340736f;
+  __syncthreads();
   const float2* pairs = reinterpret_cast<const float2*>(mz) + (static_cast<int64_t>(b) * hq + g * G) * max_chunks;
-
-  int tph = 1;  // threads per head: a power of two, tph * G <= kThreads
-  while (tph * 2 * G <= kThreads) tph *= 2;
-  const int hl = t / tph, j = t % tph;
-  float m = -INFINITY, z = 0.f;
-  if (hl < G) {
-    const float2* p = pairs + static_cast<int64_t>(hl) * max_chunks;
-    for (int c0 = j; c0 < chunks; c0 += kFinalizeLoads * tph) {
-      float2 v[kFinalizeLoads];
-#pragma unroll
-      for (int u = 0; u < kFinalizeLoads; ++u) {
-        const int c = c0 + u * tph;
-        v[u] = c < chunks ? p[c] : make_float2(-INFINITY, 0.f);
-      }
-#pragma unroll
-      for (int u = 0; u < kFinalizeLoads; ++u) merge_mz(m, z, v[u].x, v[u].y);
-    }
-  }
-  const int span = tph < 64 ? tph : 64;
-  for (int off = 1; off < span; off <<= 1) merge_mz(m, z, __shfl_xor(m, off, 64), __shfl_xor(z, off, 64));
-  s_m[t] = m;
-  s_z[t] = z;
-  __syncthreads();
-  if (t < G) {
-    float mh = -INFINITY, zh = 0.f;
-    for (int k = 0; k < tph; k += 64) merge_mz(mh, zh, s_m[t * tph + k], s_z[t * tph + k]);
-    const float lse2 = zh > 0.f ? mh + __log2f(zh) : -INFINITY;
-    s_lse2[t] = lse2;
-    if (lse_out && s == 0) lse_out[static_cast<int64_t>(b) * lse_stride + g * G + t] = lse2 * 0.69314718055994530942f;
-  }
-  __syncthreads();
   for (int c = c_begin + t; c < c_end; c += kThreads) {
     float2 v[kMaxGroup];
 #pragma unroll
@@ -169,7 +183,7 @@ __global__ __launch_bounds__(kThreads) void lse_finalize_kernel(const float* __r
     float sum = 0.f;
 #pragma unroll
     for (int h = 0; h < kMaxGroup; ++h) {
-      if (v[h].x != -INFINITY) sum += v[h].y * __builtin_amdgcn_exp2f(v[h].x - s_lse2[h]);
+      if (v[h].x != -INFINITY && s_lse2[h] != -INFINITY) sum += v[h].y * __builtin_amdgcn_exp2f(v[h].x - s_lse2[h]);
     }
     partial[(static_cast<int64_t>(b) * max_chunks + c) * hkv + g] = sum;
   }
@@ -248,9 +262,10 @@ int make_score_args(ScoreArgs& a, int64_t& upper_units, bool& uniform_page, int 
   // No LSE: the pass computes it (head mean only); the pairs need mz.
   DS_SUPPORTED(lse || !hmax, "head_reduce=max needs a supplied softmax LSE");
   DS_REQUIRE(lse || mz,
-             "workspace too small: need %zu bytes without an LSE (batch * max_chunks * (kv_heads + 2 * q_heads) * 4)",
-             static_cast<size_t>(batch) * max_chunks * (num_kv_heads + 2 * static_cast<size_t>(num_q_heads)) *
-                 sizeof(float));
+             "workspace too small: need %zu bytes without an LSE (batch * (max_chunks * (kv_heads + 2 * q_heads) + "
+             "q_heads) * 4)",
+             static_cast<size_t>(batch) *
+                 (max_chunks * (num_kv_heads + 2 * static_cast<size_t>(num_q_heads)) + num_q_heads) * sizeof(float));
   if (!hmax) {
     const size_t need = static_cast<size_t>(batch) * max_chunks * num_kv_heads * sizeof(float);
     DS_REQUIRE(partial != nullptr && partial_bytes >= need,
@@ -323,6 +338,8 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
                                  max_chunks, scale, head_reduce, partial, out, out_stride, write_tail, partial_bytes,
                                  mz);
   if (rc != DS_OK || upper_units == 0) return rc;
+  DS_REQUIRE(lse != nullptr || lse_out != nullptr, "null LSE output pointer (the scores without a supplied LSE "
+                                                   "compute it there)");
   const bool hmax = head_reduce == DS_HEAD_MAX;
   const bool lse_free = lse == nullptr;
   const int64_t upper_blocks = (upper_units + kWaves - 1) / kWaves;
@@ -337,12 +354,16 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
   }
   int rc2 = check_launch("ds_chunk_scores");
   if (rc2 != DS_OK || !lse_free) return rc2;
+  lse_heads_kernel<<<batch * num_kv_heads, kThreads, 0, stream>>>(a.mz, a.src, max_chunks, num_q_heads,
+                                                                  num_kv_heads, chunk_size, lse_out, lse_out_stride);
+  rc2 = check_launch("ds_chunk_scores lse");
+  if (rc2 != DS_OK) return rc2;
   const int64_t grid = static_cast<int64_t>(batch) * num_kv_heads * ((max_chunks + kFinalizeSlice - 1) / kFinalizeSlice);
   DS_SUPPORTED(grid < (int64_t{1} << 31), "too many (row, KV head, chunk slice) workgroups");
-  lse_finalize_kernel<<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(a.mz, a.src, max_chunks, num_q_heads,
-                                                                            num_kv_heads, chunk_size, partial, lse_out,
-                                                                            lse_out_stride);
-  return check_launch("ds_chunk_scores lse");
+  lse_partials_kernel<<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(a.mz, a.src, max_chunks, num_q_heads,
+                                                                            num_kv_heads, chunk_size, lse_out,
+                                                                            lse_out_stride, partial);
+  return check_launch("ds_chunk_scores partials");
 }
 
 }  // namespace ds355
@@ -359,25 +380,29 @@ extern "C" int ds_chunk_scores(ds_stream_t stream, int dtype, const void* query,
   src.seq_lens = seq_lens;
   const bool hmax = head_reduce == DS_HEAD_MAX;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  // Without an LSE the workspace starts with the (max, sum) pairs (8-byte
-  // aligned with the workspace), then the per-KV-head partials; a workspace
-  // too small for both is reported with the other argument checks.
+  // Without an LSE the workspace holds the (max, sum) pairs first (8-byte
+  // aligned with the workspace), then each row's LSE ([batch, Hq]), then the
+  // per-KV-head partials; a workspace too small for all three is reported
+  // with the other argument checks.
   float* mz = nullptr;
+  float* lse_rows = nullptr;
   float* partial = workspace;
   size_t partial_bytes = workspace_bytes;
   if (lse == nullptr && !hmax && batch > 0 && max_chunks > 0 && num_q_heads > 0 && num_kv_heads > 0) {
     const size_t pairs = static_cast<size_t>(batch) * max_chunks * num_q_heads * 2;
-    const size_t need = (static_cast<size_t>(batch) * max_chunks * num_kv_heads + pairs) * sizeof(float);
+    const size_t lses = static_cast<size_t>(batch) * num_q_heads;
+    const size_t need = (static_cast<size_t>(batch) * max_chunks * num_kv_heads + pairs + lses) * sizeof(float);
     if (workspace != nullptr && workspace_bytes >= need) {
       mz = workspace;
-      partial = workspace + pairs;
-      partial_bytes = workspace_bytes - pairs * sizeof(float);
+      lse_rows = workspace + pairs;
+      partial = lse_rows + lses;
+      partial_bytes = workspace_bytes - (pairs + lses) * sizeof(float);
     }
   }
   int rc = launch_chunk_scores(s, dtype, query, q_stride, key_cache, k_block_stride, k_token_stride, k_head_stride,
                                lse, lse_row_stride, lse_head_stride, block_table, bt_stride, src, batch, num_q_heads,
                                num_kv_heads, head_dim, block_size, chunk_size, max_chunks, scale, head_reduce,
-                               partial, out, out_stride, 1, partial_bytes, mz, nullptr, 0);
+                               partial, out, out_stride, 1, partial_bytes, mz, lse_rows, num_q_heads);
   if (rc != DS_OK || hmax || batch == 0 || max_chunks == 0) return rc;
   DS_REQUIRE(out != nullptr, "null score output pointer");
   const int64_t n = static_cast<int64_t>(batch) * max_chunks;

@@ -1,7 +1,8 @@
 // One retrieval step on one stream: the single-launch kernel (fused.hip)
 // when the descriptor brings a workspace and fits it, otherwise a chain:
 //   chunk_score_kernel (rows with committed tokens; committed query; rejected
-//   suffix cut; without a softmax LSE, plus lse_finalize_kernel) ->
+//   suffix cut; without a softmax LSE, plus lse_heads_kernel and
+//   lse_partials_kernel) ->
 //   select_plan_kernel (selection into the per-slot state, then a plan row
 //   for every real row) -> gather kernel over the plan.
 // No host synchronisation; launch shapes depend only on the descriptor's
@@ -66,8 +67,9 @@ extern "C" int ds_retrieval_step(ds_stream_t stream_handle, const ds_step_desc* 
     DS_REQUIRE(d->num_kv_heads > 0 && d->num_q_heads > 0, "head counts must be positive");
   }
   if (score) {
-    DS_REQUIRE(d->lse != nullptr || d->lse_partials != nullptr,
-               "without a softmax LSE the step needs lse_partials ([batch_rows, Hq, max_chunks, 2] fp32)");
+    DS_REQUIRE(d->lse != nullptr || (d->lse_partials != nullptr && d->lse_out != nullptr),
+               "without a softmax LSE the step needs lse_partials ([batch_rows, Hq, max_chunks, 2] fp32) and "
+               "lse_out ([batch_rows, Hq] fp32)");
   }
   src.max_len = static_cast<int>(std::min<int64_t>(static_cast<int64_t>(d->max_chunks) * d->chunk_size, INT32_MAX));
   bool launched = false;

@@ -80,9 +80,11 @@ def paged_chunk_attention_scores(
     workspace = None
     if mode == _lib.DS_HEAD_MEAN:
         # Per-KV-head partials; without an LSE, preceded by a (max, sum) pair
-        # per (query head, chunk).
-        width = num_kv_heads + (2 * num_query_heads if lse is None else 0)
-        workspace = torch.empty((batch_size, max_chunks, width), dtype=torch.float32, device=device)
+        # per (query head, chunk) and each row's head LSEs.
+        size = batch_size * max_chunks * num_kv_heads
+        if lse is None:
+            size += batch_size * (max_chunks * 2 * num_query_heads + num_query_heads)
+        workspace = torch.empty(size, dtype=torch.float32, device=device)
     _lib.check(lib.ds_chunk_scores(
         _lib.stream_handle(device), _lib.dtype_code(query.dtype),
         query.data_ptr(), query.stride(0),

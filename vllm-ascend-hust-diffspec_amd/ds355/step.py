@@ -125,8 +125,9 @@ def build_step_desc(
     one launch when its shapes allow it; the results are the same.
 
     Without a snapshot LSE, SCORE needs ``lse_partials`` (``[batch_rows, Hq,
-    max_chunks, 2]`` fp32 scratch: each chunk's (max, sum) per query head) and may write ``lse_out`` (``[batch_rows, Hq]`` fp32, each
-    scored row's natural-log LSE); such a step runs as the kernel chain.
+    max_chunks, 2]`` fp32 scratch: each chunk's (max, sum) per query head)
+    and ``lse_out`` (``[batch_rows, Hq]`` fp32, where each scored row's
+    natural-log LSE is written); such a step runs as the kernel chain.
     """
     if stages & ~ALL:
         raise ValueError(f"unknown stage bits {stages:#x}")
@@ -203,13 +204,13 @@ def build_step_desc(
                     or lse_partials.shape != (batch_rows, hq, scores.shape[1], 2)):
                 raise ValueError("without a softmax LSE, lse_partials must be a contiguous fp32 "
                                  "[batch_rows, query_heads, max_chunks, 2] buffer")
-            if lse_out is not None and (lse_out.dtype != torch.float32 or lse_out.ndim != 2
-                                        or lse_out.shape != (batch_rows, hq) or lse_out.stride(1) != 1):
-                raise ValueError("lse_out must be fp32 [batch_rows, query_heads] with unit head stride")
+            if lse_out is None or (lse_out.dtype != torch.float32 or lse_out.ndim != 2
+                                   or lse_out.shape != (batch_rows, hq) or lse_out.stride(1) != 1):
+                raise ValueError("without a softmax LSE, lse_out must be fp32 [batch_rows, query_heads] "
+                                 "with unit head stride")
             tensors += [lse_partials, lse_out]
             desc.lse_partials = lse_partials.data_ptr()
-            desc.lse_out = _lib.ptr(lse_out)
-            desc.lse_out_stride = 0 if lse_out is None else lse_out.stride(0)
+            desc.lse_out, desc.lse_out_stride = lse_out.data_ptr(), lse_out.stride(0)
         if bt.dtype != torch.int32 or bt.ndim != 2 or bt.stride(1) != 1 or bt.shape[0] < batch_rows:
             raise ValueError("block_table must be int32 [rows, blocks] with unit last stride")
         if q.dtype != kc.dtype:

@@ -10,6 +10,13 @@ not hit in the 256 MB Infinity Cache.
 Prints ONE JSON line.  The default workload is the 16-request ragged batch
 (context lengths uniform in [4096, 40960], 4 KV heads x 128, 32 query heads,
 chunk 64, token budget 2048, K = 4 draft tokens -> 1984 history tokens).
+
+Besides the step (value, roofline, per-stage kernel times, cpu_baseline) the
+line carries the path's neighbours on the same inputs: the scores without a
+supplied LSE (lse_free_scoring), the draft decode attention over the working
+caches the step gathered (draft_attention), the raw-KV capture of one draft
+token per row (draft_capture) and the host time of the runtime's calls over
+whole draft cycles (runtime_host).
 """
 
 from __future__ import annotations

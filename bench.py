@@ -307,8 +307,10 @@ def run(args):
         key = "fused_kernel_hbm_bytes_per_launch" if fused else "score_kernel_hbm_bytes_per_launch"
         traffic = json.loads(traffic_file.read_text()).get(key)
     if fused:
-        # The whole step is one kernel: it is the dominant (and only) one.
-        roof_kernel, roof_bytes, roof_us = "fused_step_kernel", chain_bytes, step_us
+        # The whole step is one kernel: it is the dominant (and only) one, and the
+        # timed region is K back-to-back launches of it, so its average launch
+        # duration is the timed region's average.
+        roof_kernel, roof_bytes, roof_us = "fused_step_kernel", chain_bytes, chain_ms * 1e3
     else:
         roof_kernel, roof_bytes, roof_us = "chunk_score_kernel", score_bytes, score_us
     roof_gbps = roof_bytes / (roof_us * 1e-6) / 1e9

@@ -148,6 +148,12 @@ def test_lse_free_validation_without_gpu():
     desc.lse_partials = fake  # the LSE output is required too
     assert lib.ds_retrieval_step(None, desc) == _lib.DS_ERR_INVALID
     assert lib.ds_last_error().decode() == msg
+    # ... with room for every query head per row, checked before anything is launched.
+    desc.lse_out, desc.lse_out_stride = fake, 4
+    desc.query = desc.key_cache = desc.block_table = fake
+    desc.block_size, desc.head_dim = 16, 128
+    assert lib.ds_retrieval_step(None, desc) == _lib.DS_ERR_INVALID
+    assert lib.ds_last_error().decode() == "LSE output rows must hold every query head"
 
 
 def test_lse_free_host_checks():

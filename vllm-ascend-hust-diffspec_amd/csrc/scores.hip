@@ -338,10 +338,16 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
                                  max_chunks, scale, head_reduce, partial, out, out_stride, write_tail, partial_bytes,
                                  mz);
   if (rc != DS_OK || upper_units == 0) return rc;
-  DS_REQUIRE(lse != nullptr || lse_out != nullptr, "null LSE output pointer (the scores without a supplied LSE "
-                                                   "compute it there)");
   const bool hmax = head_reduce == DS_HEAD_MAX;
   const bool lse_free = lse == nullptr;
+  // Everything the LSE kernels need is checked before the first launch.
+  const int64_t partial_grid =
+      static_cast<int64_t>(batch) * num_kv_heads * ((max_chunks + kFinalizeSlice - 1) / kFinalizeSlice);
+  if (lse_free) {
+    DS_REQUIRE(lse_out != nullptr, "null LSE output pointer (the scores without a supplied LSE compute it there)");
+    DS_REQUIRE(lse_out_stride >= num_q_heads, "LSE output rows must hold every query head");
+    DS_SUPPORTED(partial_grid < (int64_t{1} << 31), "too many (row, KV head, chunk slice) workgroups");
+  }
   const int64_t upper_blocks = (upper_units + kWaves - 1) / kWaves;
   if (dtype == DS_BF16) {
     if (hmax) launch_steps<DS_BF16, true, false>(stream, a, upper_blocks, uniform_page);
@@ -358,9 +364,7 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
                                                                   num_kv_heads, chunk_size, lse_out, lse_out_stride);
   rc2 = check_launch("ds_chunk_scores lse");
   if (rc2 != DS_OK) return rc2;
-  const int64_t grid = static_cast<int64_t>(batch) * num_kv_heads * ((max_chunks + kFinalizeSlice - 1) / kFinalizeSlice);
-  DS_SUPPORTED(grid < (int64_t{1} << 31), "too many (row, KV head, chunk slice) workgroups");
-  lse_partials_kernel<<<static_cast<unsigned>(grid), kThreads, 0, stream>>>(a.mz, a.src, max_chunks, num_q_heads,
+  lse_partials_kernel<<<static_cast<unsigned>(partial_grid), kThreads, 0, stream>>>(a.mz, a.src, max_chunks, num_q_heads,
                                                                             num_kv_heads, chunk_size, lse_out,
                                                                             lse_out_stride, partial);
   return check_launch("ds_chunk_scores partials");

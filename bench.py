@@ -354,8 +354,7 @@ def run(args):
     free_gbps = score_bytes / (free_score_us * 1e-6) / 1e9
     lse_free_leg = {
         "what": "scores without a supplied softmax LSE: chunk_score_kernel keeps (max, sum) pairs, "
-                "lse_heads_kernel merges them into each head's LSE and lse_partials_kernel writes the "
-                "per-KV-head partials",
+                "lse_finalize_kernel merges them into each head's LSE and writes the per-KV-head partials",
         "score_us": round(free_score_us, 2), "step_us": round(free_step_us, 2),
         "score_us_with_lse": round(score_us, 2),
         "achieved_gbps": round(free_gbps, 1), "frac": round(free_gbps / HBM_PEAK_GBPS, 4),

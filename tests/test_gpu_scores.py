@@ -186,6 +186,28 @@ def test_lse_free_large_logits_stay_finite(cuda):
     torch.testing.assert_close(actual, expected, rtol=1e-3, atol=1e-6)
 
 
+def test_lse_free_long_rows_take_wider_slices(cuda):
+    """Rows of up to 2500 chunks: a (row, KV head) finalizes in at most 8 workgroups, so each
+    takes slices wider than its 256 threads (chunks t and t + 256 of the slice)."""
+    g = gen(13)
+    lengths = [40000, 23000, 17, 4097, 16 * 1024 + 1]
+    query = randn((len(lengths), 8, 64), torch.bfloat16, g)
+    key_cache, table = paged_keys(lengths, 2, 64, 256, torch.bfloat16, g)
+    scale = default_scale(64)
+    actual = _gpu_scores(query, key_cache, None, table, lengths, 16, scale, cuda)
+    expected = O.paged_chunk_attention_scores(query, key_cache, None, table, torch.tensor(lengths), chunk_size=16,
+                                              max_seq_len=max(lengths), scale=scale)
+    torch.testing.assert_close(actual, expected, rtol=1e-3, atol=1e-6)
+    lse = lse_for(query, key_cache, table, lengths, scale)
+    supplied = _gpu_scores(query, key_cache, lse, table, lengths, 16, scale, cuda)
+    torch.testing.assert_close(actual, supplied, rtol=1e-3, atol=1e-6)
+    for b, n in enumerate(lengths):  # a row's chunk masses add up to one
+        c = (n + 15) // 16
+        sizes = torch.full((c,), 16.0)
+        sizes[-1] = n - (c - 1) * 16
+        assert abs(float((actual[b, :c].double() * sizes.double()).sum()) - 1.0) < 2e-3
+
+
 def test_lse_free_headline_shape_scores(cuda):
     """16 requests, L ~ U[4096, 40960], 32 q heads / 4 KV heads x 128, chunk 64, no LSE."""
     g = gen(0)

@@ -29,9 +29,8 @@
 // softmax_lse=None, diffspec/runtime.py:321-322: the LSE of each query head
 // over the row's scored tokens) the same single pass keeps, per lane, a
 // running (max, sum of 2^(logit - max)) per chunk and query head, merges the
-// 16 token lanes with DPP permutes and stores the pairs; lse_heads_kernel
-// then merges a row's chunks into each head's LSE and lse_partials_kernel
-// writes the usual per-KV-head partials, sum over the group's heads of
+// 16 token lanes with DPP permutes and stores the pairs; lse_finalize_kernel
+// then merges a row's chunks into each head's LSE and writes the usual per-KV-head partials, sum over the group's heads of
 // z * 2^(m - lse), so selection and the drop-in finalize read them unchanged.
 #include "score_body.h"
 
@@ -100,36 +99,55 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(const float* __restr
   }
 }
 
-// Scores without a supplied LSE, after the pass: two small kernels.
-//   lse_heads_kernel, one workgroup per (row, KV head): each query head of
-//     the group merges all of the row's (max, sum) pairs into its LSE and
-//     writes it (natural log) to lse_out.  A head's pairs are contiguous:
-//     tph threads per head stream them with kLseLoads loads in flight and
-//     merge by lane shuffles (and LDS when a head spans several waves).
-//   lse_partials_kernel, one workgroup per (row, KV head, slice of
-//     kFinalizeSlice chunks): the KV head's partial of every chunk of the
-//     slice, sum over the group's heads of z * 2^(m - lse), which selection
-//     and the drop-in finalize read as with a supplied LSE.
-// Every pair is read once by each kernel, however long the row.
+// Scores without a supplied LSE, after the pass: lse_finalize_kernel, one
+// workgroup per (row, KV head, slice of finalize_slice(max_chunks) chunks:
+// 128, more when a row would need more than kMaxSlices slices).
+//   - Each query head of the group merges all of the row's (max, sum) pairs
+//     into its LSE.  A head's pairs are contiguous: tph threads per head
+//     stream them with kLseLoads loads in flight and merge by lane shuffles
+//     (and LDS when a head spans several waves).  The slice-0 workgroup
+//     writes the LSEs (natural log) to lse_out.
+//   - Then the KV head's partial of every chunk of the slice, sum over the
+//     group's heads of z * 2^(m - lse), which selection and the drop-in
+//     finalize read as with a supplied LSE.  The exponent uses the LSE as
+//     written (natural log, fp32) times log2(e).
+// Every slice of a row repeats the merge (its pairs come from L2 after the
+// first), which costs less than a second launch waiting on the first; the
+// cap on slices bounds the repeats at kMaxSlices reads of a row's pairs.
 constexpr int kLseLoads = 16;
-constexpr int kFinalizeSlice = 128;  // chunks per partials workgroup
-__global__ __launch_bounds__(kThreads) void lse_heads_kernel(const float* __restrict__ mz, RowSource src,
-                                                             int max_chunks, int hq, int hkv, int chunk,
-                                                             float* __restrict__ lse_out, int64_t lse_stride) {
+constexpr int kFinalizeSlice = 128;  // chunks per workgroup, at least
+constexpr int kMaxSlices = 8;        // workgroups per (row, KV head), at most
+__host__ __device__ inline int finalize_slice(int max_chunks) {
+  const int even = (max_chunks + kMaxSlices - 1) / kMaxSlices;
+  return even > kFinalizeSlice ? even : kFinalizeSlice;
+}
+__global__ __launch_bounds__(kThreads) void lse_finalize_kernel(const float* __restrict__ mz, RowSource src,
+                                                                int max_chunks, int hq, int hkv, int chunk,
+                                                                float* __restrict__ lse_out, int64_t lse_stride,
+                                                                float* __restrict__ partial) {
   __shared__ float s_m[kThreads], s_z[kThreads];
-  const int b = blockIdx.x / hkv, g = blockIdx.x % hkv;
+  __shared__ float s_lse2[kMaxGroup];
+  const int slice = finalize_slice(max_chunks);
+  const int slices = (max_chunks + slice - 1) / slice;
+  const int s = blockIdx.x % slices;
+  const int g = (blockIdx.x / slices) % hkv;
+  const int b = blockIdx.x / slices / hkv;
   const RowDesc d = row_desc(src, b);
   const int len = d.active ? d.len : 0;
-  if (len <= 0) return;  // workgroup-uniform
   const int chunks = (len + chunk - 1) / chunk;
+  const int c_begin = s * slice;
+  if (c_begin >= chunks) return;  // workgroup-uniform (also rows with nothing scored)
+  const int c_end = min(chunks, c_begin + slice);
   const int G = hq / hkv;
   const int t = threadIdx.x;
+  const float2* pairs = reinterpret_cast<const float2*>(mz) + (static_cast<int64_t>(b) * hq + g * G) * max_chunks;
+
   int tph = 1;  // threads per head: a power of two, tph * G <= kThreads
   while (tph * 2 * G <= kThreads) tph *= 2;
   const int hl = t / tph, j = t % tph;
   float m = -INFINITY, z = 0.f;
   if (hl < G) {
-    const float2* p = reinterpret_cast<const float2*>(mz) + (static_cast<int64_t>(b) * hq + g * G + hl) * max_chunks;
+    const float2* p = pairs + static_cast<int64_t>(hl) * max_chunks;
     for (int c0 = j; c0 < chunks; c0 += kLseLoads * tph) {
       float2 v[kLseLoads];
 #pragma unroll
@@ -150,30 +168,12 @@ __global__ __launch_bounds__(kThreads) void lse_heads_kernel(const float* __rest
     float mh = -INFINITY, zh = 0.f;
     for (int k = 0; k < tph; k += 64) merge_mz(mh, zh, s_m[t * tph + k], s_z[t * tph + k]);
     const float lse2 = zh > 0.f ? mh + __log2f(zh) : -INFINITY;
-    lse_out[static_cast<int64_t>(b) * lse_stride + g * G + t] = lse2 * 0.69314718055994530942f;
+    const float lse = lse2 * 0.69314718055994530942f;
+    if (s == 0) lse_out[static_cast<int64_t>(b) * lse_stride + g * G + t] = lse;
+    s_lse2[t] = lse * 1.44269504088896340736f;
   }
-}
-
-__global__ __launch_bounds__(kThreads) void lse_partials_kernel(const float* __restrict__ mz, RowSource src,
-                                                                int max_chunks, int hq, int hkv, int chunk,
-                                                                const float* __restrict__ lse, int64_t lse_stride,
-                                                                float* __restrict__ partial) {
-  __shared__ float s_lse2[kMaxGroup];
-  const int slices = (max_chunks + kFinalizeSlice - 1) / kFinalizeSlice;
-  const int s = blockIdx.x % slices;
-  const int g = (blockIdx.x / slices) % hkv;
-  const int b = blockIdx.x / slices / hkv;
-  const RowDesc d = row_desc(src, b);
-  const int len = d.active ? d.len : 0;
-  const int chunks = (len + chunk - 1) / chunk;
-  const int c_begin = s * kFinalizeSlice;
-  if (c_begin >= chunks) return;  // workgroup-uniform (also rows with nothing scored)
-  const int c_end = min(chunks, c_begin + kFinalizeSlice);
-  const int G = hq / hkv;
-  const int t = threadIdx.x;
-  if (t < G) s_lse2[t] = lse[static_cast<int64_t>(b) * lse_stride + g * G + t] * 1.44269504088896340736f;
   __syncthreads();
-  const float2* pairs = reinterpret_cast<const float2*>(mz) + (static_cast<int64_t>(b) * hq + g * G) * max_chunks;
+
   for (int c = c_begin + t; c < c_end; c += kThreads) {
     float2 v[kMaxGroup];
 #pragma unroll
@@ -340,9 +340,10 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
   if (rc != DS_OK || upper_units == 0) return rc;
   const bool hmax = head_reduce == DS_HEAD_MAX;
   const bool lse_free = lse == nullptr;
-  // Everything the LSE kernels need is checked before the first launch.
+  // Everything the LSE kernel needs is checked before the first launch.
   const int64_t partial_grid =
-      static_cast<int64_t>(batch) * num_kv_heads * ((max_chunks + kFinalizeSlice - 1) / kFinalizeSlice);
+      static_cast<int64_t>(batch) * num_kv_heads *
+      ((max_chunks + finalize_slice(max_chunks) - 1) / finalize_slice(max_chunks));
   if (lse_free) {
     DS_REQUIRE(lse_out != nullptr, "null LSE output pointer (the scores without a supplied LSE compute it there)");
     DS_REQUIRE(lse_out_stride >= num_q_heads, "LSE output rows must hold every query head");
@@ -360,14 +361,9 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
   }
   int rc2 = check_launch("ds_chunk_scores");
   if (rc2 != DS_OK || !lse_free) return rc2;
-  lse_heads_kernel<<<batch * num_kv_heads, kThreads, 0, stream>>>(a.mz, a.src, max_chunks, num_q_heads,
-                                                                  num_kv_heads, chunk_size, lse_out, lse_out_stride);
-  rc2 = check_launch("ds_chunk_scores lse");
-  if (rc2 != DS_OK) return rc2;
-  lse_partials_kernel<<<static_cast<unsigned>(partial_grid), kThreads, 0, stream>>>(a.mz, a.src, max_chunks, num_q_heads,
-                                                                            num_kv_heads, chunk_size, lse_out,
-                                                                            lse_out_stride, partial);
-  return check_launch("ds_chunk_scores partials");
+  lse_finalize_kernel<<<static_cast<unsigned>(partial_grid), kThreads, 0, stream>>>(
+      a.mz, a.src, max_chunks, num_q_heads, num_kv_heads, chunk_size, lse_out, lse_out_stride, partial);
+  return check_launch("ds_chunk_scores lse");
 }
 
 }  // namespace ds355

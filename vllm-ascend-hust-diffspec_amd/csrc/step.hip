@@ -1,8 +1,7 @@
 // One retrieval step on one stream: the single-launch kernel (fused.hip)
 // when the descriptor brings a workspace and fits it, otherwise a chain:
 //   chunk_score_kernel (rows with committed tokens; committed query; rejected
-//   suffix cut; without a softmax LSE, plus lse_heads_kernel and
-//   lse_partials_kernel) ->
+//   suffix cut; without a softmax LSE, plus lse_finalize_kernel) ->
 //   select_plan_kernel (selection into the per-slot state, then a plan row
 //   for every real row) -> gather kernel over the plan.
 // No host synchronisation; launch shapes depend only on the descriptor's

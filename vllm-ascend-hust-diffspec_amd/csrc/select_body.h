@@ -112,8 +112,12 @@ typedef uint32_t U4 __attribute__((ext_vector_type(4)));
 // ascending, into sh.ids[0..K).  key4_at(q) returns the keys of candidates
 // 4q .. 4q + 3 (values past N are ignored).  Starts and ends on a
 // barrier-separated LDS state; requires N + 1 > K.
-//   - Four 8-bit MSB radix passes (LDS histogram, block scan over the bins)
-//     find T, the (K-1)-th largest key.  A thread reads 4 keys at a time.
+//   - Up to four 8-bit MSB radix passes (LDS histogram, block scan over the
+//     bins) find T, the (K-1)-th largest key.  A thread reads 4 keys at a
+//     time.  A pass whose bin holding the (K-1)-th key is taken whole ends
+//     the search: T is then that bin's prefix with the low bits zero, every
+//     key of the bin is > T or == T, and all ties are taken, so the
+//     selected set is the one the remaining passes would have found.
 //   - Compaction: wave w owns the contiguous candidates
 //     [w * span, (w + 1) * span), 256 at a time, lane l holding candidates
 //     4l .. 4l + 3 of each 256.  A first sweep counts keys > T and ties
@@ -150,8 +154,9 @@ __device__ __forceinline__ void select_top(SelectShared<KEYS>& sh, int N, int K,
       prefix |= static_cast<uint32_t>(sh.digit) << shift;
       pmask |= 0xffu << shift;
       need -= sh.above;
-      if (shift == 0) take_all_ties = (need == sh.eq);
+      take_all_ties = need == sh.eq;  // the last pass decides; an earlier one may end the search
       lds_barrier();
+      if (take_all_ties) break;  // workgroup-uniform: every thread read the same counts
     }
   }
   // need = ties (key == T) still to take, lowest indices first.

@@ -237,6 +237,12 @@ def run(args):
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t_wall) * 1e3
     chain_ms = start.elapsed_time(stop) / args.steps
+    if single:
+        # Every timed launch must have completed its waits: a launch whose
+        # bounded wait expired leaves a status bit and invalid results.
+        status = [step.workspace_status(st["workspace"]) for st in states]
+        if any(status):
+            raise RuntimeError(f"single-launch status words {status} after the timed steps: results not valid")
 
     # Per-kernel durations with HIP events on the launch stream.
     def time_stage(stages, reps):

@@ -224,7 +224,21 @@ typedef struct ds_step_desc {
   float* lse_partials;               /* [batch_rows, Hq, max_chunks, 2] fp32 scratch; required when lse == NULL */
   float* lse_out;                    /* [batch_rows, Hq] natural-log LSE of each scored row; required when lse == NULL */
   int64_t lse_out_stride;            /* elements between rows of lse_out */
+  int flags;                         /* DS_STEP_* bits; 0 for normal use */
 } ds_step_desc;
+
+/*
+ * ds_step_desc.flags, for tests of the single launch's rare paths; 0 in
+ * normal use.
+ *   DS_STEP_SELECTORS_GATHER: the scoring waves leave every gather task to
+ *     the selecting workgroups, the path a task takes when its scoring wave
+ *     gave up waiting for the plan.  Same results, slower.
+ *   DS_STEP_EXPIRE_WAITS: every selector reports an expired wait (status
+ *     bit 0), so the launch's bounded waits stop early and its results are
+ *     not valid; every wave still finishes.  Tests that one launch's expiry
+ *     is handed to the owner's status word and does not reach the next.
+ */
+enum ds_step_flags { DS_STEP_SELECTORS_GATHER = 1, DS_STEP_EXPIRE_WAITS = 2 };
 
 int ds_retrieval_step(ds_stream_t stream, const ds_step_desc* desc);
 
@@ -234,9 +248,11 @@ int ds_retrieval_step(ds_stream_t stream, const ds_step_desc* desc);
  * hand-over state (64 header bytes; a tagged copy of each plan row, 128
  * 8-byte columns per row; a 4-byte state per gather task,
  * ceil(token_budget / 8) per row, rounded up to 256 bytes; tagged score
- * partials [batch_rows, max_chunks, num_kv_heads] x 8 bytes).  A workspace serves one launch at a time; word 2
- * of its header is a status word that stays 0 unless a wait of the fused
- * kernel expired (then that launch's results are not valid).
+ * partials [batch_rows, max_chunks, num_kv_heads] x 8 bytes).  A workspace
+ * serves one launch at a time.  Word 2 of its header is the owner's status
+ * word: 0 unless a bounded wait of a single launch expired since the owner
+ * last cleared it (then that launch's results are not valid); each launch
+ * ORs its own bits in when it ends and never clears it.
  */
 size_t ds_step_workspace_bytes(int batch_rows, int max_chunks, int num_kv_heads, int token_budget);
 
@@ -321,6 +337,9 @@ size_t ds_draft_attention_workspace_bytes(int batch_rows, int num_q_heads, int n
  *       neither              : positions[t];
  *   rope_positions[t] = 0 for count <= t < prev_count (the previous call's
  *                              stale tail).
+ * tokens <= count, or count == 0: the scatter alone, with no RoPE input
+ * (DiffSpecDraftCache.populate_prefill, diffspec/runtime.py:1336-1347,
+ * which writes the draft's projected prefill rows, rejected ones included).
  * positions, local_positions and rope_positions are int32, or int64 when
  * positions_int64 != 0.  key/value rows: element (t, h, d) at
  * t * row_stride + h * head_stride + d.  raw caches: [num_slots,

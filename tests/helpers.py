@@ -72,5 +72,34 @@ def default_scale(head_dim: int) -> float:
     return 1.0 / math.sqrt(head_dim)
 
 
+SCORE_RTOL = 1e-3  # chunk scores: within 1e-3 relative of the oracle, chunk by chunk
+SCORE_FLOOR = 1e-12  # absolute slack for masses at the fp32 underflow edge (0.1% of a 1e-9 mass)
+
+
+def assert_scores_close(actual: torch.Tensor, expected: torch.Tensor, rtol: float = SCORE_RTOL,
+                        what: str = "scores") -> float:
+    """Every chunk score within ``rtol`` of the oracle's, relative to that chunk's own value.
+
+    ``|actual - expected| <= rtol * |expected| + 1e-12``: at 40k tokens a chunk
+    holds about 2.5e-5 of the mass, so an absolute tolerance of the usual size
+    would hide errors of several percent.  Zero chunks (beyond a row) must be
+    zero.  Returns the largest relative error among chunks of mass >= 1e-9,
+    which is printed.
+    """
+    a = actual.detach().float().cpu()
+    e = expected.detach().float().cpu()
+    assert a.shape == e.shape, (a.shape, e.shape)
+    err = (a - e).abs()
+    bad = ~(err <= rtol * e.abs() + SCORE_FLOOR)  # NaN counts as bad
+    mask = e.abs() >= 1e-9
+    worst = float((err[mask] / e[mask].abs()).max()) if mask.any() else 0.0
+    print(f"{what}: {int(mask.sum())} chunks, max relative error {worst:.3e}")
+    if bad.any():
+        i = int(bad.reshape(-1).nonzero()[0])
+        raise AssertionError(f"{what}: {int(bad.sum())} chunks outside {rtol} relative; first at flat index {i}: "
+                             f"{float(a.reshape(-1)[i])!r} vs {float(e.reshape(-1)[i])!r}")
+    return worst
+
+
 __all__ = ["O", "gen", "randn", "rope_table_recipe", "paged_keys", "lse_for", "uniform_lengths",
-           "max_ulp_bf16", "default_scale"]
+           "max_ulp_bf16", "default_scale", "assert_scores_close", "SCORE_RTOL"]

@@ -96,3 +96,43 @@ def test_fused_fp16_and_gptj(cuda, dtype, neox, head_dim):
     check_step(case, fused)
     chain = run_gpu(case, cuda, path="chain")
     _same(chain, fused)
+
+
+def test_selectors_gather_every_task(cuda):
+    """The recovery path of the single launch, for every gather task: a scoring
+    wave that stops waiting for its row's plan marks the task skipped and the
+    row's selector does it.  Forced from the host (no scorer waits at all);
+    the bytes equal the chain's and the status stays 0."""
+    from ds355 import step
+
+    case = _ragged(17, 12, 1000, 20000)
+    chain = run_gpu(case, cuda, path="chain")
+    fused = run_gpu(case, cuda, path="fused", flags=step.SELECTORS_GATHER)
+    _same(chain, fused)
+    check_step(case, fused)
+
+
+def test_expired_wait_stays_with_its_launch(cuda):
+    """A launch whose wait expired (forced from the host: every selector reports
+    one) leaves its bit in the owner's status word and nothing in the launch
+    word; the next launch on the same workspace runs its waits in full and
+    equals the chain bit for bit, and clearing the owner's word works."""
+    from ds355 import step
+
+    case = _ragged(18, 10, 1000, 16000)
+    chain = run_gpu(case, cuda, path="chain")
+    state = run_gpu(case, cuda, path="fused", flags=step.EXPIRE_WAITS, expect_status=None)
+    expired = step.workspace_status(state["workspace"])
+    assert expired & 1  # bit 1 may join it: the launch's other waits stop early too
+    for key in ("work_k", "work_v"):
+        state[key].fill_(float("nan"))
+    state["sel_count"].fill_(-1)
+    run_gpu(case, cuda, state=state, path="fused", expect_status=expired)  # the owner has not cleared it
+    _same(chain, state)
+    step.clear_workspace_status(state["workspace"])
+    for key in ("work_k", "work_v"):
+        state[key].fill_(float("nan"))
+    state["sel_count"].fill_(-1)
+    run_gpu(case, cuda, state=state, path="fused")
+    _same(chain, state)
+    assert step.workspace_epoch(state["workspace"]) == 3

@@ -12,7 +12,7 @@ per-row logsumexp.
 import pytest
 import torch
 
-from helpers import O, default_scale, gen, lse_for, paged_keys, randn, uniform_lengths
+from helpers import O, assert_scores_close, default_scale, gen, lse_for, paged_keys, randn, uniform_lengths
 
 pytestmark = pytest.mark.gpu
 
@@ -51,12 +51,12 @@ def test_paged_scores_match_dense_bf16_gqa(cuda, block_size, num_query_heads, nu
             reference[chunk] = probabilities[:, chunk * chunk_size:(chunk + 1) * chunk_size].mean()
         references.append(reference)
     actual = _gpu_scores(query, keys, torch.stack(normalizers), tables, lengths, chunk_size, scale, cuda)
-    torch.testing.assert_close(actual, torch.stack(references), rtol=1e-3, atol=1e-6)
+    assert_scores_close(actual, torch.stack(references))
     assert torch.isfinite(actual).all()
     oracle = O.paged_chunk_attention_scores(query, keys, torch.stack(normalizers), tables,
                                             torch.tensor(lengths), chunk_size=chunk_size,
                                             max_seq_len=max(lengths), scale=scale)
-    torch.testing.assert_close(actual, oracle, rtol=1e-3, atol=1e-6)
+    assert_scores_close(actual, oracle)
 
 
 def test_zero_keys_give_uniform_mass(cuda):
@@ -70,7 +70,7 @@ def test_zero_keys_give_uniform_mass(cuda):
         expected = torch.zeros((2, chunks))
         for row, length in enumerate(lengths):
             expected[row, : (length + 15) // 16] = 1.0 / length
-        torch.testing.assert_close(actual, expected, rtol=1e-3, atol=1e-6)
+        assert_scores_close(actual, expected)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -86,7 +86,7 @@ def test_ragged_batch_matches_oracle(cuda, dtype, head_dim, chunk, block_size):
     actual = _gpu_scores(query, key_cache, lse, table, lengths, chunk, scale, cuda)
     expected = O.paged_chunk_attention_scores(query, key_cache, lse, table, torch.tensor(lengths), chunk_size=chunk,
                                               max_seq_len=max(lengths), scale=scale)
-    torch.testing.assert_close(actual, expected, rtol=1e-3, atol=1e-6)
+    assert_scores_close(actual, expected)
 
 
 def test_head_reduce_max_matches_oracle(cuda):
@@ -99,7 +99,7 @@ def test_head_reduce_max_matches_oracle(cuda):
     actual = _gpu_scores(query, key_cache, lse, table, lengths, 64, scale, cuda, head_reduce="max")
     expected = O.paged_chunk_attention_scores(query, key_cache, lse, table, torch.tensor(lengths), chunk_size=64,
                                               max_seq_len=max(lengths), scale=scale, head_reduce="max")
-    torch.testing.assert_close(actual, expected, rtol=1e-3, atol=1e-6)
+    assert_scores_close(actual, expected)
 
 
 def test_headline_shape_scores(cuda):
@@ -113,7 +113,7 @@ def test_headline_shape_scores(cuda):
     actual = _gpu_scores(query, key_cache, lse, table, lengths, 64, scale, cuda)
     expected = O.paged_chunk_attention_scores(query, key_cache, lse, table, torch.tensor(lengths), chunk_size=64,
                                               max_seq_len=max(lengths), scale=scale)
-    torch.testing.assert_close(actual, expected, rtol=1e-3, atol=1e-6)
+    assert_scores_close(actual, expected)
     # Size-independent property: the chunk masses of a row, weighted by the
     # chunk sizes, sum to 1 (a softmax with the exact LSE).
     for b, n in enumerate(lengths):
@@ -152,11 +152,11 @@ def test_lse_free_ragged_batch_matches_oracle(cuda, dtype, head_dim, chunk, bloc
     actual = _gpu_scores(query, key_cache, None, table, lengths, chunk, scale, cuda)
     expected = O.paged_chunk_attention_scores(query, key_cache, None, table, torch.tensor(lengths), chunk_size=chunk,
                                               max_seq_len=max(lengths), scale=scale)
-    torch.testing.assert_close(actual, expected, rtol=1e-3, atol=1e-6)
+    assert_scores_close(actual, expected)
     # The same scores as with the exact LSE supplied.
     lse = lse_for(query, key_cache, table, lengths, scale)
     supplied = _gpu_scores(query, key_cache, lse, table, lengths, chunk, scale, cuda)
-    torch.testing.assert_close(actual, supplied, rtol=1e-3, atol=1e-6)
+    assert_scores_close(actual, supplied)
 
 
 def test_lse_free_zero_keys_give_uniform_mass(cuda):
@@ -169,7 +169,7 @@ def test_lse_free_zero_keys_give_uniform_mass(cuda):
         expected = torch.zeros((2, chunks))
         for row, length in enumerate(lengths):
             expected[row, : (length + 15) // 16] = 1.0 / length
-        torch.testing.assert_close(actual, expected, rtol=1e-3, atol=1e-6)
+        assert_scores_close(actual, expected)
 
 
 def test_lse_free_large_logits_stay_finite(cuda):
@@ -183,7 +183,7 @@ def test_lse_free_large_logits_stay_finite(cuda):
     assert torch.isfinite(actual).all()
     expected = O.paged_chunk_attention_scores(query, key_cache, None, table, torch.tensor(lengths), chunk_size=64,
                                               max_seq_len=max(lengths), scale=scale)
-    torch.testing.assert_close(actual, expected, rtol=1e-3, atol=1e-6)
+    assert_scores_close(actual, expected)
 
 
 def test_lse_free_long_rows_take_wider_slices(cuda):
@@ -197,10 +197,10 @@ def test_lse_free_long_rows_take_wider_slices(cuda):
     actual = _gpu_scores(query, key_cache, None, table, lengths, 16, scale, cuda)
     expected = O.paged_chunk_attention_scores(query, key_cache, None, table, torch.tensor(lengths), chunk_size=16,
                                               max_seq_len=max(lengths), scale=scale)
-    torch.testing.assert_close(actual, expected, rtol=1e-3, atol=1e-6)
+    assert_scores_close(actual, expected)
     lse = lse_for(query, key_cache, table, lengths, scale)
     supplied = _gpu_scores(query, key_cache, lse, table, lengths, 16, scale, cuda)
-    torch.testing.assert_close(actual, supplied, rtol=1e-3, atol=1e-6)
+    assert_scores_close(actual, supplied)
     for b, n in enumerate(lengths):  # a row's chunk masses add up to one
         c = (n + 15) // 16
         sizes = torch.full((c,), 16.0)
@@ -218,7 +218,7 @@ def test_lse_free_headline_shape_scores(cuda):
     actual = _gpu_scores(query, key_cache, None, table, lengths, 64, scale, cuda)
     expected = O.paged_chunk_attention_scores(query, key_cache, None, table, torch.tensor(lengths), chunk_size=64,
                                               max_seq_len=max(lengths), scale=scale)
-    torch.testing.assert_close(actual, expected, rtol=1e-3, atol=1e-6)
+    assert_scores_close(actual, expected)
     for b, n in enumerate(lengths):
         c = (n + 63) // 64
         sizes = torch.full((c,), 64.0)

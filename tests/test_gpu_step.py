@@ -13,7 +13,7 @@ canonical slots) and checks every stage against the oracle:
 import pytest
 import torch
 
-from helpers import O, default_scale, gen, max_ulp_bf16, paged_keys, randn
+from helpers import O, assert_scores_close, default_scale, gen, max_ulp_bf16, paged_keys, randn
 
 pytestmark = pytest.mark.gpu
 
@@ -59,7 +59,7 @@ def path(request):
 
 
 def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="chain", single_launch=None,
-            lse_free=False):
+            lse_free=False, flags=0, expect_status=0):
     from ds355 import step
 
     i32 = lambda xs: torch.tensor(xs, dtype=torch.int32, device=device)  # noqa: E731
@@ -103,7 +103,7 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="cha
         row_active=None if row_active is None else i32(row_active),
         workspace=state.get("workspace") if fused else None,
         lse_partials=state.get("lse_partials") if lse_free else None,
-        lse_out=state.get("lse_out") if lse_free else None,
+        lse_out=state.get("lse_out") if lse_free else None, flags=flags,
     )
     torch.cuda.synchronize()
     if fused:  # the single launch ran (epoch + 1) or, for other shapes, the chain did
@@ -111,7 +111,9 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="cha
             # Batches of fewer rows, and steps without a supplied LSE, run the chain.
             single_launch = rows >= 8 and not lse_free
         assert step.workspace_epoch(state["workspace"]) == epoch + (1 if single_launch else 0)
-        assert step.workspace_status(state["workspace"]) == 0
+        if expect_status is not None:
+            assert step.workspace_status(state["workspace"]) == expect_status
+        assert step.workspace_launch_status(state["workspace"]) == 0  # handed over at the launch's end
     return state
 
 
@@ -125,7 +127,7 @@ def check_step(case, state, *, previous=None, row_active=None):
         torch.tensor(lengths), chunk_size=chunk, max_seq_len=max(lengths), scale=case["scale"])
     for j, b in enumerate(rows_idx):
         c = (lengths[j] + chunk - 1) // chunk
-        torch.testing.assert_close(gpu_scores[b, :c], expected_scores[j, :c], rtol=1e-3, atol=1e-6)
+        assert_scores_close(gpu_scores[b, :c], expected_scores[j, :c])
     # Selection on identical (GPU) scores: bit-exact.
     selections = dict(previous or {})
     for j, b in enumerate(rows_idx):
@@ -331,3 +333,84 @@ def test_runtime_retrieval_and_rebuild_match_oracle(cuda, lse_free):
     if lse_free:
         rows_idx, q_index, _ = O.retrieval_rows(case["counts"], case["ends"], case["tlens"], 12)
         torch.testing.assert_close(cache.scored_lse[rows_idx].cpu(), case["lse"][q_index], rtol=1e-5, atol=1e-4)
+
+
+def test_runtime_populate_prefill_then_compact_prefill(cuda):
+    """The proposer's compact-draft-root sequence (proposer.py:256-307) on the GPU:
+    accept_target_queries (score + select), begin_cycle, populate_prefill of every
+    padded verifier token's projected raw K/V (rejected ones included), then
+    prepare_compact_prefill at the committed roots.  Against the oracle's
+    write_raw (runtime.py:1602-1618) followed by the per-request CPU rebuild
+    (runtime.py:1683-1711) over the same selections: raw caches and working
+    caches bit-exact, nothing written past each row's history."""
+    from types import SimpleNamespace
+
+    from ds355 import runtime
+
+    g = gen(23)
+    rows, qlen, chunk, token_budget, lmax = 6, 5, 32, 1024, 9000
+    lens = [int(x) for x in torch.randint(2500, lmax + 1, (rows,), generator=g)]
+    counts = [int(x) for x in torch.randint(1, qlen + 1, (rows,), generator=g)]
+    case = build_case(23, real_rows=rows, pad_rows=0, target_lens=lens, query_len=qlen, counts=counts, hq=16, hkv=2,
+                      head_dim=64, chunk=chunk, token_budget=token_budget, block_size=64, lmax=lmax,
+                      slots=list(range(rows)), num_slots=rows)
+
+    class Rotary:
+        rotary_dim = 64
+        is_neox_style = True
+        cos_sin_cache = case["cos_sin"].to(cuda)
+
+    settings = runtime.DiffSpecSettings(chunk_size=chunk, token_budget=token_budget, retrieval_interval=1,
+                                        max_tree_nodes=4, max_tree_depth=4, tree_threshold=0.7, adaptive_profile=False)
+    cache = runtime.DiffSpecDraftCache(settings, max_num_reqs=rows, max_model_len=lmax, num_kv_heads=2, head_dim=64,
+                                       target_num_layers=2, dtype=torch.bfloat16, device=cuda,
+                                       rotary_embedding=Rotary())
+    cache.raw_key.copy_(case["raw_k"])
+    cache.raw_value.copy_(case["raw_v"])
+    cache.working_key.fill_(float("nan"))
+    cache.working_value.fill_(float("nan"))
+    ids = [f"r{i}" for i in range(rows)]
+    meta = SimpleNamespace(actual_seq_lengths_q=case["ends"], seq_lens_list=case["tlens"],
+                           block_tables=case["table"].to(cuda), num_prefills=0)
+    cache.prepare_target_batch(ids, {})
+    cache.begin_target_forward(ids)
+    cache.capture_target_attention(case["query"].to(cuda), case["lse"].to(cuda), case["key_cache"].to(cuda), meta,
+                                   case["scale"])
+    cache.accept_target_queries(torch.tensor(counts, dtype=torch.int32, device=cuda), is_prefill=False)
+    cache.begin_cycle(ids)
+    # The draft's projection of every verifier token: positions target_len - qlen + j.
+    positions = [tl - qlen + j for tl in lens for j in range(qlen)]
+    key = torch.randn((rows * qlen, 2 * 64), generator=g).to(torch.bfloat16)
+    value = torch.randn((rows * qlen, 2, 64), generator=g).to(torch.bfloat16)
+    cache.populate_prefill(torch.tensor(positions, dtype=torch.int64, device=cuda), key.to(cuda), value.to(cuda),
+                           meta)
+    cache.prepare_compact_prefill(meta, rows, committed_seq_lens=case["committed"])
+    torch.cuda.synchronize()
+    cache.end_cycle()
+    assert cache.capture_status() == 0
+
+    raw_k, raw_v = case["raw_k"].clone(), case["raw_v"].clone()
+    token_slots = [r for r in range(rows) for _ in range(qlen)]
+    O.write_raw(raw_k, raw_v, token_slots, positions, key, value)
+    assert torch.equal(cache.raw_key.cpu(), raw_k) and torch.equal(cache.raw_value.cpu(), raw_v)
+    # Selections on the GPU's scores (bit-exact selection is checked elsewhere on the same inputs).
+    rows_idx, _, lengths = O.retrieval_rows(counts, case["ends"], case["tlens"], rows)
+    scores = cache.scores[:rows].cpu()
+    budget = O.history_budget(token_budget, 4, chunk)
+    selections = {}
+    for j, b in enumerate(rows_idx):
+        c = (lengths[j] + chunk - 1) // chunk
+        sel = O.select_context_chunks(scores[b, :c].contiguous(), lengths[j], chunk, budget)
+        selections[b] = sel.token_indices
+        assert cache.sel_ids[b, : sel.chunk_indices.numel()].cpu().tolist() == sel.chunk_indices.tolist()
+    exp_k = torch.full(tuple(cache.working_key.shape), float("nan"), dtype=torch.bfloat16)
+    exp_v = exp_k.clone()
+    roots = O.rebuild_working_cache_per_request(raw_k, raw_v, exp_k, exp_v, list(range(rows)), case["committed"],
+                                                selections, case["cos_sin"], chunk_size=chunk, budget=budget,
+                                                rotary_dim=64, is_neox_style=True)
+    assert cache.local_positions.cpu().tolist() == roots
+    assert cache.working_lens.cpu().tolist() == roots
+    got_k, got_v = cache.working_key.cpu(), cache.working_value.cpu()
+    assert torch.equal(got_k.isnan(), exp_k.isnan()) and torch.equal(got_v.isnan(), exp_v.isnan())
+    assert torch.equal(torch.nan_to_num(got_k), torch.nan_to_num(exp_k))
+    assert torch.equal(torch.nan_to_num(got_v), torch.nan_to_num(exp_v))

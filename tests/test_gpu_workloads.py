@@ -1,0 +1,196 @@
+"""GPU parity at the benchmark's own workloads, at full size.
+
+Every workload bench.py can measure (the five configurations the step is
+specified on, plus 16 requests of 40960 tokens) runs here with the shapes,
+seeds, recent windows, padding, permuted slots and slot reuse that
+``bench.WORKLOADS`` / ``bench.build_inputs`` give it, so the measured step and
+the tested step cannot drift apart:
+
+  single-8k        1 x 8192, chunk 64, budget 2048, window 256
+  ragged16-40k     16 x U[4096, 40960], chunk 64, budget 2048, window 256
+  fixed16-40k      16 x 40960
+  long4-128k       4 x 131072, chunk 32, budget 2048 (k = 63, 4096 chunks a row)
+  specmask16-pad32 16 x U[8192, 40960] + 16 padding rows, 5 query tokens,
+                   accepted 0..4, permuted slots
+  stress64         64 x U[2048, 40960], Hkv 8 / Hq 64, chunk 128, budget 4096,
+                   window 512, a random half of the rows keeps its working rows
+
+Both implementations of the step run on the same inputs: the kernel chain and,
+with a workspace, the single launch (batches of 8+ rows; smaller ones run the
+chain there too).  They must agree bit for bit, and the chain's results are
+checked against the oracle:
+  scores      every chunk within 1e-3 relative (reference: kernels.py:11-150);
+  selection   bit-exact on identical (GPU) scores, and on the oracle's own
+              scores up to chunks whose score sits within 2e-3 of the cut
+              (runtime.py:348-414);
+  plans       bit-exact (runtime.py:1713-1757, tail of the configured window);
+  working KV  bit-exact per re-gathered row against the oracle's rebuild
+              (compact_kv.py:8-133), rows that keep their contents untouched
+              (NaN), working_lens = each row's history length.
+Reference analogues: tests/test_retrieval_npu.py:16-29 (long-row device vs CPU
+selection), tests/test_retrieval_dynamic_npu.py:15-45 (growing lengths).
+"""
+
+import pytest
+import torch
+
+import bench
+from helpers import O, assert_scores_close
+
+pytestmark = pytest.mark.gpu
+
+SEED = 0
+
+
+def _state(inp, spec, device):
+    rows, total = inp["rows"], inp["total_rows"]
+    chunk, budget, hkv, d = spec["chunk"], spec["budget"], spec["hkv"], spec["d"]
+    max_chunks = (max(inp["tlens"]) + chunk - 1) // chunk
+    work = torch.full((rows, hkv, budget, d), float("nan"), dtype=torch.bfloat16, device=device)
+    return dict(
+        scores=torch.zeros((total, max_chunks), dtype=torch.float32, device=device),
+        partials=torch.zeros((total, max_chunks, hkv), dtype=torch.float32, device=device),
+        sel_ids=torch.zeros((rows, budget // chunk), dtype=torch.int32, device=device),
+        sel_count=torch.full((rows,), -1, dtype=torch.int32, device=device),
+        plan=torch.zeros((total, 5 + budget // chunk), dtype=torch.int64, device=device),
+        working_lens=torch.zeros((rows,), dtype=torch.int32, device=device),
+        work_k=work, work_v=work.clone(),
+    )
+
+
+def _run(inp, spec, st, device, *, cos_sin, hb, row_active, workspace=None):
+    from ds355 import step
+
+    i32 = lambda xs: torch.tensor(xs, dtype=torch.int32, device=device)  # noqa: E731
+    step.retrieval_step(
+        snapshot=step.VerifierSnapshot(inp["query"], inp["lse"], inp["key_cache"], inp["table"], inp["scale"]),
+        rows=step.VerifierRows(i32(inp["counts"]), i32(inp["starts"]), i32(inp["qlens"]), i32(inp["tlens"]),
+                               inp["rows"]),
+        scores=st["scores"], score_partials=st["partials"], sel_ids=st["sel_ids"], sel_count=st["sel_count"],
+        slots=i32(inp["slots"]), committed_lens=i32(inp["committed"]), plan=st["plan"],
+        working_lens=st["working_lens"], raw_key=inp["raw_k"], raw_value=inp["raw_v"], working_key=st["work_k"],
+        working_value=st["work_v"], cos_sin_cache=cos_sin, rotary_dim=spec["d"], is_neox_style=True,
+        chunk_size=spec["chunk"], history_budget=hb, recent_window=spec.get("window", bench.RECENT_WINDOW),
+        row_active=None if row_active is None else i32(row_active), workspace=workspace,
+    )
+    torch.cuda.synchronize()
+
+
+def _same(a, b):
+    return torch.equal(torch.nan_to_num(a), torch.nan_to_num(b)) and torch.equal(a.isnan(), b.isnan())
+
+
+def _check_selection_margin(gpu_ids, oracle_scores, length, chunk, hb):
+    """The oracle's own selection differs from the GPU's only by chunks whose
+    oracle score lies within 2e-3 (relative) of the selection cut."""
+    expected = O.select_context_chunks(oracle_scores, length, chunk, hb).chunk_indices.tolist()
+    if expected == gpu_ids:
+        return 0
+    c = oracle_scores.numel()
+    ranked = oracle_scores[: c - 1].sort(descending=True).values
+    cut = float(ranked[hb // chunk - 2])  # the (K-1)-th largest non-newest score
+    differing = set(expected) ^ set(gpu_ids)
+    for i in differing:
+        assert abs(float(oracle_scores[i]) - cut) <= 2e-3 * abs(cut), (i, float(oracle_scores[i]), cut)
+    return len(differing)
+
+
+@pytest.mark.parametrize("name", sorted(bench.WORKLOADS))
+def test_workload_step_matches_oracle(cuda, name):
+    from ds355 import step
+    from ds355.plan import history_budget
+
+    print(f"workload {name}, seed {SEED}", flush=True)
+    spec = bench.WORKLOADS[name]
+    chunk, budget, d = spec["chunk"], spec["budget"], spec["d"]
+    window = spec.get("window", bench.RECENT_WINDOW)
+    hb = history_budget(budget, bench.DRAFT_TOKENS, chunk)
+    inp = bench.build_inputs(spec, SEED, cuda)
+    rows, total = inp["rows"], inp["total_rows"]
+    cos_sin = O.rope_cos_sin_cache(d, budget, base=bench.ROPE_THETA)
+    cos_dev = cos_sin.to(cuda)
+    row_active = None
+    if spec.get("reuse_half"):
+        g = torch.Generator().manual_seed(SEED + 7)
+        row_active = [int(x) for x in (torch.rand(total, generator=g) >= 0.5)]
+
+    chain = _state(inp, spec, cuda)
+    _run(inp, spec, chain, cuda, cos_sin=cos_dev, hb=hb, row_active=row_active)
+    fused = _state(inp, spec, cuda)
+    max_chunks = chain["scores"].shape[1]
+    workspace = step.new_workspace(total, max_chunks, spec["hkv"], budget, cuda)
+    _run(inp, spec, fused, cuda, cos_sin=cos_dev, hb=hb, row_active=row_active, workspace=workspace)
+    single = total >= 8
+    assert step.workspace_epoch(workspace) == (1 if single else 0)
+    assert step.workspace_status(workspace) == 0
+    for key in ("scores", "sel_ids", "sel_count", "plan", "working_lens", "work_k", "work_v"):
+        assert _same(fused[key], chain[key]), f"single launch != chain: {key}"
+    del fused, workspace
+
+    # Scores: every committed row against the oracle with the same LSE.
+    ends = [s + q for s, q in zip(inp["starts"], inp["qlens"])]
+    rows_idx, q_index, lengths = O.retrieval_rows(inp["counts"], ends, inp["tlens"], rows)
+    assert lengths == [inp["committed"][b] for b in rows_idx]
+    key_cpu = inp["key_cache"].cpu()
+    expected = O.paged_chunk_attention_scores(
+        inp["query"][q_index].cpu(), key_cpu, inp["lse"][q_index].cpu(), inp["table"][rows_idx].cpu(),
+        torch.tensor(lengths), chunk_size=chunk, max_seq_len=max(lengths), scale=inp["scale"])
+    del key_cpu
+    gpu_scores = chain["scores"].cpu()
+    assert_scores_close(gpu_scores[rows_idx, : expected.shape[1]], expected, what=f"{name} scores")
+
+    # Selection: bit-exact on the GPU's scores; the oracle's own scores pick
+    # the same chunks up to near-ties at the cut.
+    sel_count, sel_ids = chain["sel_count"].cpu(), chain["sel_ids"].cpu()
+    selections = {}
+    near_ties = 0
+    for j, b in enumerate(rows_idx):
+        c = (lengths[j] + chunk - 1) // chunk
+        ids = O.select_context_chunks(gpu_scores[b, :c].contiguous(), lengths[j], chunk, hb).chunk_indices.tolist()
+        slot = inp["slots"][b]
+        assert int(sel_count[slot]) == len(ids) and sel_ids[slot, : len(ids)].tolist() == ids, (name, b)
+        near_ties += _check_selection_margin(ids, expected[j, :c].contiguous(), lengths[j], chunk, hb)
+        selections[slot] = ids
+    print(f"{name}: {len(rows_idx)} rows selected, {near_ties} near-tie chunks against the oracle's own scores")
+
+    # Plans, bit-exact, with the configured recent window; padding rows are zero.
+    plans = []
+    for b in range(total):
+        slot = inp["slots"][b]
+        if slot < 0:
+            plans.append([0, 0, 0, 0, 0])
+        else:
+            plans.append(O.history_plan(slot, selections.get(slot), max(0, inp["committed"][b] - 1), chunk, hb,
+                                        window))
+    expected_plan = O.pad_plan(plans, budget, chunk)
+    assert torch.equal(chain["plan"].cpu(), expected_plan)
+    lens = chain["working_lens"].cpu().tolist()
+    for b in range(total):
+        if inp["slots"][b] >= 0:
+            assert lens[inp["slots"][b]] == plans[b][1]
+
+    # Working caches, row by row (the raw cache is copied one slot at a time).
+    work_k, work_v = chain["work_k"], chain["work_v"]
+    checked = 0
+    for b in range(total):
+        slot, length = plans[b][0], plans[b][1]
+        if inp["slots"][b] < 0:
+            continue
+        if row_active is not None and not row_active[b]:
+            assert work_k[slot].isnan().all() and work_v[slot].isnan().all()
+            continue
+        end = max(0, inp["committed"][b] - 1)
+        raw_k = inp["raw_k"][slot, : max(end, 1)].cpu()[None]
+        raw_v = inp["raw_v"][slot, : max(end, 1)].cpu()[None]
+        exp_k = torch.full((1, *work_k.shape[1:]), float("nan"), dtype=torch.bfloat16)
+        exp_v = exp_k.clone()
+        row_plan = expected_plan[b : b + 1].clone()
+        row_plan[0, 0] = 0
+        O.rebuild_compact_kv_from_plan(raw_k, raw_v, exp_k, exp_v, row_plan, cos_sin, chunk_size=chunk,
+                                       max_width=length, rotary_dim=d, is_neox_style=True)
+        assert _same(work_k[slot].cpu(), exp_k[0]), (name, b)
+        assert _same(work_v[slot].cpu(), exp_v[0]), (name, b)
+        checked += 1
+    print(f"{name}: working caches of {checked} rows bit-exact")
+    del chain, inp
+    torch.cuda.empty_cache()

@@ -269,3 +269,97 @@ def test_draft_attention_pending_state(launches, attention_calls):
     cache._pending_local_positions = [8]
     with pytest.raises(RuntimeError, match="DiffSpec working cache exhausted"):
         cache.forward_attention(q, kv, kv, 0.25, torch.zeros_like(q))
+
+
+@pytest.fixture
+def capture_calls(monkeypatch):
+    from ds355 import capture
+
+    calls = []
+
+    def record(key, value, raw_key, raw_value, token_slots, absolute_positions, rope_buffer, *, tokens,
+               working_lens=None, local_positions=None, prev_count=0, status=None):
+        calls.append(dict(slots=token_slots[:tokens].tolist(), positions=absolute_positions.reshape(-1).tolist(),
+                          tokens=tokens, rope=rope_buffer is not None, working_lens=working_lens is not None,
+                          key=key[:tokens].clone()))
+        if rope_buffer is None:
+            return None
+        count = absolute_positions.numel()
+        return rope_buffer[:count].view(absolute_positions.shape)
+
+    monkeypatch.setattr(capture, "capture_raw_kv_rows", record)
+    return calls
+
+
+def test_linear_call_sequence_of_the_plugin(launches, attention_calls, capture_calls):
+    """The hooks the unchanged plugin calls on one linear verify + draft cycle, in its order:
+    the runner's prepare_target_batch (ascend_patch.py:274) and begin_target_forward (:301),
+    the attention patch's is_target_retrieval_layer / capture_target_attention (:198, :233)
+    and target_tree_active reads (:165, :279, :311), the proposer's clear_proposed_tree
+    (proposer.py:357), accept_target_queries (:216), prepare_inputs_padded's
+    target_tree_active read (:224), begin_cycle (:103), populate_prefill (:266),
+    prepare_compact_prefill (:303), the draft layer's capture + attention, end_cycle (:119)."""
+    cache = _cache(settings=dict(retrieval_interval=1, token_budget=16), max_model_len=32, target_num_layers=3)
+    ids = ["a", "b"]
+    # Verifier step: the runner activates the batch (linear: no proposed tree).
+    cache.prepare_target_batch(ids, {"a": [5, 6, 7], "b": [1, 2, 3]})
+    assert cache.target_tree_active is False
+    cache.begin_target_forward(ids)
+    assert cache._active_slots == [0, 1]
+    assert [cache.is_target_retrieval_layer(i) for i in range(3)] == [False, False, True]
+    assert not cache.has_pending_attention()  # the target's attention is not diverted
+    q = torch.zeros((8, 2, 2))
+    lse = torch.zeros((8, 2))
+    meta = _metadata([4, 8], [20, 12], prefill=False)
+    cache.capture_target_attention(q, lse, torch.zeros((4, 8, 1, 2)), meta, 0.5)
+    assert cache.target_tree_active is False  # the sampler keeps its own path
+    # Proposer: linear proposal, retrieval on the accepted counts.
+    cache.clear_proposed_tree()
+    assert cache.proposed_token_ids is None and cache.proposed_depths_cpu == []
+    cache.accept_target_queries(torch.tensor([2, 4]), is_prefill=cache.target_is_prefill)
+    assert launches[-1]["stages"] == step.SCORE | step.SELECT
+    assert launches[-1]["rows"].counts.tolist() == [2, 4]
+    assert not cache.target_tree_active  # prepare_inputs_padded returns its result unchanged
+    with pytest.raises(RuntimeError, match="tree has not been verified"):
+        cache.accepted_target_token_indices()
+    cache.rewrite_target_positions([0, 1, 2], [3])  # no-op in linear verification
+    # Draft cycle: project the padded prefill's raw K/V, then rebuild at the committed roots.
+    cache.begin_cycle(ids)
+    positions = torch.tensor([16, 17, 18, 19, 8, 9, 10, 11], dtype=torch.int64)
+    raw_kv = torch.arange(16, dtype=torch.float32).view(8, 2)
+    cache.populate_prefill(positions, raw_kv, raw_kv, meta)
+    scatter = capture_calls[-1]
+    assert scatter["slots"] == [0, 0, 0, 0, 1, 1, 1, 1]  # token -> row from the query ends -> slot
+    assert scatter["positions"] == positions.tolist() and scatter["tokens"] == 8
+    assert not scatter["rope"] and not scatter["working_lens"]  # raw rows only (runtime.py:1336-1347)
+    torch.testing.assert_close(scatter["key"], raw_kv)
+    cache.prepare_compact_prefill(meta, 2, committed_seq_lens=[18, 12])
+    assert launches[-1]["stages"] == step.PLAN and launches[-1]["committed_lens"].tolist() == [18, 12]
+    assert cache.has_pending_attention()
+    # The draft layer: capture (the vllm::diffspec_capture_raw_kv op body) then attention.
+    roots = torch.tensor([17, 11], dtype=torch.int64)
+    rope = cache.graph_safe_rope_positions(roots, cache.capture_raw_kv(0, roots, raw_kv[:2], raw_kv[:2]))
+    assert capture_calls[-1]["slots"] == [0, 1] and capture_calls[-1]["working_lens"]
+    assert rope.shape == roots.shape
+    cache.forward_attention(torch.zeros((2, 2, 2)), raw_kv[:2].view(2, 1, 2), raw_kv[:2].view(2, 1, 2), 0.5,
+                            torch.zeros((2, 2, 2)))
+    assert attention_calls[-1]["slots"] == [0, 1]
+    cache.end_cycle()
+    assert not cache.has_pending_attention()
+    # Outside a cycle populate_prefill still maps tokens by the query ends; an empty call is a no-op.
+    cache.populate_prefill(positions[:0], raw_kv[:0], raw_kv[:0], meta)
+    assert len(capture_calls) == 2
+
+
+def test_retrieval_with_host_counts_and_no_committed_rows_is_skipped(launches):
+    """All-zero host counts: skipped and counted, as runtime.py:1253-1257 does."""
+    cache = _cache(settings=dict(retrieval_interval=1))
+    cache.begin_target_forward(["a", "b"])
+    cache.capture_target_attention(torch.zeros((2, 2, 2)), torch.zeros((2, 2)), torch.zeros((1, 2, 1, 2)),
+                                   _metadata([1, 2], [6, 4], prefill=False), 0.5)
+    cache.accept_target_queries(torch.tensor([0, 0]), is_prefill=False)
+    assert launches == []
+    status = cache.retrieval_status()
+    assert status["retrieval_skipped_no_committed_tokens"] == 1 and status["retrieval_count"] == 0
+    cache.accept_target_queries(torch.tensor([0, 1]), is_prefill=False)
+    assert len(launches) == 1 and cache.retrieval_status()["retrieval_count"] == 1

@@ -124,7 +124,7 @@ int capture_impl(hipStream_t stream, int dtype, const void* key, int64_t k_row, 
                  int prev_count, int32_t* status) {
   DS_REQUIRE(dtype == DS_BF16 || dtype == DS_FP16 || dtype == DS_FP32, "KV caches must use BF16, FP16 or FP32");
   DS_REQUIRE(tokens >= 0 && count >= 0 && prev_count >= 0, "token counts must be non-negative");
-  DS_REQUIRE(tokens <= count, "captured tokens exceed the position count");
+  DS_REQUIRE(tokens <= count || count == 0, "captured tokens exceed the position count");
   DS_REQUIRE(num_slots > 0 && max_model_len > 0 && heads > 0 && head_dim > 0,
              "raw sequence, head and head dimensions must be positive");
   DS_REQUIRE(!(working_lens && local_positions), "give working lengths or local positions, not both");

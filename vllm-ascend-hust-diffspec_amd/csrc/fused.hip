@@ -50,8 +50,14 @@
 // the launch get fresh tags.  Tags stay below 2^31 (bit 31 marks skipped
 // tasks).
 //
+// Status: an expired wait ORs a bit into the launch's own status word
+// (header[3]), which every bounded wait of that launch reads to stop early.
+// The last workgroup moves those bits into the owner's status word
+// (header[2], cleared only by the owner) and zeroes header[3], so one
+// launch's expiry never shortens the waits of the next.
+//
 // Workspace (zero-filled once by its owner; one launch at a time):
-//   uint32 header[16]               epoch, done counter, status
+//   uint32 header[16]               epoch, done counter, status, launch status
 //   uint64 plans[rows][kPlanCols]   tagged plan copies
 //   uint32 state[rows][task_cap]    gather task done / skipped
 //   uint64 partials[rows, max_chunks, Hkv]
@@ -100,7 +106,7 @@ constexpr uint32_t kOwnerSpins = 1u << 12;  // polls before a scorer leaves a ta
 constexpr uint32_t kSkipped = 0x80000000u;
 constexpr int kSleep = 8;          // s_sleep units (64 cycles each) between polls
 
-enum { kEpoch = 0, kDone = 1, kStatus = 2, kHeaderWords = 16 };
+enum { kEpoch = 0, kDone = 1, kStatus = 2, kLaunchStatus = 3, kHeaderWords = 16 };
 enum { kStatusPartials = 1u, kStatusTasks = 2u };
 constexpr int kLine = 256;
 constexpr int kPlanCols = 128;     // tagged plan columns per row (plan_width <= 128)
@@ -115,17 +121,21 @@ struct FusedArgs {
   uint32_t* state;  // [rows, task_cap]
   int task_cap;
   int selectors;
+  uint32_t owner_spins;  // polls a scorer waits for a plan (0: every task goes to the selectors)
+  int expire;            // test flag: every selector raises kStatusPartials as if a wait had expired
 };
 
+// The read-modify-write completes before the thread goes on (acquire), so
+// the bit is in memory before the workgroup counts itself done.
 __device__ __forceinline__ void raise_status(uint32_t* header, uint32_t bit) {
-  __hip_atomic_fetch_or(header + kStatus, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_fetch_or(header + kLaunchStatus, bit, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
 }
 // A wait without deadline gives up after kSpinLimit polls, or early once
-// another one has.
+// another wait of this launch has.
 __device__ __forceinline__ bool give_up(uint32_t spin, const uint32_t* header) {
   return spin >= kSpinLimit ||
          (spin % kStatusEvery == kStatusEvery - 1 &&
-          __builtin_amdgcn_readfirstlane(coherent_load(header + kStatus)) != 0u);
+          __builtin_amdgcn_readfirstlane(coherent_load(header + kLaunchStatus)) != 0u);
 }
 __device__ __forceinline__ int64_t uniform64(int64_t v) {
   const uint64_t u = static_cast<uint64_t>(v);
@@ -169,7 +179,8 @@ __device__ __forceinline__ void poll_chunk_sums(const uint64_t* part, int base, 
       if (i < C && static_cast<uint32_t>(v[e] >> 32) != tag) ready = false;
     }
     if (ready) break;
-    if (spin >= kSpinLimit || (spin % kStatusEvery == kStatusEvery - 1 && coherent_load(header + kStatus) != 0u)) {
+    if (spin >= kSpinLimit ||
+        (spin % kStatusEvery == kStatusEvery - 1 && coherent_load(header + kLaunchStatus) != 0u)) {
       raise_status(header, kStatusPartials);
       break;
     }
@@ -197,6 +208,7 @@ __device__ __forceinline__ void select_row(const FusedArgs& f, int b, uint32_t t
   const bool slot_ok = slot >= 0 && slot < a.num_slots;
   const int committed = a.committed_lens[b];
   const int stored_count = slot_ok ? a.counts[slot] : 0;
+  if (f.expire && tid == 0) raise_status(f.header, kStatusPartials);
   int n_sel = -1;
   if (d.active && slot_ok) {
     const int C = (d.len + a.chunk - 1) / a.chunk;
@@ -330,7 +342,7 @@ __device__ __forceinline__ void gather_owned(const FusedArgs& f, const int* task
     const int r = __builtin_amdgcn_readfirstlane(lo);
     if (r != cur) {
       cur = r;
-      published = poll_plan(f, r, tag, kOwnerSpins, v);
+      published = poll_plan(f, r, tag, f.owner_spins, v);
     }
     const int t = __builtin_amdgcn_readfirstlane(task - task_prefix[r]);
     if (published) run_task<DT, NEOX>(ga, L, v, t);
@@ -439,11 +451,16 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
     gather_owned<DT, NEOX>(f, s_task_prefix, gw, tw, tag);
   }
 
-  // The last workgroup to finish publishes this launch's tag as the epoch.
+  // The last workgroup to finish hands this launch's status bits to the
+  // owner's word, clears them for the next launch and publishes the tag as
+  // the epoch.
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(f.header + kDone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = __hip_atomic_fetch_add(f.header + kDone, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     if (prev == gridDim.x - 1) {
+      const uint32_t bits =
+          __hip_atomic_exchange(f.header + kLaunchStatus, 0u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+      if (bits != 0u) __hip_atomic_fetch_or(f.header + kStatus, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       coherent_store(f.header + kDone, 0u);
       coherent_store(f.header + kEpoch, tag);
     }
@@ -550,6 +567,8 @@ int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource
   ws += state_bytes(d->batch_rows, d->token_budget);
   f.s.tagged = reinterpret_cast<uint64_t*>(ws);
   f.selectors = std::min(d->batch_rows, kSelectors);
+  f.owner_spins = (d->flags & DS_STEP_SELECTORS_GATHER) != 0 ? 0u : kOwnerSpins;
+  f.expire = (d->flags & DS_STEP_EXPIRE_WAITS) != 0 ? 1 : 0;
   const int ppw = 64 / f.g.lanes_per_row;
   const int64_t upper_tasks = static_cast<int64_t>(d->batch_rows) * ((f.g.pos_limit + ppw - 1) / ppw);
   const bool neox = d->is_neox_style != 0;

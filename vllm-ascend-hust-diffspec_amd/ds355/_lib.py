@@ -8,6 +8,7 @@ live on a GPU.  There is no CPU fallback.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import torch
@@ -18,7 +19,8 @@ DS_OK, DS_ERR_INVALID, DS_ERR_UNSUPPORTED, DS_ERR_HIP = 0, 1, 2, 3
 DS_BF16, DS_FP16, DS_FP32 = 0, 1, 2
 DS_HEAD_MEAN, DS_HEAD_MAX = 0, 1
 DS_STAGE_SCORE, DS_STAGE_SELECT, DS_STAGE_PLAN, DS_STAGE_ALL = 1, 2, 4, 7
-ABI_VERSION = 5
+DS_STEP_SELECTORS_GATHER, DS_STEP_EXPIRE_WAITS = 1, 2
+ABI_VERSION = 6
 
 EXPORTED_SYMBOLS = (
     "ds_last_error",
@@ -35,6 +37,12 @@ EXPORTED_SYMBOLS = (
 )
 
 _DTYPES = {torch.bfloat16: DS_BF16, torch.float16: DS_FP16, torch.float32: DS_FP32}
+
+# Host-side checks of the preconditions the reference leaves to its callers
+# (distinct slots across plan rows, in-range plan entries;
+# diffspec/compact_kv.py:199-205).  They read device values back, so they
+# are off unless DS355_DEBUG_CHECKS is set to a value other than "" or "0".
+DEBUG_CHECKS = os.environ.get("DS355_DEBUG_CHECKS", "0") not in ("", "0")
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int
@@ -76,6 +84,7 @@ class StepDesc(ctypes.Structure):
         ("chunk_size", _i32), ("history_budget", _i32), ("recent_window", _i32),
         ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),
         ("lse_partials", _p), ("lse_out", _p), ("lse_out_stride", _i64),
+        ("flags", _i32),
     ]
 
 

@@ -34,14 +34,14 @@ def capture_raw_kv_rows(
     raw_value: torch.Tensor,
     token_slots: torch.Tensor,
     absolute_positions: torch.Tensor,
-    rope_buffer: torch.Tensor,
+    rope_buffer: torch.Tensor | None,
     *,
     tokens: int,
     working_lens: torch.Tensor | None = None,
     local_positions: torch.Tensor | None = None,
     prev_count: int = 0,
     status: torch.Tensor | None = None,
-) -> torch.Tensor:
+) -> torch.Tensor | None:
     """Scatter the first ``tokens`` rows of ``key``/``value`` into the raw caches
     at ``[token_slots[t], absolute_positions[t]]`` and write the RoPE input.
 
@@ -49,7 +49,8 @@ def capture_raw_kv_rows(
     positions), viewed with their shape: each draft row's working length when
     ``working_lens`` is given (0 for rows past ``tokens``), else
     ``local_positions``, else the absolute positions.  ``rope_buffer[count:
-    prev_count]`` is zeroed.  Returns the view.
+    prev_count]`` is zeroed.  Returns the view.  With ``rope_buffer=None``
+    only the rows are scattered (``populate_prefill``) and None is returned.
     """
     num_slots, max_model_len, heads, head_dim = raw_key.shape
     if raw_value.shape != raw_key.shape or not (raw_key.is_contiguous() and raw_value.is_contiguous()):
@@ -60,11 +61,15 @@ def capture_raw_kv_rows(
         raise ValueError("absolute positions must be contiguous")
     if positions.dtype not in (torch.int32, torch.int64):
         raise ValueError("absolute positions must be int32 or int64")
-    if rope_buffer.dtype != positions.dtype or not rope_buffer.is_contiguous():
+    if rope_buffer is None:
+        if prev_count or working_lens is not None or local_positions is not None:
+            raise ValueError("local positions and a stale tail need a RoPE buffer")
+        count = 0  # scatter only
+    elif rope_buffer.dtype != positions.dtype or not rope_buffer.is_contiguous():
         raise ValueError("the RoPE buffer must be contiguous with the positions' dtype")
-    if max(count, prev_count) > rope_buffer.numel():
+    elif max(count, prev_count) > rope_buffer.numel():
         raise RuntimeError("DiffSpec RoPE input exceeds its persistent buffer")
-    if tokens < 0 or tokens > count:
+    if tokens < 0 or tokens > positions.numel():
         raise ValueError("captured tokens must be between zero and the number of positions")
     k = _rows(key, heads, head_dim, "key")
     v = _rows(value, heads, head_dim, "value")
@@ -89,6 +94,8 @@ def capture_raw_kv_rows(
         positions.data_ptr(), 1 if positions.dtype == torch.int64 else 0,
         token_slots.data_ptr(), tokens, raw_key.data_ptr(), raw_value.data_ptr(),
         num_slots, max_model_len, heads, head_dim,
-        _lib.ptr(working_lens), _lib.ptr(local), rope_buffer.data_ptr(), count, prev_count, _lib.ptr(status),
+        _lib.ptr(working_lens), _lib.ptr(local), _lib.ptr(rope_buffer), count, prev_count, _lib.ptr(status),
     ))
+    if rope_buffer is None:
+        return None
     return rope_buffer[:count].view(absolute_positions.shape)

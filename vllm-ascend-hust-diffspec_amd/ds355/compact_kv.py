@@ -62,6 +62,40 @@ def _validate_compact_inputs(
         raise ValueError("KV caches, plan and cos/sin cache must share a device")
 
 
+def check_plan_preconditions(plan: torch.Tensor, *, num_slots: int, max_model_len: int, token_budget: int,
+                             chunk_size: int, row_active: torch.Tensor | None = None) -> None:
+    """Preconditions the reference states but does not check (diffspec/compact_kv.py:199-205).
+
+    Every active row with a history has a slot in ``[0, num_slots)`` that no
+    other such row uses, ``history_len <= token_budget``, and decodes to
+    positions inside ``[0, max_model_len)``.  Duplicate slots would make two
+    rows write the same working rows concurrently.  Reads the plan back
+    (host synchronisation): a debugging aid, run when ``DS355_DEBUG_CHECKS``
+    is set.
+    """
+    rows = plan.detach().to("cpu").tolist()
+    active = None if row_active is None else row_active.detach().to("cpu").tolist()
+    seen: dict[int, int] = {}
+    for r, row in enumerate(rows):
+        slot, length, tail_start, prefix_len, drop = row[:5]
+        if length <= 0 or (active is not None and not active[r]):
+            continue
+        if not 0 <= slot < num_slots:
+            raise ValueError(f"plan row {r}: slot {slot} outside [0, {num_slots})")
+        if slot in seen:
+            raise ValueError(f"plan rows {seen[slot]} and {r} share slot {slot}; slots must be distinct")
+        seen[slot] = r
+        if length > token_budget or not 0 <= prefix_len <= length or drop < 0:
+            raise ValueError(f"plan row {r}: inconsistent lengths {row[1:5]}")
+        chunks = row[5:]
+        last = prefix_len + drop - 1
+        if prefix_len and (last // chunk_size >= len(chunks)
+                           or not all(0 <= c * chunk_size < max_model_len for c in chunks[: last // chunk_size + 1])):
+            raise ValueError(f"plan row {r}: prefix chunks outside the raw cache")
+        if tail_start < 0 or tail_start + length - prefix_len > max_model_len:
+            raise ValueError(f"plan row {r}: tail outside the raw cache")
+
+
 def rebuild_compact_kv_from_plan(
     raw_key: torch.Tensor,
     raw_value: torch.Tensor,
@@ -102,6 +136,9 @@ def rebuild_compact_kv_from_plan(
         row_active = row_active.contiguous()
     lib = _lib.load()
     slots, max_model_len, heads, head_dim = raw_key.shape
+    if _lib.DEBUG_CHECKS:
+        check_plan_preconditions(plan, num_slots=slots, max_model_len=max_model_len,
+                                 token_budget=working_key.shape[2], chunk_size=chunk_size, row_active=row_active)
     _lib.check(lib.ds_rebuild_compact_kv(
         _lib.stream_handle(device), _lib.dtype_code(raw_key.dtype),
         raw_key.data_ptr(), raw_value.data_ptr(), working_key.data_ptr(), working_value.data_ptr(),

@@ -216,6 +216,15 @@ class DiffSpecDraftCache:
         self._rope_position_buffers: dict[torch.dtype, torch.Tensor] = {}
         self._rope_position_written: dict[torch.dtype, int] = {}
         self._capture_status = torch.zeros((1,), dtype=torch.int32, device=self.device)
+        self._token_staging: _Staging | None = None  # token -> slot rows of populate_prefill
+        # Verification is linear: this cache proposes no draft tree, so the
+        # reference's tree activation (runtime.py:795-813) never fires and
+        # these keep their "no tree" values (runtime.py:708-712).
+        self.target_tree_active = False
+        self.proposed_token_ids: torch.Tensor | None = None
+        self.proposed_parent_indices: torch.Tensor | None = None
+        self.proposed_depths: torch.Tensor | None = None
+        self.proposed_depths_cpu: list[int] = []
 
     # -- draft cycle (runtime.py:731-753) -----------------------------------------------------------
     def begin_cycle(self, request_ids: list[str]) -> None:
@@ -263,6 +272,35 @@ class DiffSpecDraftCache:
         self._target_query_ends = []
         self._target_seq_lens = []
         self.target_is_prefill = True
+
+    def prepare_target_batch(self, request_ids: list[str], scheduled_spec_token_ids: dict[str, list[int]]) -> None:
+        """Slots for the verifier batch; verification stays linear (runtime.py:795-813).
+
+        The reference turns tree verification on only when a proposed tree
+        was scheduled whole; this cache never proposes one.
+        """
+        del scheduled_spec_token_ids  # only consulted for a proposed tree
+        self.set_active_requests(request_ids)
+        self.target_tree_active = False
+
+    def rewrite_target_positions(self, positions: Any, cumulative_query_lens: Any) -> None:
+        """Tree-node positions (runtime.py:815-829): nothing to rewrite in linear verification."""
+        del positions, cumulative_query_lens
+
+    def accepted_target_token_indices(self) -> torch.Tensor:
+        """Accepted tree-node offsets (runtime.py:831-834); no tree is ever verified here."""
+        raise RuntimeError("DiffSpec tree has not been verified")
+
+    def is_target_retrieval_layer(self, layer_index: int) -> bool:
+        """The verifier layer whose query, LSE and K feed scoring: the last one (runtime.py:838-839)."""
+        return layer_index == self.target_last_layer
+
+    def clear_proposed_tree(self) -> None:
+        """Drop a proposed tree (runtime.py:1526-1531); called before every linear proposal."""
+        self.proposed_token_ids = None
+        self.proposed_parent_indices = None
+        self.proposed_depths = None
+        self.proposed_depths_cpu = []
 
     # -- verifier snapshot (runtime.py:841-894) ---------------------------------------------------
     @staticmethod
@@ -354,6 +392,16 @@ class DiffSpecDraftCache:
             raise RuntimeError("DiffSpec batch exceeds max_batch_rows")
         if self.target_tensor_parallel_size > 1:
             raise NotImplementedError("the chunk-score all-reduce across tensor-parallel ranks is not built")
+        # A step where no row committed a token is skipped and counted, as
+        # runtime.py:1253-1257 does, whenever that is known on the host: an
+        # empty batch, or counts held in host memory.  Device counts stay on
+        # the device (no synchronisation): such a step then runs, scores
+        # nothing and leaves every selection as it was, with the same result
+        # but without the counter.
+        if batch_size == 0 or (valid_sampled_token_count.device.type == "cpu"
+                               and int(valid_sampled_token_count.reshape(-1)[:batch_size].max()) <= 0):
+            self.metrics.retrieval_skipped_no_committed_tokens += 1
+            return
         ends = self._target_query_ends[:batch_size]
         starts = [0, *ends[:-1]]
         lens = [e - s for s, e in zip(starts, ends)]
@@ -412,6 +460,37 @@ class DiffSpecDraftCache:
         self._compact_prefill = True
         self._draft_step += 1
         return self.local_positions
+
+    def populate_prefill(self, absolute_positions: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                         metadata: Any) -> None:
+        """Write the draft's projected prefill rows into the raw cache (runtime.py:1336-1347).
+
+        Token t goes to its request's slot (rows from ``metadata``'s query
+        ends, runtime.py:1580-1594) at ``absolute_positions[t]``, every KV
+        head, rejected tokens included (a later step overwrites them): one
+        scatter launch, no RoPE input.  The next compact prefill's gather
+        reads these rows, and runs after this launch on the same stream.
+        """
+        if not self._active_slots:
+            raise RuntimeError("DiffSpec request slots have not been initialized")
+        num_tokens = key.shape[0]
+        if num_tokens == 0:
+            return
+        rows = self._request_indices(metadata, num_tokens)
+        if max(rows) >= len(self._active_slots):
+            raise RuntimeError("DiffSpec request slots have not been initialized")
+        token_slots = [self._active_slots[r] for r in rows]
+        staging = self._token_staging
+        if staging is None or staging.device.shape[1] < num_tokens:
+            capacity = max(num_tokens, 8 * self.max_batch_rows)
+            staging = self._token_staging = _Staging(1, capacity, self.device)
+        slots = staging.upload([token_slots])[0, :num_tokens]
+        positions = absolute_positions.reshape(-1)[:num_tokens]
+        if not positions.is_contiguous():
+            positions = positions.contiguous()
+        _capture.capture_raw_kv_rows(
+            key, value, self.raw_key, self.raw_value, slots, positions, None, tokens=num_tokens,
+            status=self._capture_status)
 
     # -- raw KV capture and RoPE input (runtime.py:1580-1618, 1767-1877) -------------------------
     @staticmethod

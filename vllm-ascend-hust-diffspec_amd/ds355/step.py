@@ -61,6 +61,7 @@ class VerifierRows:
 
 
 SCORE, SELECT, PLAN, ALL = _lib.DS_STAGE_SCORE, _lib.DS_STAGE_SELECT, _lib.DS_STAGE_PLAN, _lib.DS_STAGE_ALL
+SELECTORS_GATHER, EXPIRE_WAITS = _lib.DS_STEP_SELECTORS_GATHER, _lib.DS_STEP_EXPIRE_WAITS
 
 
 def retrieval_step(**kwargs) -> None:
@@ -113,6 +114,7 @@ def build_step_desc(
     workspace: torch.Tensor | None = None,
     lse_partials: torch.Tensor | None = None,
     lse_out: torch.Tensor | None = None,
+    flags: int = 0,
 ) -> tuple[_lib.StepDesc, torch.device]:
     """Validate and pack a step descriptor for ``stages`` (``SCORE | SELECT | PLAN``; ``ALL`` = one step).
 
@@ -128,6 +130,12 @@ def build_step_desc(
     max_chunks, 2]`` fp32 scratch: each chunk's (max, sum) per query head)
     and ``lse_out`` (``[batch_rows, Hq]`` fp32, where each scored row's
     natural-log LSE is written); such a step runs as the kernel chain.
+
+    ``flags`` (tests only): ``SELECTORS_GATHER`` makes the single launch's
+    selecting workgroups do every gather task (the path of a task whose
+    scoring wave stopped waiting for its plan; same results);
+    ``EXPIRE_WAITS`` makes every selector report an expired wait (status bit
+    0, results not valid).
     """
     if stages & ~ALL:
         raise ValueError(f"unknown stage bits {stages:#x}")
@@ -246,7 +254,28 @@ def build_step_desc(
     desc.recent_window = chunk_size if recent_window is None else recent_window
     desc.workspace = _lib.ptr(workspace)
     desc.workspace_bytes = 0 if workspace is None else workspace.numel()
+    if flags & ~(SELECTORS_GATHER | EXPIRE_WAITS):
+        raise ValueError(f"unknown step flags {flags:#x}")
+    if _lib.DEBUG_CHECKS and stages & PLAN:
+        check_distinct_slots(slots, num_slots, row_active)
+    desc.flags = flags
     return desc, device
+
+
+def check_distinct_slots(slots: torch.Tensor, num_slots: int, row_active: torch.Tensor | None = None) -> None:
+    """The plan stage's precondition (diffspec/compact_kv.py:199-205): no two
+    re-gathered rows share a slot.  Rows whose slot is outside ``[0,
+    num_slots)`` are graph padding.  Reads ``slots`` back (host
+    synchronisation): run when ``DS355_DEBUG_CHECKS`` is set."""
+    values = slots.detach().to("cpu").tolist()
+    active = None if row_active is None else row_active.detach().to("cpu").tolist()
+    seen: dict[int, int] = {}
+    for r, slot in enumerate(values):
+        if not 0 <= slot < num_slots or (active is not None and not active[r]):
+            continue
+        if slot in seen:
+            raise ValueError(f"rows {seen[slot]} and {r} share slot {slot}; slots must be distinct")
+        seen[slot] = r
 
 
 def workspace_bytes(batch_rows: int, max_chunks: int, num_kv_heads: int, token_budget: int) -> int:
@@ -268,6 +297,18 @@ def workspace_epoch(workspace: torch.Tensor) -> int:
     return int(workspace[:4].view(torch.int32).item()) & 0xFFFFFFFF
 
 
+def workspace_launch_status(workspace: torch.Tensor) -> int:
+    """Header word 3, the running launch's own status bits: 0 between launches (synchronises)."""
+    return int(workspace[12:16].view(torch.int32).item()) & 0xFFFFFFFF
+
+
 def workspace_status(workspace: torch.Tensor) -> int:
-    """Status word: 0 unless a bounded wait of the single-launch step expired (synchronises)."""
+    """Status word: 0 unless a bounded wait of a single-launch step on this
+    workspace expired since it was created or last cleared (synchronises).
+    Bit 0: score partials, bit 1: gather tasks."""
     return int(workspace[8:12].view(torch.int32).item()) & 0xFFFFFFFF
+
+
+def clear_workspace_status(workspace: torch.Tensor) -> None:
+    """Zero the status word, stream-ordered (a fill kernel, no host synchronisation)."""
+    workspace[8:12].zero_()

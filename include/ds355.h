@@ -257,6 +257,37 @@ int ds_retrieval_step(ds_stream_t stream, const ds_step_desc* desc);
 size_t ds_step_workspace_bytes(int batch_rows, int max_chunks, int num_kv_heads, int token_budget);
 
 /*
+ * The retrieval step with its scratch memory in a static device array.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops that forbid
+ * allocation).  Same work and results as ds_retrieval_step; the descriptor's
+ * score_partials, workspace (and workspace_bytes) and lse_partials must be
+ * NULL / 0, since those buffers live in a file-scope __device__ array of
+ * DS_STATIC_SCRATCH_BYTES that each GPU holds from library load until the
+ * process ends.  Every other buffer (inputs, outputs, per-slot state) is the
+ * caller's, as before.  Nothing is allocated and no allocating routine is
+ * called.
+ *
+ * Limits, rejected with DS_ERR_INVALID and a message:
+ *   batch_rows x max_chunks x num_kv_heads x 4 bytes <= DS_STATIC_PARTIALS_BYTES;
+ *   without an LSE, batch_rows x num_q_heads x max_chunks x 8 bytes <= DS_STATIC_PAIRS_BYTES.
+ * A full step runs as the single launch when ds_step_workspace_bytes() of its
+ * shape fits DS_STATIC_FUSED_BYTES (and the shape suits it), else as the chain.
+ * status (optional, a device word the caller owns and clears): a single
+ * launch whose bounded wait expired ORs its status bits into it (then that
+ * call's results are not valid).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (several streams or threads) race and must be serialised by the
+ * caller.  The current device must be the stream's device.
+ */
+#define DS_STATIC_FUSED_BYTES ((size_t)8 << 20)
+#define DS_STATIC_PARTIALS_BYTES ((size_t)4 << 20)
+#define DS_STATIC_PAIRS_BYTES ((size_t)12 << 20)
+#define DS_STATIC_SCRATCH_BYTES (DS_STATIC_FUSED_BYTES + DS_STATIC_PARTIALS_BYTES + DS_STATIC_PAIRS_BYTES)
+
+int ds_retrieval_step_static(ds_stream_t stream, const ds_step_desc* desc, uint32_t* status);
+
+/*
  * Draft decode attention over the working cache (linear drafting, one query
  * token per row).
  * Replaces DiffSpecDraftCache.forward_attention's linear path

@@ -344,3 +344,23 @@ def test_capture_refuses_cpu_tensors():
     with pytest.raises(RuntimeError, match="exceeds its persistent buffer"):
         capture_raw_kv_rows(key, key, raw, raw.clone(), torch.zeros(1, dtype=torch.int32),
                             torch.zeros(5, dtype=torch.int64), torch.zeros(4, dtype=torch.int64), tokens=1)
+
+
+def test_static_scratch_step_rejects_what_does_not_fit():
+    """ds_retrieval_step_static checks its limits on the host, before any HIP call."""
+    from ds355 import _lib
+
+    lib = _lib.load()
+    desc = _lib.StepDesc()
+    desc.stages = _lib.DS_STAGE_SCORE | _lib.DS_STAGE_SELECT
+    desc.batch_rows, desc.batch_size, desc.max_chunks = 64, 64, 4096
+    desc.num_kv_heads, desc.num_q_heads = 8, 64  # 64 x 4096 x 8 x 4 B = 8 MiB of partials > 4 MiB
+    desc.lse = 1  # a supplied LSE: only the partials count
+    assert lib.ds_retrieval_step_static(None, desc, None) == _lib.DS_ERR_INVALID
+    assert b"score partials need 8388608 bytes" in lib.ds_last_error()
+    desc.max_chunks, desc.lse = 512, None  # partials fit; pairs: 64 x 64 x 512 x 8 B = 16 MiB > 12 MiB
+    assert lib.ds_retrieval_step_static(None, desc, None) == _lib.DS_ERR_INVALID
+    assert b"(max, sum) pairs" in lib.ds_last_error()
+    desc.score_partials = 64  # caller scratch is refused: it lives in the static array
+    assert lib.ds_retrieval_step_static(None, desc, None) == _lib.DS_ERR_INVALID
+    assert b"takes no score_partials" in lib.ds_last_error()

@@ -123,6 +123,7 @@ struct FusedArgs {
   int selectors;
   uint32_t owner_spins;  // polls a scorer waits for a plan (0: every task goes to the selectors)
   int expire;            // test flag: every selector raises kStatusPartials as if a wait had expired
+  uint32_t* status_out;  // optional caller word that also receives the launch's status bits
 };
 
 // The read-modify-write completes before the thread goes on (acquire), so
@@ -460,7 +461,12 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
     if (prev == gridDim.x - 1) {
       const uint32_t bits =
           __hip_atomic_exchange(f.header + kLaunchStatus, 0u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-      if (bits != 0u) __hip_atomic_fetch_or(f.header + kStatus, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (bits != 0u) {
+        __hip_atomic_fetch_or(f.header + kStatus, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (f.status_out != nullptr) {
+          __hip_atomic_fetch_or(f.status_out, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
       coherent_store(f.header + kDone, 0u);
       coherent_store(f.header + kEpoch, tag);
     }
@@ -515,7 +521,8 @@ size_t fused_workspace_bytes(int rows, int max_chunks, int num_kv_heads, int tok
 
 // Runs the whole step as one launch when the descriptor fits the fused
 // kernel; `launched` stays false (and nothing is launched) otherwise.
-int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource& src, bool& launched) {
+int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource& src, uint32_t* status_out,
+                      bool& launched) {
   launched = false;
   // Without a supplied LSE a row's scores need all of its chunks first: the chain runs.
   if (d->workspace == nullptr || d->stages != DS_STAGE_ALL || d->lse == nullptr) return clear_error();
@@ -569,6 +576,7 @@ int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource
   f.selectors = std::min(d->batch_rows, kSelectors);
   f.owner_spins = (d->flags & DS_STEP_SELECTORS_GATHER) != 0 ? 0u : kOwnerSpins;
   f.expire = (d->flags & DS_STEP_EXPIRE_WAITS) != 0 ? 1 : 0;
+  f.status_out = status_out;
   const int ppw = 64 / f.g.lanes_per_row;
   const int64_t upper_tasks = static_cast<int64_t>(d->batch_rows) * ((f.g.pos_limit + ppw - 1) / ppw);
   const bool neox = d->is_neox_style != 0;

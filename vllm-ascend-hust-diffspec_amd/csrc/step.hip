@@ -32,14 +32,13 @@ int rebuild_compact_kv_impl(hipStream_t stream, int dtype, const void* raw_key, 
                             int rotary_dim, int is_neox_style, int max_width, const int32_t* row_active,
                             bool padded_rows);
 
-int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource& src, bool& launched);
+int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource& src, uint32_t* status_out,
+                      bool& launched);
 
-}  // namespace ds355
-
-extern "C" int ds_retrieval_step(ds_stream_t stream_handle, const ds_step_desc* d) {
-  using namespace ds355;
+// The step for a descriptor whose scratch buffers are already set.
+// status_out (optional): a single launch ORs its status bits into it.
+int retrieval_step(hipStream_t stream, const ds_step_desc* d, uint32_t* status_out) {
   DS_REQUIRE(d != nullptr, "null step descriptor");
-  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_handle);
   const bool score = (d->stages & DS_STAGE_SCORE) != 0;
   const bool select = (d->stages & DS_STAGE_SELECT) != 0;
   const bool rebuild = (d->stages & DS_STAGE_PLAN) != 0;
@@ -72,7 +71,7 @@ extern "C" int ds_retrieval_step(ds_stream_t stream_handle, const ds_step_desc* 
   }
   src.max_len = static_cast<int>(std::min<int64_t>(static_cast<int64_t>(d->max_chunks) * d->chunk_size, INT32_MAX));
   bool launched = false;
-  int rc = launch_fused_step(stream, d, src, launched);
+  int rc = launch_fused_step(stream, d, src, status_out, launched);
   if (rc != DS_OK || launched) return rc;
   if (score) {
     rc = launch_chunk_scores(stream, d->dtype, d->query, d->q_stride, d->key_cache, d->k_block_stride,
@@ -97,4 +96,10 @@ extern "C" int ds_retrieval_step(ds_stream_t stream_handle, const ds_step_desc* 
                                  d->num_slots, d->max_model_len, d->draft_heads, d->draft_head_dim, d->token_budget,
                                  d->chunk_size, d->rotary_dim, d->is_neox_style, d->history_budget, d->row_active,
                                  true);
+}
+
+}  // namespace ds355
+
+extern "C" int ds_retrieval_step(ds_stream_t stream, const ds_step_desc* d) {
+  return ds355::retrieval_step(reinterpret_cast<hipStream_t>(stream), d, nullptr);
 }

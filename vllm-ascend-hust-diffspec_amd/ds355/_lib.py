@@ -20,6 +20,8 @@ DS_BF16, DS_FP16, DS_FP32 = 0, 1, 2
 DS_HEAD_MEAN, DS_HEAD_MAX = 0, 1
 DS_STAGE_SCORE, DS_STAGE_SELECT, DS_STAGE_PLAN, DS_STAGE_ALL = 1, 2, 4, 7
 DS_STEP_SELECTORS_GATHER, DS_STEP_EXPIRE_WAITS = 1, 2
+# Regions of the static scratch of ds_retrieval_step_static (include/ds355.h).
+DS_STATIC_FUSED_BYTES, DS_STATIC_PARTIALS_BYTES, DS_STATIC_PAIRS_BYTES = 8 << 20, 4 << 20, 12 << 20
 ABI_VERSION = 6
 
 EXPORTED_SYMBOLS = (
@@ -30,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "ds_build_plan",
     "ds_rebuild_compact_kv",
     "ds_retrieval_step",
+    "ds_retrieval_step_static",
     "ds_step_workspace_bytes",
     "ds_draft_attention",
     "ds_draft_attention_workspace_bytes",
@@ -102,6 +105,7 @@ _SIGNATURES = {
         _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p,
     ]),
     "ds_retrieval_step": (_i32, [_p, ctypes.POINTER(StepDesc)]),
+    "ds_retrieval_step_static": (_i32, [_p, ctypes.POINTER(StepDesc), _p]),
     "ds_step_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32, _i32]),
     "ds_draft_attention": (_i32, [
         _p, _i32, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64,

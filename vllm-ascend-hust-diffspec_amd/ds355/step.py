@@ -87,6 +87,27 @@ def launch(desc: _lib.StepDesc, device: torch.device, stages: int | None = None)
             desc.stages = saved
 
 
+def launch_static(desc: _lib.StepDesc, device: torch.device, status: torch.Tensor | None = None) -> None:
+    """Launch a prebuilt descriptor through ``ds_retrieval_step_static``.
+
+    The step's scratch (score partials, the single launch's workspace, the
+    LSE pairs) then lives in the library's static device array, so the
+    descriptor's ``score_partials``, ``workspace`` and ``lse_partials`` are
+    cleared for this call (the descriptor itself is not changed).  Nothing is
+    allocated.  ``status`` (an int32 device word the caller clears) receives
+    the status bits of a single launch whose bounded wait expired.  Calls
+    that overlap on one GPU share that array and must be serialised.
+    """
+    local = _lib.StepDesc.from_buffer_copy(desc)
+    local.score_partials = None
+    local.workspace = None
+    local.workspace_bytes = 0
+    local.lse_partials = None
+    if status is not None and (status.dtype != torch.int32 or status.device != device or status.numel() < 1):
+        raise ValueError("status must be an int32 device word on the step's device")
+    _lib.check(_lib.load().ds_retrieval_step_static(_lib.stream_handle(device), local, _lib.ptr(status)))
+
+
 def build_step_desc(
     *,
     stages: int = ALL,

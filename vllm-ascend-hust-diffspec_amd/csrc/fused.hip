@@ -126,10 +126,11 @@ struct FusedArgs {
   uint32_t* status_out;  // optional caller word that also receives the launch's status bits
 };
 
-// The read-modify-write completes before the thread goes on (acquire), so
-// the bit is in memory before the workgroup counts itself done.
+// The read-modify-write completes before the thread goes on (acquire: the
+// wave waits for its return), so the bit is in memory before the workgroup
+// counts itself done.  No release: that would write back the XCD's L2.
 __device__ __forceinline__ void raise_status(uint32_t* header, uint32_t bit) {
-  __hip_atomic_fetch_or(header + kLaunchStatus, bit, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_fetch_or(header + kLaunchStatus, bit, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
 }
 // A wait without deadline gives up after kSpinLimit polls, or early once
 // another wait of this launch has.
@@ -454,13 +455,16 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
 
   // The last workgroup to finish hands this launch's status bits to the
   // owner's word, clears them for the next launch and publishes the tag as
-  // the epoch.
+  // the epoch.  Every raise of a workgroup has returned before that
+  // workgroup's count (the barrier below orders them), so the last count
+  // comes after every raise.  The atomics are relaxed: a release here would
+  // write back the XCD's L2 in every workgroup.
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(f.header + kDone, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t prev = __hip_atomic_fetch_add(f.header + kDone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (prev == gridDim.x - 1) {
       const uint32_t bits =
-          __hip_atomic_exchange(f.header + kLaunchStatus, 0u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_exchange(f.header + kLaunchStatus, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (bits != 0u) {
         __hip_atomic_fetch_or(f.header + kStatus, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (f.status_out != nullptr) {

@@ -115,6 +115,113 @@ __global__ __launch_bounds__(kThreads) void gather_scalar_kernel(GatherArgs a, i
   }
 }
 
+// Where plan rows come from when the gather builds them itself: the
+// per-slot selection state and each row's committed length.
+struct PlanSource {
+  const int32_t* sel_ids;    // [num_slots, sel_stride] ascending chunk ids
+  int64_t sel_stride;
+  const int32_t* sel_count;  // [num_slots]: -1 none, 0 empty, n ids
+  const int32_t* slots;      // [rows]; outside [0, num_slots): padding
+  const int32_t* committed;  // [rows] root position + 1
+  int64_t* plan;             // [rows, plan_width] output
+  int32_t* working_lens;     // [num_slots] output, or nullptr
+  int hb, window, cap;       // history budget, rolling tail, chunk ids per plan row (<= 128)
+};
+
+// Plan and gather of one row in one launch (the compact prefill of
+// diffspec/runtime.py:1737-1765 + compact_kv.py:8-133 without a plan kernel
+// in between).  Workgroup (r, blk) covers local positions [blk * 4 * ppw,
+// (blk + 1) * 4 * ppw) of row r, one task of ppw positions per wave.  Each
+// wave derives the row's plan itself (diffspec/runtime.py:1713-1735, the
+// arithmetic of write_plan_row): the slot and committed length, then the
+// slot's selection count and ids in the same round trip (lane l holds ids l
+// and 64 + l), a wave sum for the prefix tokens.  Workgroup (r, 0) stores the
+// plan row and working_lens[slot].  Then the wave moves its positions with
+// the chunk ids taken from its own registers.
+template <int DT, bool NEOX, int HG>
+__global__ __launch_bounds__(kThreads) void plan_gather_kernel(GatherArgs a, PlanSource ps) {
+  const int lane = static_cast<int>(threadIdx.x) & 63;
+  const int wave = static_cast<int>(threadIdx.x) >> 6;
+  const int r = static_cast<int>(blockIdx.y);
+  const int ppw = 64 / a.lanes_per_row;
+  const int p0 = (static_cast<int>(blockIdx.x) * (kThreads / 64) + wave) * ppw;
+
+  const int slot = scalar_load(ps.slots + r);
+  const int committed = scalar_load(ps.committed + r);
+  const bool active = a.row_active == nullptr || scalar_load(a.row_active + r) != 0;
+  const bool slot_ok = slot >= 0 && slot < a.num_slots;
+  const bool writer = blockIdx.x == 0 && wave == 0;
+  int count = -1;
+  uint32_t lo = 0, hi = 0;
+  if (slot_ok) {
+    const int32_t* ids = ps.sel_ids + static_cast<int64_t>(slot) * ps.sel_stride;
+    count = scalar_load(ps.sel_count + slot);
+    lo = lane < ps.cap ? static_cast<uint32_t>(ids[lane]) : 0u;
+    hi = lane + 64 < ps.cap ? static_cast<uint32_t>(ids[lane + 64]) : 0u;
+  }
+  if (!slot_ok) {  // padding row: a zero plan row, nothing gathered
+    if (writer) {
+      int64_t* prow = ps.plan + static_cast<int64_t>(r) * a.plan_width;
+      for (int j = lane; j < a.plan_width; j += 64) prow[j] = 0;
+    }
+    return;
+  }
+  const int n = count < 0 ? -1 : min(count, ps.cap);
+  const int64_t end = max(0, committed - 1);
+  const int64_t hb = ps.hb;
+  int64_t len, tail_start, prefix_len = 0, drop = 0;
+  if (n < 0) {
+    len = min(end, hb);
+    tail_start = end - len;
+  } else {
+    const int64_t tail_len = min(min(end, static_cast<int64_t>(ps.window)), hb);
+    tail_start = end - tail_len;
+    len = tail_len;
+    if (n > 0) {
+      const int lastc = n - 1;
+      const uint32_t last = lastc < 64 ? __builtin_amdgcn_readlane(lo, lastc) : __builtin_amdgcn_readlane(hi, lastc - 64);
+      const int64_t prefix_end = min(tail_start, static_cast<int64_t>(last) * a.chunk);
+      auto clipped = [&](uint32_t id, bool in) -> int {
+        const int64_t t = prefix_end - static_cast<int64_t>(id) * a.chunk;
+        return !in || t <= 0 ? 0 : static_cast<int>(t < a.chunk ? t : a.chunk);
+      };
+      const int64_t prefix_tokens = wave_sum_int(clipped(lo, lane < n) + clipped(hi, lane + 64 < n));
+      prefix_len = min(prefix_tokens, hb - tail_len);
+      drop = prefix_tokens - prefix_len;
+      len = prefix_len + tail_len;
+    }
+  }
+  if (writer) {
+    int64_t* prow = ps.plan + static_cast<int64_t>(r) * a.plan_width;
+    const int ncols = max(n, 0);
+    // Whole-wave iterations: a lane permute reads only lanes that are active.
+    for (int base = 0; base < a.plan_width; base += 64) {
+      const int j = base + lane;
+      const int c = j - 5;
+      const uint32_t lv = __builtin_amdgcn_ds_bpermute((c & 63) << 2, static_cast<int>(lo));
+      const uint32_t hv = __builtin_amdgcn_ds_bpermute((c & 63) << 2, static_cast<int>(hi));
+      int64_t v;
+      if (j == 0) v = slot;
+      else if (j == 1) v = len;
+      else if (j == 2) v = tail_start;
+      else if (j == 3) v = prefix_len;
+      else if (j == 4) v = drop;
+      else v = c < ncols ? static_cast<int64_t>(c < 64 ? lv : hv) : 0;
+      if (j < a.plan_width) prow[j] = v;
+    }
+    if (lane == 0 && ps.working_lens != nullptr) ps.working_lens[slot] = static_cast<int32_t>(len);
+  }
+  const int64_t limit = min(len, static_cast<int64_t>(a.pos_limit));
+  if (!active || p0 >= limit) return;
+  const GatherLane L = gather_lane<DT, NEOX>(a);
+  gather_task<DT, NEOX, HG>(a, L, p0, slot, limit, tail_start, prefix_len, drop, [&](int64_t c) {
+    const int col = static_cast<int>(c);
+    const int l = __builtin_amdgcn_ds_bpermute((col & 63) << 2, static_cast<int>(lo));
+    const int h = __builtin_amdgcn_ds_bpermute((col & 63) << 2, static_cast<int>(hi));
+    return static_cast<int64_t>(col < 64 ? l : h);
+  });
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // One wave per task, capped at the workgroups that fit on the device at once
@@ -180,6 +287,25 @@ int launch_gather(hipStream_t stream, const GatherArgs& a, bool neox, bool vec, 
   }
   gather_scalar_kernel<DT><<<grid, kThreads, 0, stream>>>(a, neox ? 1 : 0);
   return check_launch("ds_rebuild_compact_kv");
+}
+
+template <int DT>
+int launch_plan_gather_dt(hipStream_t stream, const GatherArgs& a, const PlanSource& ps, bool neox) {
+  const int ppw = 64 / a.lanes_per_row;
+  const int per_wg = (kThreads / 64) * ppw;
+  const dim3 grid(static_cast<unsigned>(std::max(1, (a.pos_limit + per_wg - 1) / per_wg)),
+                  static_cast<unsigned>(a.rows));
+  if (a.heads >= 4) {
+    if (neox) plan_gather_kernel<DT, true, 4><<<grid, kThreads, 0, stream>>>(a, ps);
+    else plan_gather_kernel<DT, false, 4><<<grid, kThreads, 0, stream>>>(a, ps);
+  } else if (a.heads >= 2) {
+    if (neox) plan_gather_kernel<DT, true, 2><<<grid, kThreads, 0, stream>>>(a, ps);
+    else plan_gather_kernel<DT, false, 2><<<grid, kThreads, 0, stream>>>(a, ps);
+  } else {
+    if (neox) plan_gather_kernel<DT, true, 1><<<grid, kThreads, 0, stream>>>(a, ps);
+    else plan_gather_kernel<DT, false, 1><<<grid, kThreads, 0, stream>>>(a, ps);
+  }
+  return check_launch("plan + gather");
 }
 
 }  // namespace
@@ -264,6 +390,52 @@ int rebuild_compact_kv_impl(hipStream_t stream, int dtype, const void* raw_key, 
     case DS_FP16: return launch_gather<DS_FP16>(stream, a, neox, vec, grid);
     default: return launch_gather<DS_FP32>(stream, a, neox, vec, grid);
   }
+}
+
+// Plans from the slot selections and the gather, as one launch.  Sets
+// `launched` when it ran; shapes the vector path does not cover (or more
+// than 128 chunk ids per plan row) launch nothing, and the caller runs the
+// plan kernel and the gather instead.
+int launch_plan_gather(hipStream_t stream, int dtype, const void* raw_key, const void* raw_value,
+                       void* working_key, void* working_value, int rows, int plan_width, const void* cos_sin,
+                       int64_t cs_stride, int cs_rows, int num_slots, int max_model_len, int heads, int head_dim,
+                       int token_budget, int chunk_size, int rotary_dim, int is_neox_style, int history_budget,
+                       const int32_t* row_active, const int32_t* sel_ids, int64_t sel_stride,
+                       const int32_t* sel_count, const int32_t* slots, const int32_t* committed_lens, int64_t* plan,
+                       int32_t* working_lens, int recent_window, bool& launched) {
+  launched = false;
+  GatherArgs a;
+  bool vec = false;
+  int grid = 0;
+  int rc = make_gather_args(a, vec, grid, dtype, raw_key, raw_value, working_key, working_value, plan, rows,
+                            plan_width, cos_sin, cs_stride, cs_rows, num_slots, max_model_len, heads, head_dim,
+                            token_budget, chunk_size, rotary_dim, is_neox_style, history_budget, row_active, true);
+  if (rc != DS_OK) return rc;
+  const int64_t cap = std::min<int64_t>(plan_width - 5, sel_stride);
+  if (rows == 0 || !vec || cap > 128 || grid <= 0) return clear_error();
+  DS_REQUIRE(sel_ids && sel_count && slots && committed_lens && plan, "null plan pointer");
+  DS_REQUIRE(recent_window > 0, "recent_window must be positive");
+  DS_REQUIRE(history_budget >= chunk_size && history_budget % chunk_size == 0,
+             "history_budget must be a positive chunk-size multiple");
+  PlanSource ps{};
+  ps.sel_ids = sel_ids;
+  ps.sel_stride = sel_stride;
+  ps.sel_count = sel_count;
+  ps.slots = slots;
+  ps.committed = committed_lens;
+  ps.plan = plan;
+  ps.working_lens = working_lens;
+  ps.hb = history_budget;
+  ps.window = recent_window;
+  ps.cap = static_cast<int>(cap);
+  const bool neox = is_neox_style != 0;
+  switch (dtype) {
+    case DS_BF16: rc = launch_plan_gather_dt<DS_BF16>(stream, a, ps, neox); break;
+    case DS_FP16: rc = launch_plan_gather_dt<DS_FP16>(stream, a, ps, neox); break;
+    default: rc = launch_plan_gather_dt<DS_FP32>(stream, a, ps, neox); break;
+  }
+  launched = rc == DS_OK;
+  return rc;
 }
 
 }  // namespace ds355

@@ -35,6 +35,14 @@ int rebuild_compact_kv_impl(hipStream_t stream, int dtype, const void* raw_key, 
 int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource& src, uint32_t* status_out,
                       bool& launched);
 
+int launch_plan_gather(hipStream_t stream, int dtype, const void* raw_key, const void* raw_value,
+                       void* working_key, void* working_value, int rows, int plan_width, const void* cos_sin,
+                       int64_t cs_stride, int cs_rows, int num_slots, int max_model_len, int heads, int head_dim,
+                       int token_budget, int chunk_size, int rotary_dim, int is_neox_style, int history_budget,
+                       const int32_t* row_active, const int32_t* sel_ids, int64_t sel_stride,
+                       const int32_t* sel_count, const int32_t* slots, const int32_t* committed_lens, int64_t* plan,
+                       int32_t* working_lens, int recent_window, bool& launched);
+
 // The step for a descriptor whose scratch buffers are already set.
 // status_out (optional): a single launch ORs its status bits into it.
 int retrieval_step(hipStream_t stream, const ds_step_desc* d, uint32_t* status_out) {
@@ -81,6 +89,18 @@ int retrieval_step(hipStream_t stream, const ds_step_desc* d, uint32_t* status_o
                              d->score_partials, nullptr, 0, 0, SIZE_MAX, d->lse_partials, d->lse_out,
                              d->lse_out_stride);
     if (rc != DS_OK) return rc;
+  }
+  if (rebuild && !select) {
+    // The compact prefill alone: plans and gather in one launch when the
+    // gather's vector path covers the shapes.
+    bool one = false;
+    rc = launch_plan_gather(stream, d->kv_dtype, d->raw_key, d->raw_value, d->working_key, d->working_value,
+                            d->batch_rows, d->plan_width, d->cos_sin, d->cs_stride, d->cs_rows, d->num_slots,
+                            d->max_model_len, d->draft_heads, d->draft_head_dim, d->token_budget, d->chunk_size,
+                            d->rotary_dim, d->is_neox_style, d->history_budget, d->row_active, d->sel_ids,
+                            d->sel_stride, d->sel_count, d->slots, d->committed_lens, d->plan, d->working_lens,
+                            d->recent_window, one);
+    if (rc != DS_OK || one) return rc;
   }
   if (select || rebuild) {
     rc = launch_select_plan(stream, d->scores, d->max_chunks, d->score_partials, d->max_chunks, d->num_kv_heads,

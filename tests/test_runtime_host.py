@@ -47,6 +47,11 @@ def launches(monkeypatch):
     return calls
 
 
+def _first(t, n):
+    """The first n entries of a per-row array (the runtime passes whole staging rows; kernels read batch_size)."""
+    return t[:n].tolist()
+
+
 def _metadata(query_ends, seq_lens, prefill):
     return SimpleNamespace(actual_seq_lengths_q=query_ends, seq_lens_list=seq_lens,
                            block_tables=torch.zeros((len(seq_lens), 1), dtype=torch.int32),
@@ -97,10 +102,10 @@ def test_retrieval_skips_prefill_snapshot_and_interval(launches):
     assert len(launches) == 1
     call = launches[0]
     assert call["stages"] == step.SCORE | step.SELECT
-    assert call["rows"].counts.tolist() == [1, 1]
-    assert call["rows"].query_start.tolist() == [0, 1]
-    assert call["rows"].query_len.tolist() == [1, 1]
-    assert call["rows"].target_len.tolist() == [6, 4]
+    assert _first(call["rows"].counts, call["rows"].batch_size) == [1, 1]
+    assert _first(call["rows"].query_start, call["rows"].batch_size) == [0, 1]
+    assert _first(call["rows"].query_len, call["rows"].batch_size) == [1, 1]
+    assert _first(call["rows"].target_len, call["rows"].batch_size) == [6, 4]
     assert call["slots"].tolist() == cache._active_slots
     assert call["snapshot"].scale == 0.5
     status = cache.retrieval_status()
@@ -163,10 +168,10 @@ def test_speculative_rows_and_graph_padding(launches):
     cache.accept_target_queries(torch.tensor([3, 0, 5, 9, 9]), is_prefill=False)
     call = launches[-1]
     assert call["rows"].batch_size == 3  # padding rows are dropped (runtime.py:1211-1222)
-    assert call["rows"].counts.tolist() == [3, 0, 5]
-    assert call["rows"].query_start.tolist() == [0, 5, 10]
-    assert call["rows"].query_len.tolist() == [5, 5, 5]
-    assert call["rows"].target_len.tolist() == [20, 30, 12]
+    assert _first(call["rows"].counts, call["rows"].batch_size) == [3, 0, 5]
+    assert _first(call["rows"].query_start, call["rows"].batch_size) == [0, 5, 10]
+    assert _first(call["rows"].query_len, call["rows"].batch_size) == [5, 5, 5]
+    assert _first(call["rows"].target_len, call["rows"].batch_size) == [20, 30, 12]
     assert call["score_partials"].shape == (3, cache.max_chunks, 1)
     # A verifier longer than the score buffer is refused on the host.
     meta.seq_lens_list = [40, 30, 12, 1, 1]
@@ -229,7 +234,7 @@ def attention_calls(monkeypatch):
     calls = []
 
     def record(query, key, value, output, working_key, working_value, working_lens, slots, positions=None, *,
-               scale, workspace):
+               scale, workspace, reuse=None):
         calls.append(dict(slots=slots.tolist() if isinstance(slots, torch.Tensor) else list(slots),
                           positions=positions.tolist() if isinstance(positions, torch.Tensor) else positions,
                           scale=scale, rows=output.shape[0]))
@@ -278,7 +283,7 @@ def capture_calls(monkeypatch):
     calls = []
 
     def record(key, value, raw_key, raw_value, token_slots, absolute_positions, rope_buffer, *, tokens,
-               working_lens=None, local_positions=None, prev_count=0, status=None):
+               working_lens=None, local_positions=None, prev_count=0, status=None, reuse=None):
         calls.append(dict(slots=token_slots[:tokens].tolist(), positions=absolute_positions.reshape(-1).tolist(),
                           tokens=tokens, rope=rope_buffer is not None, working_lens=working_lens is not None,
                           key=key[:tokens].clone()))
@@ -318,7 +323,7 @@ def test_linear_call_sequence_of_the_plugin(launches, attention_calls, capture_c
     assert cache.proposed_token_ids is None and cache.proposed_depths_cpu == []
     cache.accept_target_queries(torch.tensor([2, 4]), is_prefill=cache.target_is_prefill)
     assert launches[-1]["stages"] == step.SCORE | step.SELECT
-    assert launches[-1]["rows"].counts.tolist() == [2, 4]
+    assert _first(launches[-1]["rows"].counts, 2) == [2, 4]
     assert not cache.target_tree_active  # prepare_inputs_padded returns its result unchanged
     with pytest.raises(RuntimeError, match="tree has not been verified"):
         cache.accepted_target_token_indices()

@@ -92,6 +92,7 @@ def draft_linear_attention(
     *,
     scale: float,
     workspace: torch.Tensor,
+    reuse: dict | None = None,
 ) -> torch.Tensor:
     """One linear draft-attention step for ``len(slots)`` rows.
 
@@ -101,8 +102,26 @@ def draft_linear_attention(
     device).  ``query``/``output`` are ``[tokens, Hq, D]`` (or ``[tokens,
     Hq*D]``), ``key``/``value`` ``[tokens, Hkv, D]``, the working caches
     ``[slots, Hkv, token_budget, D]`` contiguous, ``working_lens`` int32.
-    Returns ``output``.
+    Returns ``output``.  ``reuse`` (a dict the caller keeps) holds validated
+    launch arguments per layout: a later call whose tensors differ only in
+    their addresses skips the checks.
     """
+    sig = None
+    if reuse is not None and isinstance(slots, torch.Tensor) and (positions is None
+                                                                   or isinstance(positions, torch.Tensor)):
+        sig = (query.shape, query.stride(), key.shape, key.stride(), value.shape, value.stride(), output.shape,
+               output.stride(), query.dtype, key.dtype, value.dtype, output.dtype, query.device,
+               working_key.data_ptr(), working_value.data_ptr(), working_lens.data_ptr(), workspace.data_ptr(),
+               slots.data_ptr(), slots.shape, slots.dtype, slots.device,
+               None if positions is None else (positions.data_ptr(), positions.shape, positions.dtype,
+                                               positions.device), float(scale))
+        args = reuse.get(sig)
+        if args is not None:
+            args[0] = _lib.stream_handle(query.device)
+            args[2], args[5], args[8], args[11] = (query.data_ptr(), key.data_ptr(), value.data_ptr(),
+                                                   output.data_ptr())
+            _lib.check(_lib.load().ds_draft_attention(*args))
+            return output
     num_slots, hkv, budget, head_dim = working_key.shape
     if working_value.shape != working_key.shape:
         raise ValueError("working key and value caches must have the same shape")
@@ -144,8 +163,7 @@ def draft_linear_attention(
     device = _lib.require_gpu(q, k, v, out, working_key, working_value, working_lens, workspace)
     slot_t = _int32_rows(slots, rows, device, "slots")
     pos_t = None if positions is None else _int32_rows(positions, rows, device, "positions")
-    lib = _lib.load()
-    _lib.check(lib.ds_draft_attention(
+    args = [
         _lib.stream_handle(device), _lib.dtype_code(working_key.dtype),
         q.data_ptr(), q.stride(0), q.stride(1),
         k.data_ptr(), k.stride(0), k.stride(1),
@@ -155,5 +173,12 @@ def draft_linear_attention(
         slot_t.data_ptr() if rows else None, _lib.ptr(pos_t) if rows else None,
         rows, out.shape[0], num_slots, hq, hkv, head_dim, budget, float(scale),
         workspace.data_ptr(), workspace.numel(),
-    ))
+    ]
+    _lib.check(_lib.load().ds_draft_attention(*args))
+    if (sig is not None and rows and slot_t.data_ptr() == slots.data_ptr()
+            and (positions is None or pos_t.data_ptr() == positions.data_ptr())):
+        # Same tensors next time: only the activations' addresses change.
+        if len(reuse) >= 64:
+            reuse.clear()
+        reuse[sig] = args
     return output

@@ -41,6 +41,7 @@ def capture_raw_kv_rows(
     local_positions: torch.Tensor | None = None,
     prev_count: int = 0,
     status: torch.Tensor | None = None,
+    reuse: dict | None = None,
 ) -> torch.Tensor | None:
     """Scatter the first ``tokens`` rows of ``key``/``value`` into the raw caches
     at ``[token_slots[t], absolute_positions[t]]`` and write the RoPE input.
@@ -51,7 +52,26 @@ def capture_raw_kv_rows(
     ``local_positions``, else the absolute positions.  ``rope_buffer[count:
     prev_count]`` is zeroed.  Returns the view.  With ``rope_buffer=None``
     only the rows are scattered (``populate_prefill``) and None is returned.
+    ``reuse`` (a dict the caller keeps) holds validated launch arguments per
+    layout: a later call whose tensors differ only in their addresses skips
+    the checks.
     """
+    sig = None
+    if reuse is not None:
+        sig = (key.shape, key.stride(), value.shape, value.stride(), key.dtype, value.dtype, key.device,
+               absolute_positions.shape, absolute_positions.stride(), absolute_positions.dtype,
+               raw_key.data_ptr(), raw_value.data_ptr(), token_slots.data_ptr(), token_slots.numel(),
+               token_slots.dtype, None if rope_buffer is None else rope_buffer.data_ptr(), tokens,
+               None if working_lens is None else working_lens.data_ptr(),
+               None if local_positions is None else (local_positions.data_ptr(), local_positions.shape,
+                                                    local_positions.dtype),
+               prev_count, None if status is None else status.data_ptr())
+        args = reuse.get(sig)
+        if args is not None:
+            args[0] = _lib.stream_handle(key.device)
+            args[2], args[5], args[8] = key.data_ptr(), value.data_ptr(), absolute_positions.data_ptr()
+            _lib.check(_lib.load().ds_capture_raw_kv(*args))
+            return None if rope_buffer is None else rope_buffer[: args[21]].view(absolute_positions.shape)
     num_slots, max_model_len, heads, head_dim = raw_key.shape
     if raw_value.shape != raw_key.shape or not (raw_key.is_contiguous() and raw_value.is_contiguous()):
         raise ValueError("raw key/value must have matching contiguous 4-D shapes")
@@ -88,14 +108,19 @@ def capture_raw_kv_rows(
         raise ValueError("working_lens must be a contiguous int32 tensor")
     device = _lib.require_gpu(k, v, raw_key, raw_value, token_slots, positions, rope_buffer, working_lens, local,
                               status)
-    _lib.check(_lib.load().ds_capture_raw_kv(
+    args = [
         _lib.stream_handle(device), _lib.dtype_code(raw_key.dtype),
         k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
         positions.data_ptr(), 1 if positions.dtype == torch.int64 else 0,
         token_slots.data_ptr(), tokens, raw_key.data_ptr(), raw_value.data_ptr(),
         num_slots, max_model_len, heads, head_dim,
         _lib.ptr(working_lens), _lib.ptr(local), _lib.ptr(rope_buffer), count, prev_count, _lib.ptr(status),
-    ))
+    ]
+    _lib.check(_lib.load().ds_capture_raw_kv(*args))
+    if sig is not None and positions.data_ptr() == absolute_positions.data_ptr():
+        if len(reuse) >= 64:
+            reuse.clear()
+        reuse[sig] = args
     if rope_buffer is None:
         return None
     return rope_buffer[:count].view(absolute_positions.shape)

@@ -217,6 +217,10 @@ class DiffSpecDraftCache:
         self._rope_position_written: dict[torch.dtype, int] = {}
         self._capture_status = torch.zeros((1,), dtype=torch.int32, device=self.device)
         self._token_staging: _Staging | None = None  # token -> slot rows of populate_prefill
+        self._step_descs: dict = {}  # validated step descriptors, reused while the shapes stay
+        self._views: dict = {}  # slices of the cache's own buffers per batch size (slicing costs microseconds)
+        self._attention_reuse: dict = {}
+        self._capture_reuse: dict = {}
         # Verification is linear: this cache proposes no draft tree, so the
         # reference's tree activation (runtime.py:795-813) never fires and
         # these keep their "no tree" values (runtime.py:708-712).
@@ -225,6 +229,14 @@ class DiffSpecDraftCache:
         self.proposed_parent_indices: torch.Tensor | None = None
         self.proposed_depths: torch.Tensor | None = None
         self.proposed_depths_cpu: list[int] = []
+
+    def _view(self, name: str, rows: int, make) -> torch.Tensor:
+        """A slice of one of the cache's buffers, made once per batch size."""
+        key = (name, rows)
+        view = self._views.get(key)
+        if view is None:
+            view = self._views[key] = make()
+        return view
 
     # -- draft cycle (runtime.py:731-753) -----------------------------------------------------------
     def begin_cycle(self, request_ids: list[str]) -> None:
@@ -410,11 +422,17 @@ class DiffSpecDraftCache:
         staged = self._rows_staging.upload([
             starts, lens, self._target_seq_lens[:batch_size], self._active_slots, [],
         ])
-        counts = staged[4, :batch_size]
-        counts.copy_(valid_sampled_token_count.reshape(-1)[:batch_size])  # device-side cast, no sync
+        # Whole staging rows serve any batch size (the kernels read the first
+        # batch_size entries); int32 device counts are read where they are.
+        counts = valid_sampled_token_count
+        if (counts.dtype != torch.int32 or counts.device != self.device or not counts.is_contiguous()
+                or counts.numel() < batch_size):
+            counts = self._view("counts", batch_size, lambda: staged[4, :batch_size])
+            counts.copy_(valid_sampled_token_count.reshape(-1)[:batch_size])  # device-side cast, no sync
         rows = _step.VerifierRows(
-            counts=staged[4, :batch_size], query_start=staged[0, :batch_size],
-            query_len=staged[1, :batch_size], target_len=staged[2, :batch_size], batch_size=batch_size,
+            counts=counts, query_start=self._view("qs", 0, lambda: staged[0]),
+            query_len=self._view("ql", 0, lambda: staged[1]), target_len=self._view("tl", 0, lambda: staged[2]),
+            batch_size=batch_size,
         )
         snapshot = _step.VerifierSnapshot(
             query=self._target_query, lse=self._target_lse, key_cache=self._target_key_cache,
@@ -422,7 +440,8 @@ class DiffSpecDraftCache:
         )
         started = time.perf_counter()
         self._launch(_step.SCORE | _step.SELECT, batch_size, snapshot=snapshot, rows=rows,
-                     slots=staged[3, :batch_size], committed=staged[2, :batch_size])
+                     slots=self._view("rs", batch_size, lambda: staged[3, :batch_size]),
+                     committed=self._view("rc", batch_size, lambda: staged[2, :batch_size]))
         self.metrics.observe_retrieval(time.perf_counter() - started)
 
     # -- rebuild (runtime.py:1349-1371, 1683-1765) ------------------------------------------------
@@ -451,8 +470,9 @@ class DiffSpecDraftCache:
             staged[1, :rows].copy_(seq_lens.reshape(-1)[:rows])
         else:
             staged = self._plan_staging.upload([slots, list(seq_lens[:rows])])
-        self._launch(_step.PLAN, rows, slots=staged[0, :rows], committed=staged[1, :rows])
-        self.local_positions = self.plan[:rows, 1]
+        self._launch(_step.PLAN, rows, slots=self._view("ps", rows, lambda: staged[0, :rows]),
+                     committed=self._view("pc", rows, lambda: staged[1, :rows]))
+        self.local_positions = self._view("roots", rows, lambda: self.plan[:rows, 1])
         # The root token attends at its history length (runtime.py:1366-1369),
         # which the plan launch also stored as the slot's working length.
         self._pending_request_indices = list(slots)
@@ -490,7 +510,7 @@ class DiffSpecDraftCache:
             positions = positions.contiguous()
         _capture.capture_raw_kv_rows(
             key, value, self.raw_key, self.raw_value, slots, positions, None, tokens=num_tokens,
-            status=self._capture_status)
+            status=self._capture_status, reuse=self._capture_reuse)
 
     # -- raw KV capture and RoPE input (runtime.py:1580-1618, 1767-1877) -------------------------
     @staticmethod
@@ -584,7 +604,8 @@ class DiffSpecDraftCache:
         if self._cycle_open:
             rope = _capture.capture_raw_kv_rows(
                 key, value, self.raw_key, self.raw_value, token_slots, absolute_positions, buffer,
-                tokens=num_tokens, working_lens=self.working_lens, prev_count=prev, status=self._capture_status)
+                tokens=num_tokens, working_lens=self.working_lens, prev_count=prev, status=self._capture_status,
+                reuse=self._capture_reuse)
             self._rope_position_written[dtype] = absolute_positions.numel()
             self._pending_request_indices = list(slots)
             self._pending_local_positions = WORKING_LENS
@@ -682,7 +703,7 @@ class DiffSpecDraftCache:
                 positions = self._attention_staging.upload([[], positions])[1, :rows]
         _attention.draft_linear_attention(
             query, key, value, output, self.working_key, self.working_value, self.working_lens,
-            slot_rows, positions, scale=scale, workspace=workspace,
+            slot_rows, positions, scale=scale, workspace=workspace, reuse=self._attention_reuse,
         )
         self._pending_request_indices = None
         self._pending_local_positions = None
@@ -706,7 +727,8 @@ class DiffSpecDraftCache:
             if self._score_partials is None or self._score_partials.shape[2] != kv_heads:
                 self._score_partials = torch.zeros((self.max_batch_rows, self.max_chunks, kv_heads),
                                                    dtype=torch.float32, device=self.device)
-            partials = self._score_partials[:batch_rows]
+                self._views = {k: v for k, v in self._views.items() if k[0] != "partials"}
+            partials = self._view("partials", batch_rows, lambda: self._score_partials[:batch_rows])
         lse_partials = lse_out = None
         if stages & _step.SCORE and snapshot.lse is None:
             q_heads = snapshot.query.shape[1]
@@ -715,13 +737,26 @@ class DiffSpecDraftCache:
                                                  dtype=torch.float32, device=self.device)
                 self.scored_lse = torch.zeros((self.max_batch_rows, q_heads), dtype=torch.float32,
                                               device=self.device)
-            lse_partials, lse_out = self._lse_partials[:batch_rows], self.scored_lse[:batch_rows]
+                self._views = {k: v for k, v in self._views.items() if k[0] not in ("pairs", "lse_out")}
+            lse_partials = self._view("pairs", batch_rows, lambda: self._lse_partials[:batch_rows])
+            lse_out = self._view("lse_out", batch_rows, lambda: self.scored_lse[:batch_rows])
+        # Everything but buffer addresses that the validated descriptor depends
+        # on: the cache's own buffers keep their shapes, so the key is the
+        # stage mask, the batch and the verifier snapshot's layout.
+        key = (stages, batch_rows, None if rows is None else rows.batch_size, cos_sin.shape, cos_sin.stride(0),
+               rotary.rotary_dim, bool(rotary.is_neox_style))
+        if snapshot is not None:
+            q, lse, kc, bt = snapshot.query, snapshot.lse, snapshot.key_cache, snapshot.block_table
+            key += (q.shape, q.stride(), q.dtype, kc.shape, kc.stride(), kc.dtype, bt.shape, bt.stride(), bt.dtype,
+                    None if lse is None else (lse.shape, lse.stride(), lse.dtype))
         _step.retrieval_step(
+            reuse=self._step_descs, reuse_key=key, fixed_buffers=True,
             stages=stages, snapshot=snapshot, rows=rows,
-            scores=self.scores[:batch_rows] if stages & (_step.SCORE | _step.SELECT) else None,
+            scores=self._view("scores", batch_rows, lambda: self.scores[:batch_rows])
+            if stages & (_step.SCORE | _step.SELECT) else None,
             score_partials=partials,
             sel_ids=self.sel_ids, sel_count=self.sel_count, slots=slots, committed_lens=committed,
-            plan=self.plan[:batch_rows], working_lens=self.working_lens,
+            plan=self._view("plan", batch_rows, lambda: self.plan[:batch_rows]), working_lens=self.working_lens,
             raw_key=self.raw_key, raw_value=self.raw_value,
             working_key=self.working_key, working_value=self.working_value,
             cos_sin_cache=cos_sin, rotary_dim=rotary.rotary_dim, is_neox_style=rotary.is_neox_style,

@@ -64,9 +64,40 @@ SCORE, SELECT, PLAN, ALL = _lib.DS_STAGE_SCORE, _lib.DS_STAGE_SELECT, _lib.DS_ST
 SELECTORS_GATHER, EXPIRE_WAITS = _lib.DS_STEP_SELECTORS_GATHER, _lib.DS_STEP_EXPIRE_WAITS
 
 
-def retrieval_step(**kwargs) -> None:
-    """Run the stages of one step (see ``build_step_desc`` for the arguments)."""
-    desc, device = build_step_desc(**kwargs)
+def retrieval_step(*, reuse: dict | None = None, reuse_key=None, fixed_buffers: bool = False, **kwargs) -> None:
+    """Run the stages of one step (see ``build_step_desc`` for the arguments).
+
+    ``reuse`` (a dict the caller keeps) with ``reuse_key`` skips validation
+    on repeated calls: the descriptor validated at the key's first call is
+    kept and only its buffer addresses, scale and batch size are refreshed.
+    The caller must change the key whenever anything but those changes
+    (stages, shapes, strides, dtypes, devices, policy values, which optional
+    buffers are given).  ``fixed_buffers`` says that, for one key, every
+    buffer but the verifier snapshot's and the committed counts is the same
+    tensor on every call (a runtime's own state): then only those addresses
+    are refreshed.
+    """
+    if reuse is None or reuse_key is None:
+        desc, device = build_step_desc(**kwargs)
+    else:
+        hit = reuse.get(reuse_key)
+        if hit is None:
+            if len(reuse) >= 64:
+                reuse.clear()
+            desc, device = build_step_desc(**kwargs)
+            reuse[reuse_key] = (desc, device)
+        else:
+            desc, device = hit
+            if fixed_buffers:
+                snapshot, rows = kwargs.get("snapshot"), kwargs.get("rows")
+                if snapshot is not None and desc.stages & (SCORE | SELECT):
+                    desc.query, desc.lse = snapshot.query.data_ptr(), _lib.ptr(snapshot.lse)
+                    desc.key_cache = snapshot.key_cache.data_ptr()
+                    desc.block_table = snapshot.block_table.data_ptr()
+                    desc.scale = float(snapshot.scale)
+                    desc.counts = rows.counts.data_ptr()
+            else:
+                _set_pointers(desc, **{k: v for k, v in kwargs.items() if k in _POINTER_ARGS})
     launch(desc, device)
 
 
@@ -208,13 +239,8 @@ def build_step_desc(
                 or score_partials.shape[:2] != scores.shape or not score_partials.is_contiguous()):
             raise ValueError("score_partials must be a contiguous fp32 [batch_rows, max_chunks, kv_heads] buffer")
         tensors += [scores, score_partials, rows.counts, rows.query_start, rows.query_len, rows.target_len]
-        desc.score_partials = score_partials.data_ptr()
         desc.num_kv_heads = score_partials.shape[2]
-        desc.counts, desc.query_start = rows.counts.data_ptr(), rows.query_start.data_ptr()
-        desc.query_len, desc.target_len = rows.query_len.data_ptr(), rows.target_len.data_ptr()
-        desc.batch_size = rows.batch_size
         desc.max_chunks = scores.shape[1]
-        desc.scores = scores.data_ptr()
     if uses_rows:
         if snapshot is None:
             raise ValueError("scoring and selection need the verifier snapshot (heads, scale)")
@@ -238,8 +264,7 @@ def build_step_desc(
                 raise ValueError("without a softmax LSE, lse_out must be fp32 [batch_rows, query_heads] "
                                  "with unit head stride")
             tensors += [lse_partials, lse_out]
-            desc.lse_partials = lse_partials.data_ptr()
-            desc.lse_out, desc.lse_out_stride = lse_out.data_ptr(), lse_out.stride(0)
+            desc.lse_out_stride = lse_out.stride(0)
         if bt.dtype != torch.int32 or bt.ndim != 2 or bt.stride(1) != 1 or bt.shape[0] < batch_rows:
             raise ValueError("block_table must be int32 [rows, blocks] with unit last stride")
         if q.dtype != kc.dtype:
@@ -248,33 +273,30 @@ def build_step_desc(
             raise ValueError("score_partials must have one column per KV head")
         tensors += [q, lse, kc, bt]
         desc.dtype = _lib.dtype_code(q.dtype)
-        desc.query, desc.q_stride = q.data_ptr(), q.stride(0)
+        desc.q_stride = q.stride(0)
         if lse is not None:
-            desc.lse, desc.lse_token_stride, desc.lse_head_stride = lse.data_ptr(), lse.stride(0), lse.stride(1)
-        desc.key_cache = kc.data_ptr()
+            desc.lse_token_stride, desc.lse_head_stride = lse.stride(0), lse.stride(1)
         desc.k_block_stride, desc.k_token_stride, desc.k_head_stride = kc.stride(0), kc.stride(1), kc.stride(2)
         desc.block_size = kc.shape[1]
-        desc.block_table, desc.bt_stride = bt.data_ptr(), bt.stride(0)
+        desc.bt_stride = bt.stride(0)
         desc.num_q_heads, desc.num_kv_heads, desc.head_dim = q.shape[1], kc.shape[2], q.shape[2]
-        desc.scale = float(snapshot.scale)
     device = _lib.require_gpu(*tensors)
     desc.batch_rows = batch_rows
-    desc.sel_ids, desc.sel_stride, desc.sel_count = sel_ids.data_ptr(), sel_ids.stride(0), sel_count.data_ptr()
-    desc.slots = slots.data_ptr()
-    desc.committed_lens, desc.plan, desc.plan_width = committed_lens.data_ptr(), plan.data_ptr(), plan.shape[1]
-    desc.working_lens = _lib.ptr(working_lens)
+    desc.sel_stride = sel_ids.stride(0)
+    desc.plan_width = plan.shape[1]
     desc.kv_dtype = _lib.dtype_code(raw_key.dtype)
-    desc.raw_key, desc.raw_value = raw_key.data_ptr(), raw_value.data_ptr()
-    desc.working_key, desc.working_value = working_key.data_ptr(), working_value.data_ptr()
     desc.num_slots, desc.max_model_len, desc.draft_heads, desc.draft_head_dim = num_slots, max_model_len, heads, head_dim
     desc.token_budget = token_budget
-    desc.cos_sin, desc.cs_stride, desc.cs_rows = cos_sin_cache.data_ptr(), cos_sin_cache.stride(0), cos_sin_cache.shape[0]
+    desc.cs_stride, desc.cs_rows = cos_sin_cache.stride(0), cos_sin_cache.shape[0]
     desc.rotary_dim, desc.is_neox_style = rotary_dim, 1 if is_neox_style else 0
-    desc.row_active = _lib.ptr(row_active)
     desc.chunk_size, desc.history_budget = chunk_size, history_budget
     desc.recent_window = chunk_size if recent_window is None else recent_window
-    desc.workspace = _lib.ptr(workspace)
     desc.workspace_bytes = 0 if workspace is None else workspace.numel()
+    _set_pointers(desc, snapshot=snapshot, rows=rows, scores=scores, score_partials=score_partials, sel_ids=sel_ids,
+                  sel_count=sel_count, slots=slots, committed_lens=committed_lens, plan=plan,
+                  working_lens=working_lens, raw_key=raw_key, raw_value=raw_value, working_key=working_key,
+                  working_value=working_value, cos_sin_cache=cos_sin_cache, row_active=row_active,
+                  workspace=workspace, lse_partials=lse_partials, lse_out=lse_out)
     if flags & ~(SELECTORS_GATHER | EXPIRE_WAITS):
         raise ValueError(f"unknown step flags {flags:#x}")
     if _lib.DEBUG_CHECKS and stages & PLAN:
@@ -297,6 +319,39 @@ def check_distinct_slots(slots: torch.Tensor, num_slots: int, row_active: torch.
         if slot in seen:
             raise ValueError(f"rows {seen[slot]} and {r} share slot {slot}; slots must be distinct")
         seen[slot] = r
+
+
+_POINTER_ARGS = frozenset((
+    "snapshot", "rows", "scores", "score_partials", "sel_ids", "sel_count", "slots", "committed_lens", "plan",
+    "working_lens", "raw_key", "raw_value", "working_key", "working_value", "cos_sin_cache", "row_active",
+    "workspace", "lse_partials", "lse_out"))
+
+
+def _set_pointers(desc: _lib.StepDesc, *, snapshot=None, rows=None, scores=None, score_partials=None, sel_ids,
+                  sel_count, slots, committed_lens, plan, working_lens=None, raw_key, raw_value, working_key,
+                  working_value, cos_sin_cache, row_active=None, workspace=None, lse_partials=None,
+                  lse_out=None) -> None:
+    """The descriptor's buffer addresses, scale and batch size: everything a
+    validated descriptor takes from the call rather than from the shapes."""
+    p = _lib.ptr
+    if desc.stages & (SCORE | SELECT):
+        desc.scores, desc.score_partials = scores.data_ptr(), score_partials.data_ptr()
+        desc.counts, desc.query_start = rows.counts.data_ptr(), rows.query_start.data_ptr()
+        desc.query_len, desc.target_len = rows.query_len.data_ptr(), rows.target_len.data_ptr()
+        desc.batch_size = rows.batch_size
+        lse = snapshot.lse
+        desc.query, desc.lse = snapshot.query.data_ptr(), p(lse)
+        desc.key_cache, desc.block_table = snapshot.key_cache.data_ptr(), snapshot.block_table.data_ptr()
+        desc.scale = float(snapshot.scale)
+        if lse is None and desc.stages & SCORE:
+            desc.lse_partials, desc.lse_out = lse_partials.data_ptr(), lse_out.data_ptr()
+    else:
+        desc.batch_size = desc.batch_rows
+    desc.sel_ids, desc.sel_count, desc.slots = sel_ids.data_ptr(), sel_count.data_ptr(), slots.data_ptr()
+    desc.committed_lens, desc.plan, desc.working_lens = committed_lens.data_ptr(), plan.data_ptr(), p(working_lens)
+    desc.raw_key, desc.raw_value = raw_key.data_ptr(), raw_value.data_ptr()
+    desc.working_key, desc.working_value = working_key.data_ptr(), working_value.data_ptr()
+    desc.cos_sin, desc.row_active, desc.workspace = cos_sin_cache.data_ptr(), p(row_active), p(workspace)
 
 
 def workspace_bytes(batch_rows: int, max_chunks: int, num_kv_heads: int, token_budget: int) -> int:

@@ -321,8 +321,9 @@ int ds_retrieval_step_static(ds_stream_t stream, const ds_step_desc* desc, uint3
  *          pointers.
  * workspace: zero-filled once, >= ds_draft_attention_workspace_bytes(),
  *          256-byte aligned; reused across launches (one stream at a time).
- *          Word 2 of its header is the status word (bit 1: a merge stopped
- *          waiting for a partial result: that launch's output is not valid).
+ *          Word 2 of its header is the status word (bit 1: the wait of the
+ *          last workgroup for the others' "seen" words expired: that
+ *          launch's working lengths were not advanced).
  * One kernel launch, no host synchronisation, fixed launch shape for the
  * given sizes (graph-capturable).
  */
@@ -340,11 +341,12 @@ int ds_draft_attention(ds_stream_t stream, int dtype,
 /*
  * Workspace bytes of ds_draft_attention for up to batch_rows rows (0 when
  * an argument is not positive or Hq is not a multiple of Hkv).  No reference
- * counterpart.  With W = batch_rows x Hkv x ceil(G / 16) x
- * ceil(token_budget / span) workgroups (span = 256 tokens, 128 for head_dim
- * 256): 256 header bytes (word 0 the epoch, word 2 the status), W 8-byte
- * tagged "seen" words rounded up to 256 bytes, then W x 16 x (head_dim + 2)
- * 8-byte tagged partial results.
+ * counterpart.  With U = batch_rows x Hkv x ceil(G / 16) row units (at most
+ * 65536) and W = U x ceil(token_budget / span) workgroups (span = 256
+ * tokens, 128 for head_dim 256): 256 header bytes (word 0 the epoch, word 2
+ * the status), 65536 4-byte span counters (0 between launches, at a fixed
+ * place for every shape), W 8-byte tagged "seen" words rounded up to 256
+ * bytes, then W x 16 x (head_dim + 4) fp32 partial results.
  */
 size_t ds_draft_attention_workspace_bytes(int batch_rows, int num_q_heads, int num_kv_heads, int head_dim,
                                           int token_budget);

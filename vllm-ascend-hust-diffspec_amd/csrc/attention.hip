@@ -67,10 +67,15 @@ constexpr int kGroupS = 8;      // other spans merged per round trip
 constexpr uint32_t kSpinA = 1u << 20;
 constexpr float kLog2e = 1.44269504088896340736f;
 
-// Workspace layout (bytes): a 256-byte header (epoch, status), then one
-// tagged "seen" word per workgroup of the pending rows, then the tagged
-// partials.  Past the header every word is a 64-bit (tag << 32 | value) word,
-// so a launch of another shape finds only older tags wherever it looks.
+// Workspace layout (bytes): a 256-byte header (epoch, status); a fixed
+// region of kMaxUnits 32-bit span counters, one per (row, KV head, query
+// block), 0 between launches (a shape-independent place, so a launch of
+// another shape never reads other words as counters); one tagged "seen"
+// word per workgroup of the pending rows (64-bit, tag << 32 | value, so a
+// launch of another shape finds only older tags); then the fp32 partial
+// results of every span.
+constexpr int kMaxUnits = 65536;
+constexpr size_t kCounterBytes = kMaxUnits * sizeof(uint32_t);
 enum { kHdrEpoch = 0, kHdrStatus = 2 };
 constexpr size_t kHeaderBytes = 256;
 constexpr uint32_t kStatusPosition = 1;  // a row's slot or position was out of range
@@ -82,7 +87,7 @@ struct AttnShape {
   static constexpr int kSpan = kWavesA * kTiles * kTileT;  // tokens per workgroup
   static constexpr int kSteps = D / 32;                    // score MFMAs per tile
   static constexpr int kJ = D / 16;                        // output column blocks
-  static constexpr int kRow = D + 2;                       // partial words per query
+  static constexpr int kRow = D + 4;                       // partial floats per query: D outputs, max, sum, 2 pad
 };
 
 struct AttnArgs {
@@ -103,7 +108,8 @@ struct AttnArgs {
   float scale;
   uint32_t* header;
   uint64_t* seen;
-  uint64_t* partials;
+  uint32_t* counters;  // [rows * hkv * qblocks] spans done this launch
+  float* partials;     // [rows * hkv * qblocks][splits][kGroupQ][kRow]
 };
 
 template <int DT>
@@ -162,6 +168,20 @@ __device__ __forceinline__ void load_words(const uint16_t* p, uint32_t (&w)[J / 
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// 16-byte accesses with the device-scope cache policy (sc1), through a raw
+// buffer resource over one row's partials.
+typedef __amdgpu_buffer_rsrc_t Rsrc16;
+constexpr int kPolicySc1 = 16;
+__device__ __forceinline__ Rsrc16 make_rsrc16(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ void store16_sc1(Rsrc16 r, uint32_t off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, static_cast<int>(off), 0, kPolicySc1);
+}
+__device__ __forceinline__ f32x4 load16_sc1(Rsrc16 r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, kPolicySc1));
+}
 
 __device__ __forceinline__ uint64_t tagged(uint32_t tag, float v) {
   return (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v);
@@ -229,8 +249,7 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
   __shared__ float s_m[kWavesA][kGroupQ];
   __shared__ float s_l[kWavesA][kGroupQ];
   __shared__ float s_acc[kWavesA - 1][kGroupQ][D + 4];
-  __shared__ float s_gm[kGroupS][kGroupQ];  // merge: other spans' max and sum
-  __shared__ float s_gl[kGroupS][kGroupQ];
+  __shared__ int s_last;
   __shared__ int s_pos;
   __shared__ uint32_t s_tag;
 
@@ -490,14 +509,16 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
     return;
   }
 
-  // Several spans.  Every span's result goes to LDS ([g][d] in s_acc[0], max
-  // and sum in s_m[0] / s_l[0]).  Every span but the last then publishes it
-  // as tagged words, written by all threads in address order (whole lines of
-  // device-scope writes), and is done; the last span's workgroup, which has
-  // the highest index of the row's spans, merges: it waits only for
-  // workgroups dispatched before it.
+  // Several spans.  Every span writes its result ((running max, sum,
+  // unnormalised output) per query, fp32) to its slot of the row's partials
+  // with device-scope stores, waits until they are done and counts itself on
+  // the row's counter.  The workgroup that counts last merges the row: the
+  // others' stores are complete before their counts, so it reads them
+  // without waiting, and it resets the counter for the next launch.  The
+  // spans are merged in index order whichever workgroup merges, so the
+  // result does not depend on arrival order.
   const int unit = (row * a.hkv + kvh) * a.qblocks + qb;
-  uint64_t* part_base = a.partials + static_cast<int64_t>(unit) * a.splits * kGroupQ * S::kRow;
+  float* part_base = a.partials + static_cast<int64_t>(unit) * a.splits * kGroupQ * S::kRow;
   lds_barrier();  // every wave is done reading s_acc
   if (wave == 0) {
 #pragma unroll
@@ -511,121 +532,91 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
     }
   }
   lds_barrier();
-  if (split < active - 1) {
-    uint64_t* pr = part_base + static_cast<int64_t>(split) * kGroupQ * S::kRow;
-    for (int w = threadIdx.x; w < gcount * S::kRow; w += kThreadsA) {
-      const int g = w / S::kRow, d = w % S::kRow;
-      const float v = d < D ? s_acc[0][g][d] : (d == D ? s_m[0][g] : s_l[0][g]);
-      coherent_store(pr + w, tagged(tag, v));
+  // The row's partials as a buffer resource: 16-byte device-scope (sc1)
+  // accesses, written through to memory and read past the per-XCD caches.
+  const Rsrc16 prs = make_rsrc16(part_base, static_cast<int64_t>(a.splits) * kGroupQ * S::kRow * 4);
+  {
+    // Row g of a span's partial: D outputs, then (max, sum, 0, 0).
+    constexpr int kVec = S::kRow / 4;
+    const uint32_t span_off = static_cast<uint32_t>(split * kGroupQ * S::kRow * 4);
+    for (int w = threadIdx.x; w < gcount * kVec; w += kThreadsA) {
+      const int g = w / kVec, c = w % kVec;
+      f32x4 v;
+      if (c < D / 4) {
+        v = f32x4{s_acc[0][g][4 * c], s_acc[0][g][4 * c + 1], s_acc[0][g][4 * c + 2], s_acc[0][g][4 * c + 3]};
+      } else {
+        v = f32x4{s_m[0][g], s_l[0][g], 0.f, 0.f};
+      }
+      store16_sc1(prs, span_off + static_cast<uint32_t>((g * S::kRow + 4 * c) * 4), v);
     }
+  }
+  // The stores are device-scope write-throughs: once this thread's are
+  // acknowledged they are visible to every workgroup.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t prev =
+        __hip_atomic_fetch_add(a.counters + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == static_cast<uint32_t>(active - 1) ? 1 : 0;
+    if (s_last) coherent_store(a.counters + unit, 0u);
+  }
+  lds_barrier();
+  if (!s_last) {
     finish();
     return;
   }
 
-  // Merge: thread -> (query g, 4 consecutive outputs), spans in index order.
-  // Per group of up to kGroupS other spans, one thread per (span, query)
-  // fetches that span's max and sum into LDS while every thread fetches its
-  // own output words, all in one round trip.
+  // Merge: thread -> (query g, 4 consecutive outputs), spans in index order,
+  // every other span's words requested at once (kGroupS spans per round).
   constexpr int kChunks = D / 4;
-  bool expired = false;
-  const int others = active - 1;
   const int items = gcount * kChunks;
-  for (int base = 0; base < items; base += kThreadsA) {
-    const int item = base + static_cast<int>(threadIdx.x);
-    const bool has_item = item < items;
-    const int g = has_item ? item / kChunks : 0;
-    const int e = has_item ? 4 * (item % kChunks) : 0;
+  for (int item = threadIdx.x; item < items; item += kThreadsA) {
+    const int g = item / kChunks;
+    const int e = 4 * (item % kChunks);
     float run_m = -INFINITY, run_l = 0.f;
-    float run[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < others; s0 += kGroupS) {
-      const int cnt = min(kGroupS, others - s0);
-      const int ml = static_cast<int>(threadIdx.x);
-      const bool has_ml = ml < cnt * gcount;
-      const uint64_t* pml = part_base + (static_cast<int64_t>(s0 + ml / gcount) * kGroupQ + ml % gcount) * S::kRow;
-      const uint64_t* pi = part_base + (static_cast<int64_t>(s0) * kGroupQ + g) * S::kRow + e;
-      // Until every word of the group carries this launch's tag, all of them
-      // are requested again at once (one round trip per round).
-      uint64_t wm = 0, wl = 0;
-      uint64_t wv[kGroupS][4];
-      for (uint32_t spins = 0;; ++spins) {
-        if (spins > 0) __builtin_amdgcn_s_sleep(2);
-        if (has_ml) {
-          wm = coherent_load(pml + D);
-          wl = coherent_load(pml + D + 1);
-        }
-        if (has_item) {
+    f32x4 run = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < active; s0 += kGroupS) {
+      const int cnt = min(kGroupS, active - s0);
+      f32x4 pv[kGroupS], pml[kGroupS];
 #pragma unroll
-          for (int u = 0; u < kGroupS; ++u) {
-#pragma unroll
-            for (int v = 0; v < 4; ++v) wv[u][v] = u < cnt ? coherent_load(pi + u * kGroupQ * S::kRow + v) : tagged(tag, 0.f);
-          }
-        }
-        uint32_t bad = 0u;
-        if (has_ml) bad = (static_cast<uint32_t>(wm >> 32) ^ tag) | (static_cast<uint32_t>(wl >> 32) ^ tag);
-        if (has_item) {
-#pragma unroll
-          for (int u = 0; u < kGroupS; ++u) {
-#pragma unroll
-            for (int v = 0; v < 4; ++v) bad |= static_cast<uint32_t>(wv[u][v] >> 32) ^ tag;
-          }
-        }
-        if (bad == 0u) break;
-        if (expired || spins >= kSpinA) {
-          if (!expired) raise_status(a, kStatusPartials);
-          expired = true;
-          break;
+      for (int u = 0; u < kGroupS; ++u) {
+        const int sp = s0 + u;
+        if (u < cnt && sp != split) {
+          const uint32_t row_off = static_cast<uint32_t>((sp * kGroupQ + g) * S::kRow * 4);
+          pv[u] = load16_sc1(prs, row_off + e * 4);
+          pml[u] = load16_sc1(prs, row_off + D * 4);
         }
       }
-      auto stale = [&](uint64_t w) { return static_cast<uint32_t>(w >> 32) != tag; };
-      auto value = [&](uint64_t w) {
-        return expired && stale(w) ? __uint_as_float(0x7fc00000u) : __uint_as_float(static_cast<uint32_t>(w));
-      };
-      if (has_ml) {
-        s_gm[ml / gcount][ml % gcount] = value(wm);
-        s_gl[ml / gcount][ml % gcount] = value(wl);
-      }
-      lds_barrier();
-      if (has_item) {
-        float gm = run_m;
 #pragma unroll
-        for (int u = 0; u < kGroupS; ++u) {
-          if (u < cnt) gm = fmaxf(gm, s_gm[u][g]);
+      for (int u = 0; u < kGroupS; ++u) {
+        const int sp = s0 + u;
+        if (u >= cnt) break;
+        float m_s, l_s;
+        f32x4 a_s;
+        if (sp == split) {
+          m_s = s_m[0][g];
+          l_s = s_l[0][g];
+          a_s = f32x4{s_acc[0][g][e], s_acc[0][g][e + 1], s_acc[0][g][e + 2], s_acc[0][g][e + 3]};
+        } else {
+          m_s = pml[u][0];
+          l_s = pml[u][1];
+          a_s = pv[u];
         }
-        const float rescale = fast_exp2(run_m - gm);
-        run_l *= rescale;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) run[v] *= rescale;
-#pragma unroll
-        for (int u = 0; u < kGroupS; ++u) {
-          if (u < cnt) {
-            const float w = fast_exp2(s_gm[u][g] - gm);
-            run_l += s_gl[u][g] * w;
-#pragma unroll
-            for (int v = 0; v < 4; ++v) run[v] += value(wv[u][v]) * w;
-          }
-        }
+        const float gm = fmaxf(run_m, m_s);
+        const float r1 = fast_exp2(run_m - gm);
+        const float r2 = fast_exp2(m_s - gm);
+        run_l = run_l * r1 + l_s * r2;
+        run = run * r1 + a_s * r2;
         run_m = gm;
       }
-      lds_barrier();  // s_gm / s_gl are refilled by the next group
     }
-    if (has_item) {
-      {  // the merging workgroup's own span, last in index order
-        const float om = s_m[0][g];
-        const float gm = fmaxf(run_m, om);
-        const float rescale = fast_exp2(run_m - gm);
-        const float w = fast_exp2(om - gm);
-        run_l = run_l * rescale + s_l[0][g] * w;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) run[v] = run[v] * rescale + s_acc[0][g][e + v] * w;
-      }
-      const float inv = 1.f / run_l;
-      uint16_t* o = static_cast<uint16_t*>(a.out) + row * a.o_row + (head0 + g) * a.o_head + e;
-      const uint32_t w0 = static_cast<uint32_t>(Elem<DT>::store(run[0] * inv)) |
-                          (static_cast<uint32_t>(Elem<DT>::store(run[1] * inv)) << 16);
-      const uint32_t w1 = static_cast<uint32_t>(Elem<DT>::store(run[2] * inv)) |
-                          (static_cast<uint32_t>(Elem<DT>::store(run[3] * inv)) << 16);
-      *reinterpret_cast<u32x2*>(o) = u32x2{w0, w1};
-    }
+    const float inv = 1.f / run_l;
+    uint16_t* o = static_cast<uint16_t*>(a.out) + row * a.o_row + (head0 + g) * a.o_head + e;
+    const uint32_t w0 = static_cast<uint32_t>(Elem<DT>::store(run[0] * inv)) |
+                        (static_cast<uint32_t>(Elem<DT>::store(run[1] * inv)) << 16);
+    const uint32_t w1 = static_cast<uint32_t>(Elem<DT>::store(run[2] * inv)) |
+                        (static_cast<uint32_t>(Elem<DT>::store(run[3] * inv)) << 16);
+    *reinterpret_cast<u32x2*>(o) = u32x2{w0, w1};
   }
   finish();
 }
@@ -639,15 +630,17 @@ int launch_attention(hipStream_t stream, const AttnArgs& a) {
 
 int span_for(int head_dim) { return head_dim <= 128 ? kWavesA * 4 * kTileT : kWavesA * 2 * kTileT; }
 
+size_t seen_bytes(size_t wgs) { return (wgs * sizeof(uint64_t) + 255) / 256 * 256; }
+
 size_t attention_workspace_bytes(int rows, int num_q_heads, int num_kv_heads, int head_dim, int token_budget) {
   if (rows <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || token_budget <= 0) return 0;
   if (num_q_heads % num_kv_heads) return 0;
   const int group = num_q_heads / num_kv_heads;
   const int qblocks = (group + kGroupQ - 1) / kGroupQ;
   const int splits = (token_budget + span_for(head_dim) - 1) / span_for(head_dim);
-  const size_t units = static_cast<size_t>(rows) * num_kv_heads * qblocks * splits;
-  const size_t seen = (units * sizeof(uint64_t) + 255) / 256 * 256;
-  return kHeaderBytes + seen + units * kGroupQ * (head_dim + 2) * sizeof(uint64_t);
+  const size_t units = static_cast<size_t>(rows) * num_kv_heads * qblocks;
+  const size_t wgs = units * splits;
+  return kHeaderBytes + kCounterBytes + seen_bytes(wgs) + wgs * kGroupQ * (head_dim + 4) * sizeof(float);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -669,6 +662,8 @@ int draft_attention_impl(hipStream_t stream, int dtype, const void* query, int64
   DS_SUPPORTED(out_rows <= kMaxRows, "at most %d output rows per launch (got %d)", kMaxRows, out_rows);
   const int group = num_q_heads / num_kv_heads;
   const int qblocks = (group + kGroupQ - 1) / kGroupQ;
+  DS_SUPPORTED(static_cast<int64_t>(out_rows) * num_kv_heads * qblocks <= kMaxUnits,
+               "at most %d (row, KV head, 16-query block) units per launch", kMaxUnits);
   if (out_rows == 0) return clear_error();
   DS_REQUIRE(query && out && (rows == 0 || (key && value && working_key && working_value && working_lens && slots)),
              "null tensor pointer");
@@ -700,10 +695,10 @@ int draft_attention_impl(hipStream_t stream, int dtype, const void* query, int64
   a.scale = scale;
   char* ws = static_cast<char*>(workspace);
   a.header = reinterpret_cast<uint32_t*>(ws);
-  const size_t seen_bytes = (static_cast<size_t>(rows) * num_kv_heads * qblocks * a.splits * sizeof(uint64_t) + 255) /
-                            256 * 256;
-  a.seen = reinterpret_cast<uint64_t*>(ws + kHeaderBytes);
-  a.partials = reinterpret_cast<uint64_t*>(ws + kHeaderBytes + seen_bytes);
+  const size_t units = static_cast<size_t>(rows) * num_kv_heads * qblocks;
+  a.counters = reinterpret_cast<uint32_t*>(ws + kHeaderBytes);
+  a.seen = reinterpret_cast<uint64_t*>(ws + kHeaderBytes + kCounterBytes);
+  a.partials = reinterpret_cast<float*>(ws + kHeaderBytes + kCounterBytes + seen_bytes(units * a.splits));
 
 #define DS_ATTN_CASE(DTV, DV) \
   if (dtype == DTV && head_dim == DV) return launch_attention<DTV, DV>(stream, a);

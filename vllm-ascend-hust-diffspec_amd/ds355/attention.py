@@ -47,7 +47,8 @@ def new_attention_workspace(batch_rows: int, num_q_heads: int, num_kv_heads: int
 
 def attention_status(workspace: torch.Tensor) -> int:
     """Status word (reads the device): bit 0 a row's slot or position was out
-    of range, bit 1 a merge stopped waiting (that launch's output is invalid)."""
+    of range, bit 1 the last workgroup's wait for the others' "seen" words
+    expired (that launch did not advance the working lengths)."""
     return int(workspace[8:12].view(torch.int32).item())
 
 

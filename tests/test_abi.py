@@ -249,15 +249,16 @@ def test_step_workspace_size():
 
 
 def test_attention_workspace_size():
-    """256 header bytes, one 8-byte seen word per workgroup of the pending rows
-    (rows x Hkv x ceil(G / 16) x spans, rounded up to 256 bytes), then tagged
-    partials: 16 x (D + 2) x 8 bytes per workgroup."""
+    """256 header bytes, 65536 4-byte span counters, one 8-byte seen word per
+    workgroup of the pending rows (rows x Hkv x ceil(G / 16) x spans, rounded
+    up to 256 bytes), then fp32 partials: 16 x (D + 4) x 4 bytes per
+    workgroup."""
     from ds355 import _lib
 
     lib = _lib.load()
 
     def expected(units, d):
-        return 256 + (units * 8 + 255) // 256 * 256 + units * 16 * (d + 2) * 8
+        return 256 + 65536 * 4 + (units * 8 + 255) // 256 * 256 + units * 16 * (d + 4) * 4
 
     assert lib.ds_draft_attention_workspace_bytes(16, 32, 4, 128, 2048) == expected(16 * 4 * 1 * 8, 128)
     # G = 32 -> two query blocks; head_dim 256 -> 128-token spans

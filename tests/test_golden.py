@@ -90,7 +90,12 @@ def test_oracle_regenerates_chain_fixture():
     z, _, _, _ = _chain()
     arrays = mod._draw_chain(int(z["seed"][0]))["arrays"]
     for name, value in arrays.items():
-        assert np.array_equal(value, z[name]), name
+        if value.dtype.kind == "f" and name in ("lse", "scores"):
+            # Floating-point reductions (logsumexp, softmax sums) may round
+            # differently on another host's vector units: within 4 ulps of fp32.
+            np.testing.assert_allclose(value, z[name], rtol=5e-7, atol=0, err_msg=name)
+        else:
+            assert np.array_equal(value, z[name]), name
 
 
 # -- GPU ------------------------------------------------------------------------------------------

@@ -173,3 +173,39 @@ def test_device_plans_with_recent_window_and_padding(cuda):
                 recent_window=window)
             assert decoded == indices.tolist()
         assert plan[20].abs().sum() == 0 and plan[21].abs().sum() == 0
+
+
+@pytest.mark.parametrize("chunk,budget", [(32, 2016), (64, 1984), (16, 512), (8, 1024)])
+def test_long_rows_shortlist_selection(cuda, chunk, budget):
+    """Long rows (513 to 4096 chunks) with few picks, as long contexts with
+    small chunks give: random scores, scores on a coarse grid so the cut
+    falls inside a run of ties, NaN and infinities among the top, a dozen
+    levels only, softmax-like means of one magnitude, and a few outliers over
+    a tiny floor.  Bit-exact against the oracle."""
+    g = gen(chunk + budget)
+    rows, lengths = [], []
+    for trial in range(48):
+        kind = trial % 6
+        c = int(torch.randint(513, 4097, (1,), generator=g))
+        length = c * chunk - int(torch.randint(0, chunk, (1,), generator=g))
+        if kind == 0:
+            s = torch.rand(c, generator=g) * 1e-4
+        elif kind == 1:  # ties at the cut: 300 levels
+            s = torch.randint(0, 300, (c,), generator=g).float() * 1e-6
+        elif kind == 2:  # NaN and +-inf among the largest
+            s = torch.randn(c, generator=g)
+            idx = torch.randint(0, c - 1, (6,), generator=g)
+            s[idx[0]], s[idx[1]], s[idx[2]] = float("nan"), float("inf"), float("nan")
+            s[idx[3]], s[idx[4]], s[idx[5]] = float("-inf"), -0.0, 0.0
+        elif kind == 3:  # 12 levels: the shortlist overflows, radix select
+            s = torch.randint(0, 12, (c,), generator=g).float()
+        elif kind == 4:  # one magnitude, as softmax chunk means are
+            s = (1.0 + 0.3 * torch.randn(c, generator=g)).abs() * 2.4e-5
+        else:  # a few large outliers, the rest tiny
+            s = torch.rand(c, generator=g) * 1e-7
+            s[torch.randint(0, c - 1, (budget // chunk // 2,), generator=g)] = 1.0
+        rows.append(s)
+        lengths.append(length)
+    actual = _select_rows(rows, lengths, chunk, budget, cuda)
+    for r, (s, n) in enumerate(zip(rows, lengths)):
+        assert actual[r] == O.select_context_chunks(s, n, chunk, budget).chunk_indices.tolist(), r

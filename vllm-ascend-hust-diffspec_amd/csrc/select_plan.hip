@@ -22,6 +22,7 @@ using namespace select;
 
 constexpr int kLdsKeys = 12288;  // candidates kept in LDS; larger rows read keys from global memory
 constexpr int kPre = 4;          // chunks per thread whose partials are loaded at kernel start
+constexpr int kMore = 12;        // chunks per thread per later round (longer rows: 4096 chunks in two rounds)
 
 template <int HKV>
 __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
@@ -71,17 +72,17 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
         const int i = u * kThreads + tid;
         if (i < C) finish(i, pre[u]);
       }
-      // Longer rows: kPre chunks per thread at a time, their loads issued
+      // Longer rows: kMore chunks per thread at a time, their loads issued
       // together (clamped to the buffer, masked when finished).
-      for (int i0 = kPre * kThreads; i0 < C; i0 += kPre * kThreads) {
-        float v[kPre];
+      for (int i0 = kPre * kThreads; i0 < C; i0 += kMore * kThreads) {
+        float v[kMore];
 #pragma unroll
-        for (int u = 0; u < kPre; ++u) {
+        for (int u = 0; u < kMore; ++u) {
           const int i = min(i0 + u * kThreads + tid, a.max_chunks - 1);
           v[u] = head_sum<HKV>(part + static_cast<int64_t>(i) * a.hkv, a.hkv);
         }
 #pragma unroll
-        for (int u = 0; u < kPre; ++u) {
+        for (int u = 0; u < kMore; ++u) {
           const int i = i0 + u * kThreads + tid;
           if (i < C) finish(i, v[u]);
         }

@@ -210,6 +210,8 @@ __device__ __forceinline__ void select_row(const FusedArgs& f, int b, uint32_t t
   const bool slot_ok = slot >= 0 && slot < a.num_slots;
   const int committed = a.committed_lens[b];
   const int stored_count = slot_ok ? a.counts[slot] : 0;
+  // The previous row's plan columns are read from sh.ids up to its end.
+  lds_barrier();
   if (f.expire && tid == 0) raise_status(f.header, kStatusPartials);
   int n_sel = -1;
   if (d.active && slot_ok) {

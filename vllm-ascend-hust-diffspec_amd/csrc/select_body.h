@@ -38,7 +38,8 @@ struct SelectArgs {
 template <int KEYS>
 struct SelectShared {
   alignas(16) uint32_t keys[KEYS + 4];  // + 4: a 4-key read at the end stays inside
-  int hist[256];
+  int hist[4][256];  // one histogram per radix pass
+  int res[4][3];     // per pass: the digit holding the cut, keys above it, keys in it
   int ids[kMaxSel];
   int scratch[4];
   int wcount[2 * kThreads / 64];  // per-wave counts of the compaction
@@ -131,31 +132,46 @@ __device__ __forceinline__ void select_top(SelectShared<KEYS>& sh, int N, int K,
   uint32_t prefix = 0u, pmask = 0u;
   bool take_all_ties = true;
   if (need > 0) {
-    for (int shift = 24; shift >= 0; shift -= 8) {
-      sh.hist[tid] = 0;
-      lds_barrier();
+    // The four passes' histograms are cleared together; a pass then takes
+    // two barriers: one after its histogram, one after wave 0 has found the
+    // digit (lane l scans digits 255 - 4l .. 252 - 4l, the wave's inclusive
+    // scan gives each lane the count of keys in higher digits).
+    for (int i = tid; i < 4 * 256; i += kThreads) sh.hist[i >> 8][i & 255] = 0;
+    lds_barrier();
+    for (int pass = 0; pass < 4; ++pass) {
+      const int shift = 24 - 8 * pass;
+      int* hist = sh.hist[pass];
       for (int q = tid; 4 * q < N; q += kThreads) {
         const U4 k4 = key4_at(q);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          if (4 * q + j < N && (k4[j] & pmask) == prefix) atomicAdd(&sh.hist[(k4[j] >> shift) & 0xffu], 1);
+          if (4 * q + j < N && (k4[j] & pmask) == prefix) atomicAdd(&hist[(k4[j] >> shift) & 0xffu], 1);
         }
       }
       lds_barrier();
-      const int digit = 255 - tid;  // thread t scans bins in descending digit order
-      const int cnt = sh.hist[digit];
-      const int incl = block_inclusive_scan(cnt, sh.scratch);
-      if (incl - cnt < need && need <= incl) {
-        sh.digit = digit;
-        sh.above = incl - cnt;
-        sh.eq = cnt;
+      if (tid < 64) {
+        int c[4], sum = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          c[e] = hist[255 - 4 * tid - e];
+          sum += c[e];
+        }
+        int before = wave_inclusive_scan(sum) - sum;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (before < need && need <= before + c[e]) {
+            sh.res[pass][0] = 255 - 4 * tid - e;
+            sh.res[pass][1] = before;
+            sh.res[pass][2] = c[e];
+          }
+          before += c[e];
+        }
       }
       lds_barrier();
-      prefix |= static_cast<uint32_t>(sh.digit) << shift;
+      prefix |= static_cast<uint32_t>(sh.res[pass][0]) << shift;
       pmask |= 0xffu << shift;
-      need -= sh.above;
-      take_all_ties = need == sh.eq;  // the last pass decides; an earlier one may end the search
-      lds_barrier();
+      need -= sh.res[pass][1];
+      take_all_ties = need == sh.res[pass][2];  // the last pass decides; an earlier one may end the search
       if (take_all_ties) break;  // workgroup-uniform: every thread read the same counts
     }
   }
@@ -235,8 +251,7 @@ __device__ __forceinline__ void select_top(SelectShared<KEYS>& sh, int N, int K,
 // (n_sel >= 0, ids in sh.ids) or the slot's stored one (n_sel < 0,
 // stored_count entries).  Writes plan[b] and working_lens[slot]; with a
 // tagged copy, also stores column j as (tag << 32) | value in tagged[j]
-// with a device-scope store (plan values are below 2^31).  Contains
-// barriers (block sum) when the selection is non-empty.
+// with a device-scope store (plan values are below 2^31).  No barriers.
 template <int KEYS>
 __device__ __forceinline__ void write_plan_row(const SelectArgs& a, int b, int slot, int committed, int n_sel,
                                                int stored_count, SelectShared<KEYS>& sh,
@@ -262,13 +277,14 @@ __device__ __forceinline__ void write_plan_row(const SelectArgs& a, int b, int s
     if (count > 0) {
       ncols = min(count, a.plan_width - 5);
       const int64_t prefix_end = min(tail_start, chunk_id(count - 1) * a.chunk);
-      int64_t part = 0;
-      for (int j = tid; j < count; j += kThreads) {
+      // Every wave sums all terms itself (no barrier): int, each term <=
+      // chunk, the total <= count * chunk.
+      int part = 0;
+      for (int j = tid & 63; j < count; j += 64) {
         const int64_t t = prefix_end - chunk_id(j) * a.chunk;
-        part += t <= 0 ? 0 : (t < a.chunk ? t : a.chunk);
+        part += static_cast<int>(t <= 0 ? 0 : (t < a.chunk ? t : a.chunk));
       }
-      // Block sum in int (each term <= chunk; the total <= count * chunk).
-      const int64_t prefix_tokens = block_sum(static_cast<int>(part), sh.scratch);
+      const int64_t prefix_tokens = wave_sum_int(part);
       prefix_len = min(prefix_tokens, hb - tail_len);
       drop = prefix_tokens - prefix_len;
       len = prefix_len + tail_len;

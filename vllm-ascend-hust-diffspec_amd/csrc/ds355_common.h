@@ -145,15 +145,46 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Inclusive scan within the wave (lane order).
+// Inclusive scan within the wave (lane order), with DPP lane moves only:
+// row shifts by 1, 2, 4, 8 scan each 16-lane row (lanes without a source
+// add 0), then row broadcasts of lanes 15 and 31 carry the row totals into
+// rows 1, 3 and 2, 3.  The whole wave must be active.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_add_int(int v) {
+  return v + __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, false);
+}
 __device__ __forceinline__ int wave_inclusive_scan(int v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    int n = __shfl_up(v, off, 64);
-    if (lane >= off) v += n;
-  }
+  v = dpp_add_int<0x111, 0xf>(v);  // row_shr:1
+  v = dpp_add_int<0x112, 0xf>(v);  // row_shr:2
+  v = dpp_add_int<0x114, 0xf>(v);  // row_shr:4
+  v = dpp_add_int<0x118, 0xf>(v);  // row_shr:8
+  v = dpp_add_int<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v = dpp_add_int<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
   return v;
+}
+// Largest / smallest unsigned value over the wave, in every lane: the same
+// DPP steps as the scan with max / min in place of add (a lane without a
+// source combines with the identity).
+template <int CTRL, int ROW_MASK, bool MAX>
+__device__ __forceinline__ uint32_t dpp_pick(uint32_t v) {
+  const uint32_t other = static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(static_cast<int>(MAX ? 0u : ~0u), static_cast<int>(v), CTRL, ROW_MASK, 0xf, false));
+  return MAX ? max(v, other) : min(v, other);
+}
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_pick(uint32_t v) {
+  v = dpp_pick<0x111, 0xf, MAX>(v);
+  v = dpp_pick<0x112, 0xf, MAX>(v);
+  v = dpp_pick<0x114, 0xf, MAX>(v);
+  v = dpp_pick<0x118, 0xf, MAX>(v);
+  v = dpp_pick<0x142, 0xa, MAX>(v);
+  v = dpp_pick<0x143, 0xc, MAX>(v);
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
+// Sum over the wave, in every lane (the scan's lane 63).
+__device__ __forceinline__ int wave_total(int v) {
+  return __builtin_amdgcn_readlane(wave_inclusive_scan(v), 63);
 }
 
 // Exclusive scan over a 256-thread block; `total` receives the block sum.

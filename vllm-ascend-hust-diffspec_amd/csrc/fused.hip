@@ -227,6 +227,7 @@ __device__ __forceinline__ void select_row(const FusedArgs& f, int b, uint32_t t
     const uint64_t* part = f.s.tagged + static_cast<int64_t>(b) * a.max_chunks * a.hkv;
     if (C > 0) wait_sentinel(part + static_cast<int64_t>(C) * a.hkv - 1, tag, f.header);
     const int per_poll = kPollLoads / a.hkv;  // chunks per thread and poll
+    uint32_t kmin = ~0u, kmax = 0u;           // bounds of this thread's candidate keys
     for (int base = 0; base < C; base += per_poll * kThreads) {
       float sum[kPollLoads];
       poll_chunk_sums(part, base, C, a.hkv, tag, f.header, sum);
@@ -236,7 +237,12 @@ __device__ __forceinline__ void select_row(const FusedArgs& f, int b, uint32_t t
         if (u < per_poll && i < C) {
           const float v = chunk_score(sum[u], a.chunk, d.len, i, a.hq);
           row_scores[i] = v;
-          if (in_lds && i < N) sh.keys[i] = order_key(v);
+          if (i < N) {
+            const uint32_t key = order_key(v);
+            kmin = min(kmin, key);
+            kmax = max(kmax, key);
+            if (in_lds) sh.keys[i] = key;
+          }
         }
       }
     }
@@ -252,7 +258,7 @@ __device__ __forceinline__ void select_row(const FusedArgs& f, int b, uint32_t t
 #pragma unroll
         for (int j = 0; j < 4; ++j) k4[j] = order_key(row_scores[min(4 * q + j, N - 1)]);
         return k4;
-      });
+      }, kmin, kmax);
       n_sel = K;
     }
     lds_barrier();

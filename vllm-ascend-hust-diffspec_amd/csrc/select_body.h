@@ -34,15 +34,17 @@ struct SelectArgs {
   int num_slots;
 };
 
-// LDS of one selecting workgroup.  KEYS = candidates whose keys stay in LDS.
-template <int KEYS>
+// LDS of one selecting workgroup of NT threads.  KEYS = candidates whose
+// keys stay in LDS.
+template <int KEYS, int NT = kThreads>
 struct SelectShared {
   alignas(16) uint32_t keys[KEYS + 4];  // + 4: a 4-key read at the end stays inside
   int hist[4][256];  // one histogram per radix pass
   int res[4][3];     // per pass: the digit holding the cut, keys above it, keys in it
+  uint32_t range[2][NT / 64];  // per wave: smallest and largest candidate key
   int ids[kMaxSel];
   int scratch[4];
-  int wcount[2 * kThreads / 64];  // per-wave counts of the compaction
+  int wcount[2 * NT / 64];  // per-wave counts of the compaction
   int digit, above, eq;
 };
 
@@ -51,36 +53,6 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;  // NaN: largest
   if ((u & 0x7fffffffu) == 0u) u = 0u;                      // -0 == +0
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-// Exclusive scan over the 256 threads through LDS; `total` gets the sum.
-__device__ __forceinline__ int lds_exclusive_scan(int v, int* scratch, int& total) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int inc = wave_inclusive_scan(v);
-  if (lane == 63) scratch[wave] = inc;
-  lds_barrier();
-  int base = 0;
-  total = 0;
-#pragma unroll
-  for (int w = 0; w < kThreads / 64; ++w) {
-    const int t = scratch[w];
-    if (w < wave) base += t;
-    total += t;
-  }
-  lds_barrier();
-  return base + inc - v;
-}
-
-__device__ __forceinline__ int block_inclusive_scan(int v, int* scratch) {
-  int total;
-  return lds_exclusive_scan(v, scratch, total) + v;
-}
-
-__device__ __forceinline__ int block_sum(int v, int* scratch) {
-  int total;
-  lds_exclusive_scan(v, scratch, total);
-  return total;
 }
 
 // Sum of one chunk's per-KV-head partials in head order (HKV == 0: runtime
@@ -111,41 +83,67 @@ typedef uint32_t U4 __attribute__((ext_vector_type(4)));
 
 // Top K - 1 of the N candidates (chunks 0..N-1) plus the newest chunk N,
 // ascending, into sh.ids[0..K).  key4_at(q) returns the keys of candidates
-// 4q .. 4q + 3 (values past N are ignored).  Starts and ends on a
-// barrier-separated LDS state; requires N + 1 > K.
-//   - Up to four 8-bit MSB radix passes (LDS histogram, block scan over the
-//     bins) find T, the (K-1)-th largest key.  A thread reads 4 keys at a
-//     time.  A pass whose bin holding the (K-1)-th key is taken whole ends
-//     the search: T is then that bin's prefix with the low bits zero, every
-//     key of the bin is > T or == T, and all ties are taken, so the
-//     selected set is the one the remaining passes would have found.
+// 4q .. 4q + 3 (values past N are ignored).  kmin / kmax: bounds of the
+// candidate keys this thread has seen (any bounds are correct; the full
+// range 0 .. ~0 when unknown).  Starts and ends on a barrier-separated LDS
+// state; requires N + 1 > K.
+//   - The block's smallest and largest key fix the leading bits every
+//     candidate shares; MSB radix passes of up to 8 bits (LDS histogram,
+//     wave 0 scans the bins) then start below them, so the first pass
+//     spreads keys of a narrow range over many bins instead of piling
+//     them into one or two (LDS atomics on one bin serialise).  They find
+//     T, the (K-1)-th largest key.  A thread reads 4 keys at a time.  A
+//     pass whose bin holding the (K-1)-th key is taken whole ends the
+//     search: T is then that bin's prefix with the low bits zero, every key
+//     of the bin is > T or == T, and all ties are taken, so the selected
+//     set is the one the remaining passes would have found.
 //   - Compaction: wave w owns the contiguous candidates
 //     [w * span, (w + 1) * span), 256 at a time, lane l holding candidates
 //     4l .. 4l + 3 of each 256.  A first sweep counts keys > T and ties
 //     (== T) with ballots; one barrier shares the four waves' counts, which
 //     fixes each wave's first output slot and how many ties it takes (ties
 //     go to the lowest indices); a second sweep writes the ids in order.
-template <int KEYS, typename Key4At>
-__device__ __forceinline__ void select_top(SelectShared<KEYS>& sh, int N, int K, Key4At key4_at) {
+template <int KEYS, int NT, typename Key4At>
+__device__ __forceinline__ void select_top(SelectShared<KEYS, NT>& sh, int N, int K, Key4At key4_at,
+                                           uint32_t kmin = 0u, uint32_t kmax = ~0u) {
   const int tid = threadIdx.x;
   int need = K - 1;
   uint32_t prefix = 0u, pmask = 0u;
   bool take_all_ties = true;
   if (need > 0) {
-    // The four passes' histograms are cleared together; a pass then takes
-    // two barriers: one after its histogram, one after wave 0 has found the
-    // digit (lane l scans digits 255 - 4l .. 252 - 4l, the wave's inclusive
-    // scan gives each lane the count of keys in higher digits).
-    for (int i = tid; i < 4 * 256; i += kThreads) sh.hist[i >> 8][i & 255] = 0;
+    // The bounds and the four passes' histograms share one barrier; a pass
+    // then takes two: one after its histogram, one after wave 0 has found
+    // the digit (lane l scans digits 255 - 4l .. 252 - 4l, the wave's
+    // inclusive scan gives each lane the count of keys in higher digits).
+    kmin = wave_pick<false>(kmin);
+    kmax = wave_pick<true>(kmax);
+    if ((tid & 63) == 0) {
+      sh.range[0][tid >> 6] = kmin;
+      sh.range[1][tid >> 6] = kmax;
+    }
+    for (int i = tid; i < 4 * 256; i += NT) sh.hist[i >> 8][i & 255] = 0;
     lds_barrier();
-    for (int pass = 0; pass < 4; ++pass) {
-      const int shift = 24 - 8 * pass;
+#pragma unroll
+    for (int w = 0; w < NT / 64; ++w) {
+      kmin = min(kmin, sh.range[0][w]);
+      kmax = max(kmax, sh.range[1][w]);
+    }
+    // Bits above `top` are the same in every candidate.
+    int top = kmin == kmax ? 0 : 32 - __clz(static_cast<int>(kmin ^ kmax));
+    if (top < 32) {
+      pmask = ~0u << top;
+      prefix = kmax & pmask;
+    }
+    if (top == 0) take_all_ties = need == N;  // every candidate equals T = kmax
+    for (int pass = 0; top > 0; ++pass) {
+      const int shift = max(top - 8, 0);
+      const uint32_t width_mask = (1u << (top - shift)) - 1u;
       int* hist = sh.hist[pass];
-      for (int q = tid; 4 * q < N; q += kThreads) {
+      for (int q = tid; 4 * q < N; q += NT) {
         const U4 k4 = key4_at(q);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          if (4 * q + j < N && (k4[j] & pmask) == prefix) atomicAdd(&hist[(k4[j] >> shift) & 0xffu], 1);
+          if (4 * q + j < N && (k4[j] & pmask) == prefix) atomicAdd(&hist[(k4[j] >> shift) & width_mask], 1);
         }
       }
       lds_barrier();
@@ -169,32 +167,34 @@ __device__ __forceinline__ void select_top(SelectShared<KEYS>& sh, int N, int K,
       }
       lds_barrier();
       prefix |= static_cast<uint32_t>(sh.res[pass][0]) << shift;
-      pmask |= 0xffu << shift;
+      pmask |= width_mask << shift;
       need -= sh.res[pass][1];
       take_all_ties = need == sh.res[pass][2];  // the last pass decides; an earlier one may end the search
       if (take_all_ties) break;  // workgroup-uniform: every thread read the same counts
+      top = shift;
     }
   }
   // need = ties (key == T) still to take, lowest indices first.
   const uint32_t T = prefix;
   if (K - 1 > 0) {
-    constexpr int kW = kThreads / 64;
+    constexpr int kW = NT / 64;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const uint64_t below = (uint64_t{1} << lane) - 1;  // lanes before this one
     const int span = ((N + kW - 1) / kW + 255) / 256 * 256;
     const int lo = min(N, wave * span);
     const int hi = min(N, lo + span);
-    int gt = 0, eq = 0;
+    int gt = 0, eq = 0;  // this lane's keys > T and == T
     for (int b = lo; b < hi; b += 256) {
       const U4 k4 = key4_at((b >> 2) + lane);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int i = b + 4 * lane + j;
-        gt += static_cast<int>(__popcll(__ballot(i < hi && k4[j] > T)));
-        eq += static_cast<int>(__popcll(__ballot(i < hi && k4[j] == T)));
+        const bool in = b + 4 * lane + j < hi;
+        gt += (in && k4[j] > T) ? 1 : 0;
+        eq += (in && k4[j] == T) ? 1 : 0;
       }
     }
+    gt = wave_total(gt);
+    eq = wave_total(eq);
     if (lane == 0) {
       sh.wcount[wave] = gt;
       sh.wcount[kW + wave] = eq;
@@ -209,39 +209,41 @@ __device__ __forceinline__ void select_top(SelectShared<KEYS>& sh, int N, int K,
       if (w == wave) take_eq = w_take;
       eq_before += w_eq;
     }
-    int taken = 0;
+    // Second sweep, 256 candidates at a time: a wave scan of the lanes' tie
+    // counts ranks each tie (lowest index first), a scan of the lanes'
+    // selected counts gives each selected id its output slot.
+    int taken = 0;  // ties of this wave's earlier candidates
     for (int b = lo; b < hi; b += 256) {
       const U4 k4 = key4_at((b >> 2) + lane);
-      uint64_t eq_mask[4], sel_mask[4];
-      bool sel[4];
-      // Ties of this lane's earlier keys in the 256, then of lanes below.
-      int tie_rank = taken;
+      bool is_eq[4], sel[4];
+      int n_eq = 0;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int i = b + 4 * lane + j;
-        eq_mask[j] = __ballot(i < hi && k4[j] == T);
-        tie_rank += static_cast<int>(__popcll(eq_mask[j] & below));
+        const bool in = b + 4 * lane + j < hi;
+        is_eq[j] = in && k4[j] == T;
+        n_eq += is_eq[j] ? 1 : 0;
       }
+      const int eq_incl = wave_inclusive_scan(n_eq);
+      int tie_rank = taken + eq_incl - n_eq;
+      int n_sel = 0;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int i = b + 4 * lane + j;
-        const bool is_eq = i < hi && k4[j] == T;
-        sel[j] = i < hi && (k4[j] > T || (is_eq && tie_rank < take_eq));
-        if (is_eq) ++tie_rank;
-        sel_mask[j] = __ballot(sel[j]);
+        const bool in = b + 4 * lane + j < hi;
+        sel[j] = in && (k4[j] > T || (is_eq[j] && tie_rank < take_eq));
+        tie_rank += is_eq[j] ? 1 : 0;
+        n_sel += sel[j] ? 1 : 0;
       }
-      int pos = out;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) pos += static_cast<int>(__popcll(sel_mask[j] & below));
+      const int sel_incl = wave_inclusive_scan(n_sel);
+      int pos = out + sel_incl - n_sel;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         if (sel[j]) {
           if (pos < kMaxSel) sh.ids[pos] = b + 4 * lane + j;
           ++pos;
         }
-        out += static_cast<int>(__popcll(sel_mask[j]));
-        taken += static_cast<int>(__popcll(eq_mask[j]));
       }
+      out += __builtin_amdgcn_readlane(sel_incl, 63);
+      taken += __builtin_amdgcn_readlane(eq_incl, 63);
     }
   }
   if (tid == 0) sh.ids[K - 1] = N;
@@ -252,9 +254,9 @@ __device__ __forceinline__ void select_top(SelectShared<KEYS>& sh, int N, int K,
 // stored_count entries).  Writes plan[b] and working_lens[slot]; with a
 // tagged copy, also stores column j as (tag << 32) | value in tagged[j]
 // with a device-scope store (plan values are below 2^31).  No barriers.
-template <int KEYS>
+template <int KEYS, int NT>
 __device__ __forceinline__ void write_plan_row(const SelectArgs& a, int b, int slot, int committed, int n_sel,
-                                               int stored_count, SelectShared<KEYS>& sh,
+                                               int stored_count, SelectShared<KEYS, NT>& sh,
                                                uint64_t* tagged = nullptr, uint32_t tag = 0) {
   const int tid = threadIdx.x;
   int64_t* prow = a.plan + static_cast<int64_t>(b) * a.plan_width;
@@ -290,7 +292,7 @@ __device__ __forceinline__ void write_plan_row(const SelectArgs& a, int b, int s
       len = prefix_len + tail_len;
     }
   }
-  for (int j = tid; j < a.plan_width; j += kThreads) {
+  for (int j = tid; j < a.plan_width; j += NT) {
     int64_t v;
     if (j == 0) v = slot;
     else if (j == 1) v = len;

@@ -23,10 +23,12 @@ using namespace select;
 constexpr int kLdsKeys = 12288;  // candidates kept in LDS; larger rows read keys from global memory
 constexpr int kPre = 4;          // chunks per thread whose partials are loaded at kernel start
 constexpr int kMore = 12;        // chunks per thread per later round (longer rows: 4096 chunks in two rounds)
+constexpr int kLongRow = 2048;   // chunks per row from which the 1024-thread workgroup selects
+constexpr int kLongThreads = 1024;
 
-template <int HKV>
-__global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
-  __shared__ SelectShared<kLdsKeys> sh;
+template <int HKV, int NT>
+__global__ __launch_bounds__(NT) void select_plan_kernel(SelectArgs a) {
+  __shared__ SelectShared<kLdsKeys, NT> sh;
 
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
@@ -45,7 +47,7 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
   if (a.do_select && a.partials != nullptr) {
 #pragma unroll
     for (int u = 0; u < kPre; ++u) {
-      const int i = min(u * kThreads + tid, a.max_chunks - 1);
+      const int i = min(u * NT + tid, a.max_chunks - 1);
       pre[u] = head_sum<HKV>(part + static_cast<int64_t>(i) * a.hkv, a.hkv);
     }
   }
@@ -55,40 +57,53 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
     const int C = (d.len + a.chunk - 1) / a.chunk;
     const int K = a.budget / a.chunk;
     if (C <= K) {
-      for (int i = tid; i < C; i += kThreads) sh.ids[i] = i;
+      for (int i = tid; i < C; i += NT) sh.ids[i] = i;
       n_sel = C;
     }
     float* row_scores = a.scores + static_cast<int64_t>(b) * a.score_stride;
     const int N = C - 1;  // candidates (newest chunk excluded from the ranking)
     const bool in_lds = C > K && N <= kLdsKeys;
+    // Bounds of the candidate keys this thread computes (for select_top).
+    uint32_t kmin = ~0u, kmax = 0u;
+    const bool bounded = a.partials != nullptr || in_lds;
     if (a.partials != nullptr) {
       auto finish = [&](int i, float sum) {
         const float v = chunk_score(sum, a.chunk, d.len, i, a.hq);
         row_scores[i] = v;
-        if (in_lds && i < N) sh.keys[i] = order_key(v);
+        if (i < N) {
+          const uint32_t key = order_key(v);
+          kmin = min(kmin, key);
+          kmax = max(kmax, key);
+          if (in_lds) sh.keys[i] = key;
+        }
       };
 #pragma unroll
       for (int u = 0; u < kPre; ++u) {
-        const int i = u * kThreads + tid;
+        const int i = u * NT + tid;
         if (i < C) finish(i, pre[u]);
       }
       // Longer rows: kMore chunks per thread at a time, their loads issued
       // together (clamped to the buffer, masked when finished).
-      for (int i0 = kPre * kThreads; i0 < C; i0 += kMore * kThreads) {
+      for (int i0 = kPre * NT; i0 < C; i0 += kMore * NT) {
         float v[kMore];
 #pragma unroll
         for (int u = 0; u < kMore; ++u) {
-          const int i = min(i0 + u * kThreads + tid, a.max_chunks - 1);
+          const int i = min(i0 + u * NT + tid, a.max_chunks - 1);
           v[u] = head_sum<HKV>(part + static_cast<int64_t>(i) * a.hkv, a.hkv);
         }
 #pragma unroll
         for (int u = 0; u < kMore; ++u) {
-          const int i = i0 + u * kThreads + tid;
+          const int i = i0 + u * NT + tid;
           if (i < C) finish(i, v[u]);
         }
       }
     } else if (in_lds) {
-      for (int i = tid; i < N; i += kThreads) sh.keys[i] = order_key(row_scores[i]);
+      for (int i = tid; i < N; i += NT) {
+        const uint32_t key = order_key(row_scores[i]);
+        kmin = min(kmin, key);
+        kmax = max(kmax, key);
+        sh.keys[i] = key;
+      }
     }
     if (in_lds) {
       lds_barrier();
@@ -102,19 +117,19 @@ __global__ __launch_bounds__(kThreads) void select_plan_kernel(SelectArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) k4[j] = order_key(row_scores[min(4 * q + j, N - 1)]);
         return k4;
-      });
+      }, bounded ? kmin : 0u, bounded ? kmax : ~0u);
       n_sel = K;
     }
     lds_barrier();
     int32_t* out = a.ids + static_cast<int64_t>(slot) * a.ids_stride;
-    for (int j = tid; j < n_sel; j += kThreads) out[j] = sh.ids[j];
+    for (int j = tid; j < n_sel; j += NT) out[j] = sh.ids[j];
     if (tid == 0) a.counts[slot] = n_sel;
   }
 
   if (!a.do_plan) return;
   if (!slot_ok) {
     int64_t* prow = a.plan + static_cast<int64_t>(b) * a.plan_width;
-    for (int j = tid; j < a.plan_width; j += kThreads) prow[j] = 0;
+    for (int j = tid; j < a.plan_width; j += NT) prow[j] = 0;
     return;
   }
   write_plan_row(a, b, slot, committed, n_sel, stored_count, sh);
@@ -168,6 +183,20 @@ int make_select_args(SelectArgs& a, float* scores, int64_t score_stride, const f
   return clear_error();
 }
 
+namespace {
+template <int NT>
+int launch_hkv(hipStream_t stream, const SelectArgs& a, int hkv, int batch) {
+  switch (hkv) {
+    case 1: select_plan_kernel<1, NT><<<batch, NT, 0, stream>>>(a); break;
+    case 2: select_plan_kernel<2, NT><<<batch, NT, 0, stream>>>(a); break;
+    case 4: select_plan_kernel<4, NT><<<batch, NT, 0, stream>>>(a); break;
+    case 8: select_plan_kernel<8, NT><<<batch, NT, 0, stream>>>(a); break;
+    default: select_plan_kernel<0, NT><<<batch, NT, 0, stream>>>(a); break;
+  }
+  return check_launch("select/plan");
+}
+}  // namespace
+
 int launch_select_plan(hipStream_t stream, float* scores, int64_t score_stride, const float* partials,
                        int max_chunks, int hkv, int hq, const RowSource& src,
                        int batch, int chunk, int budget, int do_select, int do_plan, int32_t* ids,
@@ -179,14 +208,11 @@ int launch_select_plan(hipStream_t stream, float* scores, int64_t score_stride, 
                                   do_select, do_plan, ids, ids_stride, counts, slots, num_slots, committed_lens, plan,
                                   plan_width, working_lens, recent_window);
   if (rc != DS_OK || batch == 0) return rc;
-  switch (do_select && partials != nullptr ? hkv : 0) {
-    case 1: select_plan_kernel<1><<<batch, kThreads, 0, stream>>>(a); break;
-    case 2: select_plan_kernel<2><<<batch, kThreads, 0, stream>>>(a); break;
-    case 4: select_plan_kernel<4><<<batch, kThreads, 0, stream>>>(a); break;
-    case 8: select_plan_kernel<8><<<batch, kThreads, 0, stream>>>(a); break;
-    default: select_plan_kernel<0><<<batch, kThreads, 0, stream>>>(a); break;
-  }
-  return check_launch("select/plan");
+  // Rows of kLongRow chunks or more are selected by 1024-thread workgroups
+  // (four times the waves for the per-candidate sweeps), shorter ones by 256.
+  const int64_t row_chunks = (static_cast<int64_t>(src.max_len) + chunk - 1) / chunk;
+  if (do_select && row_chunks >= kLongRow) return launch_hkv<kLongThreads>(stream, a, partials != nullptr ? hkv : 0, batch);
+  return launch_hkv<kThreads>(stream, a, do_select && partials != nullptr ? hkv : 0, batch);
 }
 
 }  // namespace ds355

@@ -248,7 +248,7 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
   constexpr int J = S::kJ;
   __shared__ float s_m[kWavesA][kGroupQ];
   __shared__ float s_l[kWavesA][kGroupQ];
-  __shared__ float s_acc[kWavesA - 1][kGroupQ][D + 4];
+  __shared__ float s_acc[kWavesA][kGroupQ][D + 4];
   __shared__ int s_last;
   __shared__ int s_pos;
   __shared__ uint32_t s_tag;
@@ -275,16 +275,54 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
   // either after they change.  No atomics: every word has one writer.
   const bool real = row < a.rows;
   const int slot = real ? scalar_load(a.slots + row) : -1;
+  const bool slot_ok = slot >= 0 && slot < a.num_slots;
   if (threadIdx.x == 0) {
     const uint32_t epoch = static_cast<uint32_t>(scalar_load(reinterpret_cast<const int32_t*>(a.header + kHdrEpoch)));
     int pos = -1;
-    if (real && slot >= 0 && slot < a.num_slots) {
-      pos = a.positions ? scalar_load(a.positions + row) : scalar_load(a.working_lens + slot);
-    }
+    if (real && slot_ok) pos = a.positions ? scalar_load(a.positions + row) : scalar_load(a.working_lens + slot);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     s_pos = (pos >= 0 && pos < a.budget) ? pos : -1;
     s_tag = epoch + 1;
     if (real) coherent_store(a.seen + blockIdx.x, tagged(epoch + 1, 0.f));
+  }
+
+  const int64_t work_base = (static_cast<int64_t>(slot_ok ? slot : 0) * a.hkv + kvh) * a.budget * D;
+  const uint16_t* kw = static_cast<const uint16_t*>(a.work_k) + work_base;
+  const uint16_t* vw = static_cast<const uint16_t*>(a.work_v) + work_base;
+  const uint16_t* kin = static_cast<const uint16_t*>(a.k_in) + row * a.k_row + kvh * a.k_head;
+  const uint16_t* vin = static_cast<const uint16_t*>(a.v_in) + row * a.v_row + kvh * a.v_head;
+  const int t0 = split * S::kSpan + wave * S::kTiles * kTileT;
+
+  // One tile's operands: K rows for the score MFMAs, V rows for the output.
+  struct Tile {
+    u32x4 k[S::kSteps];
+    uint32_t v[4][J / 2];
+  };
+  // Loads of tile tb from the working rows only (rows clamped to the
+  // cache); the rows from the position on are fixed up once it is known.
+  auto load_tile_rows = [&](Tile& T, int tb) {
+    const uint16_t* pk = kw + static_cast<int64_t>(min(tb + col, a.budget - 1)) * D + 8 * quad;
+#pragma unroll
+    for (int i = 0; i < S::kSteps; ++i) T.k[i] = load16(pk + 32 * i);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      load_words<J>(vw + static_cast<int64_t>(min(tb + 4 * quad + r, a.budget - 1)) * D + J * col, T.v[r]);
+    }
+  };
+  // The first pair of the wave's tiles and this row's input K / V slices are
+  // requested before the position arrives (the position is a second
+  // dependent load after the slot).  Every address is valid whatever the
+  // position: working rows below the cache capacity and the input row.
+  Tile ta, tb_, tc, td;
+  u32x4 kin_s[S::kSteps];
+  uint32_t vin_s[J / 2];
+  const bool early = real && slot_ok && t0 < a.budget;
+  if (early) {
+    load_tile_rows(ta, t0);
+    load_tile_rows(tb_, t0 + kTileT);
+#pragma unroll
+    for (int i = 0; i < S::kSteps; ++i) kin_s[i] = load16(kin + 8 * quad + 32 * i);
+    load_words<J>(vin + J * col, vin_s);
   }
   lds_barrier();
   const int pos = s_pos;
@@ -311,12 +349,6 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
     return;
   }
 
-  const int64_t work_base = (static_cast<int64_t>(slot) * a.hkv + kvh) * a.budget * D;
-  const uint16_t* kw = static_cast<const uint16_t*>(a.work_k) + work_base;
-  const uint16_t* vw = static_cast<const uint16_t*>(a.work_v) + work_base;
-  const uint16_t* kin = static_cast<const uint16_t*>(a.k_in) + row * a.k_row + kvh * a.k_head;
-  const uint16_t* vin = static_cast<const uint16_t*>(a.v_in) + row * a.v_row + kvh * a.v_head;
-
   // Query block as the B operand of the score MFMAs: lane (quad, col) holds
   // q[head0 + col][32 i + 8 quad .. + 8]; columns past the group are zero.
   // Every load of the main loop is unconditional (addresses clamped to valid
@@ -338,15 +370,9 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
   for (int j = 0; j < J; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, lsum = 0.f;
   const float c = a.scale * kLog2e;
-  const int t0 = split * S::kSpan + wave * S::kTiles * kTileT;
 
-  // One tile's operands: K rows for the score MFMAs, V rows for the output.
   // Rows at or past n read row n - 1 = pos (the new token's input row): a
   // valid, finite row whose scores are masked to -inf below.
-  struct Tile {
-    u32x4 k[S::kSteps];
-    uint32_t v[4][J / 2];
-  };
   auto row_ptr = [&](const uint16_t* work, const uint16_t* in, int t) {
     return t >= pos ? in : work + static_cast<int64_t>(t) * D;
   };
@@ -356,6 +382,22 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
     for (int i = 0; i < S::kSteps; ++i) T.k[i] = load16(pk + 32 * i);
 #pragma unroll
     for (int r = 0; r < 4; ++r) load_words<J>(row_ptr(vw, vin, tb + 4 * quad + r) + J * col, T.v[r]);
+  };
+  // A tile loaded from the working rows: the position's row becomes the
+  // input row, later rows of V become zeros (their probabilities are 0, and
+  // stale cache words may not be finite; K rows there only feed masked
+  // scores).
+  auto fix_tile = [&](Tile& T, int tb) {
+    if (tb + col == pos) {
+#pragma unroll
+      for (int i = 0; i < S::kSteps; ++i) T.k[i] = kin_s[i];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = tb + 4 * quad + r;
+#pragma unroll
+      for (int w = 0; w < J / 2; ++w) T.v[r][w] = t == pos ? vin_s[w] : (t > pos ? 0u : T.v[r][w]);
+    }
   };
   // Scores, online softmax and output for the 32 tokens tb .. tb + 31 held in
   // tiles T0 and T1.  The output MFMAs are 16x16x32 in the cache dtype with
@@ -413,33 +455,29 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
     }
   };
 
-  // All of the wave's tiles are in flight before the first pair is computed
-  // (the scheduling barrier keeps the compiler from sinking the loads next to
-  // their use); pairs wholly past n are loaded (cache hits on row pos) but
+  // The first pair came from the working rows and is fixed up here; the
+  // second pair is requested now, before the first is computed (the
+  // scheduling barrier keeps the compiler from sinking the loads next to
+  // their use); a pair wholly past n is loaded (cache hits on row pos) but
   // not computed.
   if (t0 < n) {
+    fix_tile(ta, t0);
+    fix_tile(tb_, t0 + kTileT);
     if constexpr (S::kTiles == 4) {
-      Tile ta, tb, tc, td;
-      load_tile(ta, t0);
-      load_tile(tb, t0 + kTileT);
       load_tile(tc, t0 + 2 * kTileT);
       load_tile(td, t0 + 3 * kTileT);
       __builtin_amdgcn_sched_barrier(0);
-      compute_pair(ta, tb, t0);
+      compute_pair(ta, tb_, t0);
       if (t0 + 2 * kTileT < n) compute_pair(tc, td, t0 + 2 * kTileT);
     } else {
-      Tile ta, tb;
-      load_tile(ta, t0);
-      load_tile(tb, t0 + kTileT);
-      __builtin_amdgcn_sched_barrier(0);
-      compute_pair(ta, tb, t0);
+      compute_pair(ta, tb_, t0);
     }
   }
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
 
-  // The new token goes into the working cache (no workgroup of this launch
-  // reads that row of the cache: rows >= pos come from the input).
+  // The new token goes into the working cache (a workgroup of this launch
+  // that reads that row of the cache early replaces it with the input row).
   if (qb == 0 && split == pos / S::kSpan && threadIdx.x < D / 4) {
     const int e = threadIdx.x % (D / 8);
     const bool is_v = threadIdx.x >= D / 8;
@@ -447,63 +485,53 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
     *reinterpret_cast<u32x4*>(dst + 8 * e) = load16((is_v ? vin : kin) + 8 * e);
   }
 
-  // Merge the four waves: common max, rescale, sum in wave order.
+  // The four waves' running max, sum and unnormalised outputs go to LDS as
+  // they are; one barrier, then thread t merges item (query g, outputs e ..
+  // e + 3) over the waves in wave order: common max, rescaled sums.
+  const int d0 = 4 * J * quad;  // lane's outputs: d = d0 + J * i + j
   if (quad == 0) {
     s_m[wave][col] = m;
     s_l[wave][col] = lsum;
   }
-  lds_barrier();
-  float mx = s_m[0][col];
 #pragma unroll
-  for (int w = 1; w < kWavesA; ++w) mx = fmaxf(mx, s_m[w][col]);
-  float total_l = 0.f;
+  for (int i = 0; i < 4; ++i) {
 #pragma unroll
-  for (int w = 0; w < kWavesA; ++w) total_l += s_l[w][col] * fast_exp2(s_m[w][col] - mx);
-  const float f = fast_exp2(m - mx);
-  const int d0 = 4 * J * quad;  // lane's outputs: d = d0 + J * i + j
-  if (wave > 0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int j = 0; j < J; ++j) s_acc[wave - 1][col][d0 + J * i + j] = acc[j][i] * f;
-    }
+    for (int j = 0; j < J; ++j) s_acc[wave][col][d0 + J * i + j] = acc[j][i];
   }
   lds_barrier();
-  // Wave 0 holds the span's result: unnormalised sums in acc, max mx, sum total_l.
-  if (wave == 0) {
+  constexpr int kChunks = D / 4;
+  const int items = gcount * kChunks;
+  // This span's (max, sum, outputs e .. e + 3) of query g.
+  auto span_item = [&](int g, int e, float& mx, float& total_l) -> f32x4 {
+    mx = s_m[0][g];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int w = 1; w < kWavesA; ++w) mx = fmaxf(mx, s_m[w][g]);
+    total_l = 0.f;
+    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < J; ++j) {
-        float v = acc[j][i] * f;
-#pragma unroll
-        for (int ww = 0; ww < kWavesA - 1; ++ww) v += s_acc[ww][col][d0 + J * i + j];
-        acc[j][i] = v;
-      }
+    for (int w = 0; w < kWavesA; ++w) {
+      const float f = fast_exp2(s_m[w][g] - mx);
+      total_l += s_l[w][g] * f;
+      const f32x4 x = *reinterpret_cast<const f32x4*>(&s_acc[w][g][e]);
+      v = w == 0 ? x * f : v + x * f;
     }
-  }
+    return v;
+  };
+  auto store_out = [&](int g, int e, f32x4 v, float inv) {
+    uint16_t* o = static_cast<uint16_t*>(a.out) + row * a.o_row + (head0 + g) * a.o_head + e;
+    const uint32_t w0 = static_cast<uint32_t>(Elem<DT>::store(v[0] * inv)) |
+                        (static_cast<uint32_t>(Elem<DT>::store(v[1] * inv)) << 16);
+    const uint32_t w1 = static_cast<uint32_t>(Elem<DT>::store(v[2] * inv)) |
+                        (static_cast<uint32_t>(Elem<DT>::store(v[3] * inv)) << 16);
+    *reinterpret_cast<u32x2*>(o) = u32x2{w0, w1};
+  };
 
   if (active == 1) {
-    if (wave == 0 && col < gcount) {
-      const float inv = 1.f / total_l;
-      uint16_t* o = static_cast<uint16_t*>(a.out) + row * a.o_row + (head0 + col) * a.o_head + d0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t w[J / 2];
-#pragma unroll
-        for (int j = 0; j < J; j += 2) {
-          w[j / 2] = static_cast<uint32_t>(Elem<DT>::store(acc[j][i] * inv)) |
-                     (static_cast<uint32_t>(Elem<DT>::store(acc[j + 1][i] * inv)) << 16);
-        }
-        if constexpr (J == 4) {
-          *reinterpret_cast<u32x2*>(o + J * i) = u32x2{w[0], w[1]};
-        } else {
-#pragma unroll
-          for (int h = 0; h < J / 8; ++h) {
-            *reinterpret_cast<u32x4*>(o + J * i + 8 * h) = u32x4{w[4 * h], w[4 * h + 1], w[4 * h + 2], w[4 * h + 3]};
-          }
-        }
-      }
+    for (int item = threadIdx.x; item < items; item += kThreadsA) {
+      const int g = item / kChunks, e = 4 * (item % kChunks);
+      float mx, total_l;
+      const f32x4 v = span_item(g, e, mx, total_l);
+      store_out(g, e, v, 1.f / total_l);
     }
     finish();
     return;
@@ -519,36 +547,17 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
   // result does not depend on arrival order.
   const int unit = (row * a.hkv + kvh) * a.qblocks + qb;
   float* part_base = a.partials + static_cast<int64_t>(unit) * a.splits * kGroupQ * S::kRow;
-  lds_barrier();  // every wave is done reading s_acc
-  if (wave == 0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int j = 0; j < J; ++j) s_acc[0][col][d0 + J * i + j] = acc[j][i];
-    }
-    if (quad == 0) {
-      s_m[0][col] = mx;
-      s_l[0][col] = total_l;
-    }
-  }
-  lds_barrier();
   // The row's partials as a buffer resource: 16-byte device-scope (sc1)
   // accesses, written through to memory and read past the per-XCD caches.
   const Rsrc16 prs = make_rsrc16(part_base, static_cast<int64_t>(a.splits) * kGroupQ * S::kRow * 4);
-  {
-    // Row g of a span's partial: D outputs, then (max, sum, 0, 0).
-    constexpr int kVec = S::kRow / 4;
-    const uint32_t span_off = static_cast<uint32_t>(split * kGroupQ * S::kRow * 4);
-    for (int w = threadIdx.x; w < gcount * kVec; w += kThreadsA) {
-      const int g = w / kVec, c = w % kVec;
-      f32x4 v;
-      if (c < D / 4) {
-        v = f32x4{s_acc[0][g][4 * c], s_acc[0][g][4 * c + 1], s_acc[0][g][4 * c + 2], s_acc[0][g][4 * c + 3]};
-      } else {
-        v = f32x4{s_m[0][g], s_l[0][g], 0.f, 0.f};
-      }
-      store16_sc1(prs, span_off + static_cast<uint32_t>((g * S::kRow + 4 * c) * 4), v);
-    }
+  // Row g of a span's partial: D outputs, then (max, sum, 0, 0).
+  const uint32_t span_off = static_cast<uint32_t>(split * kGroupQ * S::kRow * 4);
+  for (int item = threadIdx.x; item < items; item += kThreadsA) {
+    const int g = item / kChunks, e = 4 * (item % kChunks);
+    float mx, total_l;
+    const f32x4 v = span_item(g, e, mx, total_l);
+    store16_sc1(prs, span_off + static_cast<uint32_t>((g * S::kRow + e) * 4), v);
+    if (e == 0) store16_sc1(prs, span_off + static_cast<uint32_t>((g * S::kRow + D) * 4), f32x4{mx, total_l, 0.f, 0.f});
   }
   // The stores are device-scope write-throughs: once this thread's are
   // acknowledged they are visible to every workgroup.
@@ -566,10 +575,8 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
     return;
   }
 
-  // Merge: thread -> (query g, 4 consecutive outputs), spans in index order,
-  // every other span's words requested at once (kGroupS spans per round).
-  constexpr int kChunks = D / 4;
-  const int items = gcount * kChunks;
+  // Merge: spans in index order, every other span's words requested at once
+  // (kGroupS spans per round); this span's values come from LDS.
   for (int item = threadIdx.x; item < items; item += kThreadsA) {
     const int g = item / kChunks;
     const int e = 4 * (item % kChunks);
@@ -594,9 +601,7 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
         float m_s, l_s;
         f32x4 a_s;
         if (sp == split) {
-          m_s = s_m[0][g];
-          l_s = s_l[0][g];
-          a_s = f32x4{s_acc[0][g][e], s_acc[0][g][e + 1], s_acc[0][g][e + 2], s_acc[0][g][e + 3]};
+          a_s = span_item(g, e, m_s, l_s);
         } else {
           m_s = pml[u][0];
           l_s = pml[u][1];
@@ -610,13 +615,7 @@ __global__ __launch_bounds__(kThreadsA, 2) void draft_attention_kernel(AttnArgs 
         run_m = gm;
       }
     }
-    const float inv = 1.f / run_l;
-    uint16_t* o = static_cast<uint16_t*>(a.out) + row * a.o_row + (head0 + g) * a.o_head + e;
-    const uint32_t w0 = static_cast<uint32_t>(Elem<DT>::store(run[0] * inv)) |
-                        (static_cast<uint32_t>(Elem<DT>::store(run[1] * inv)) << 16);
-    const uint32_t w1 = static_cast<uint32_t>(Elem<DT>::store(run[2] * inv)) |
-                        (static_cast<uint32_t>(Elem<DT>::store(run[3] * inv)) << 16);
-    *reinterpret_cast<u32x2*>(o) = u32x2{w0, w1};
+    store_out(g, e, run, 1.f / run_l);
   }
   finish();
 }

@@ -234,7 +234,7 @@ def attention_calls(monkeypatch):
     calls = []
 
     def record(query, key, value, output, working_key, working_value, working_lens, slots, positions=None, *,
-               scale, workspace, reuse=None):
+               scale, workspace, reuse=None, reuse_key=None):
         calls.append(dict(slots=slots.tolist() if isinstance(slots, torch.Tensor) else list(slots),
                           positions=positions.tolist() if isinstance(positions, torch.Tensor) else positions,
                           scale=scale, rows=output.shape[0]))
@@ -283,7 +283,8 @@ def capture_calls(monkeypatch):
     calls = []
 
     def record(key, value, raw_key, raw_value, token_slots, absolute_positions, rope_buffer, *, tokens,
-               working_lens=None, local_positions=None, prev_count=0, status=None, reuse=None):
+               working_lens=None, local_positions=None, prev_count=0, status=None, reuse=None,
+               reuse_key=None):
         calls.append(dict(slots=token_slots[:tokens].tolist(), positions=absolute_positions.reshape(-1).tolist(),
                           tokens=tokens, rope=rope_buffer is not None, working_lens=working_lens is not None,
                           key=key[:tokens].clone()))

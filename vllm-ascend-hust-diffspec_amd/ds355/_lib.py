@@ -169,6 +169,37 @@ def ptr(t: torch.Tensor | None) -> int | None:
 # kernels launch on); a few microseconds cheaper than building a Stream object.
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
+_hip: ctypes.CDLL | None = None
+HIP_MEMCPY_HOST_TO_DEVICE = 1
+HIP_EVENT_DISABLE_TIMING = 2
+
+
+def hip_runtime() -> ctypes.CDLL:
+    """The HIP runtime already loaded in the process (torch's, which the
+    library's kernels and streams share), for small host-side copies and
+    events without torch's dispatch cost.  Never loads a second copy."""
+    global _hip
+    if _hip is None:
+        hip = ctypes.CDLL("libamdhip64.so.7", mode=os.RTLD_NOLOAD | os.RTLD_LAZY)
+        hip.hipMemcpyAsync.restype = ctypes.c_int
+        hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                       ctypes.c_void_p]
+        hip.hipEventCreateWithFlags.restype = ctypes.c_int
+        hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        hip.hipEventRecord.restype = ctypes.c_int
+        hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        hip.hipEventSynchronize.restype = ctypes.c_int
+        hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        hip.hipEventDestroy.restype = ctypes.c_int
+        hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        _hip = hip
+    return _hip
+
+
+def hip_check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise RuntimeError(f"{what} failed with HIP error {rc}")
+
 
 def stream_handle(device: torch.device) -> int:
     """Raw HIP handle of torch's current stream on ``device``."""

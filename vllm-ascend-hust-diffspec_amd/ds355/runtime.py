@@ -19,12 +19,14 @@ drafting and the adaptive controller are outside this module.
 
 from __future__ import annotations
 
+import ctypes
 import time
 from dataclasses import dataclass
 from typing import Any
 
 import torch
 
+from . import _lib
 from . import attention as _attention
 from . import capture as _capture
 from . import step as _step
@@ -75,32 +77,58 @@ class DiffSpecRuntimeMetrics:
 
 
 class _Staging:
-    """Ring of pinned host buffers for small int32 row arrays (non-blocking H2D)."""
+    """Ring of pinned host buffers for small int32 row arrays (non-blocking H2D).
+
+    On a GPU the copy and the ring's events go straight to the HIP runtime
+    (a few microseconds less per upload than torch's copy and Event); a
+    buffer is refilled only after its previous copy has run (its event)."""
 
     def __init__(self, fields: int, rows: int, device: torch.device, depth: int = 4) -> None:
         pin = device.type == "cuda"
         self.host = [torch.zeros((fields, rows), dtype=torch.int32, pin_memory=pin) for _ in range(depth)]
         self.host_np = [h.numpy() for h in self.host]  # list -> pinned buffer without a temporary tensor
-        self.events = [torch.cuda.Event() for _ in range(depth)] if pin else None
         self.recorded = [False] * depth
-        self.device_index = device.index if device.index is not None else (torch.cuda.current_device() if pin else 0)
         self.device = torch.zeros((fields, rows), dtype=torch.int32, device=device)
         self.index = 0
+        self.hip = None
+        if pin:
+            self.hip = _lib.hip_runtime()
+            self.torch_device = device if device.index is not None else torch.device("cuda", torch.cuda.current_device())
+            self.events = []
+            for _ in range(depth):
+                ev = ctypes.c_void_p()
+                _lib.hip_check(self.hip.hipEventCreateWithFlags(ctypes.byref(ev), _lib.HIP_EVENT_DISABLE_TIMING),
+                               "hipEventCreateWithFlags")
+                self.events.append(ev)
+            self.nbytes = fields * rows * 4
+            self.host_ptr = [h.data_ptr() for h in self.host]
+            self.device_ptr = self.device.data_ptr()
+
+    def __del__(self) -> None:
+        hip = getattr(self, "hip", None)
+        if hip is not None:
+            for ev in self.events:
+                hip.hipEventDestroy(ev)
 
     def upload(self, columns: list[list[int]]) -> torch.Tensor:
         i = self.index
         self.index = (i + 1) % len(self.host)
-        if self.recorded[i]:
-            self.events[i].synchronize()  # only waits if the GPU is a full ring behind
+        hip = self.hip
+        if hip is not None and self.recorded[i]:
+            # Only waits if the GPU is a full ring behind.
+            _lib.hip_check(hip.hipEventSynchronize(self.events[i]), "hipEventSynchronize")
         buf = self.host_np[i]
         for f, values in enumerate(columns):
             if len(values):
                 buf[f, : len(values)] = values
-        self.device.copy_(self.host[i], non_blocking=True)
-        if self.events is not None:
-            # An explicit stream: record() without one resolves the current device first.
-            self.events[i].record(torch.cuda.current_stream(self.device_index))
-            self.recorded[i] = True
+        if hip is None:
+            self.device.copy_(self.host[i])
+            return self.device
+        stream = _lib.stream_handle(self.torch_device)
+        _lib.hip_check(hip.hipMemcpyAsync(self.device_ptr, self.host_ptr[i], self.nbytes,
+                                          _lib.HIP_MEMCPY_HOST_TO_DEVICE, stream), "hipMemcpyAsync")
+        _lib.hip_check(hip.hipEventRecord(self.events[i], stream), "hipEventRecord")
+        self.recorded[i] = True
         return self.device
 
 
@@ -209,6 +237,7 @@ class DiffSpecDraftCache:
         self._pending_request_indices: list[int] | None = None
         self._pending_local_positions: Any = None
         self._attention_workspace: torch.Tensor | None = None
+        self._attention_workspace_for: tuple[int, int] | None = None  # (rows, heads) it was checked for
         # Draft cycle and capture state (runtime.py:677-699, 731-753, 1767-1794).
         self._cycle_open = False
         self._draft_step = 0
@@ -533,7 +562,7 @@ class DiffSpecDraftCache:
         if self._slot_map_list != slots:
             self._slot_map.upload([slots])
             self._slot_map_list = list(slots)
-        return self._slot_map.device[0, : len(slots)]
+        return self._view("slot_map", len(slots), lambda: self._slot_map.device[0, : len(slots)])
 
     def _rope_buffer(self, dtype: torch.dtype) -> torch.Tensor:
         buffer = self._rope_position_buffers.get(dtype)
@@ -602,10 +631,15 @@ class DiffSpecDraftCache:
         buffer = self._rope_buffer(dtype)
         prev = self._rope_position_written.get(dtype, 0)
         if self._cycle_open:
+            # The cache's own buffers (raw caches, RoPE buffer of this dtype,
+            # working lengths, status, the slot row of this length) are fixed:
+            # the launch layout is the draft tensors' layout and the counts.
+            reuse_key = (key.shape, key.stride(), value.shape, value.stride(), key.dtype, value.dtype,
+                         absolute_positions.shape, absolute_positions.stride(), dtype, num_tokens, prev)
             rope = _capture.capture_raw_kv_rows(
                 key, value, self.raw_key, self.raw_value, token_slots, absolute_positions, buffer,
                 tokens=num_tokens, working_lens=self.working_lens, prev_count=prev, status=self._capture_status,
-                reuse=self._capture_reuse)
+                reuse=self._capture_reuse, reuse_key=reuse_key)
             self._rope_position_written[dtype] = absolute_positions.numel()
             self._pending_request_indices = list(slots)
             self._pending_local_positions = WORKING_LENS
@@ -684,13 +718,15 @@ class DiffSpecDraftCache:
         rows = len(slots)
         heads = query.shape[1] if query.dim() == 3 else query.shape[1] // self.head_dim
         workspace = self._attention_workspace
-        need = _attention.attention_workspace_bytes(max(self.max_batch_rows, rows), heads, self.num_kv_heads,
-                                                    self.head_dim, self.settings.token_budget)
-        if workspace is None or workspace.numel() < need:
-            workspace = _attention.new_attention_workspace(max(self.max_batch_rows, rows), heads,
-                                                           self.num_kv_heads, self.head_dim,
-                                                           self.settings.token_budget, self.device)
-            self._attention_workspace = workspace
+        if self._attention_workspace_for != (rows, heads):
+            need = _attention.attention_workspace_bytes(max(self.max_batch_rows, rows), heads, self.num_kv_heads,
+                                                        self.head_dim, self.settings.token_budget)
+            if workspace is None or workspace.numel() < need:
+                workspace = _attention.new_attention_workspace(max(self.max_batch_rows, rows), heads,
+                                                               self.num_kv_heads, self.head_dim,
+                                                               self.settings.token_budget, self.device)
+                self._attention_workspace = workspace
+            self._attention_workspace_for = (rows, heads)
         if isinstance(positions, list):
             if len(positions) != rows:
                 raise ValueError("one local position per pending row is required")
@@ -701,9 +737,16 @@ class DiffSpecDraftCache:
             slot_rows = self._device_slots(list(slots))
             if isinstance(positions, list):
                 positions = self._attention_staging.upload([[], positions])[1, :rows]
+        # Fixed here: the working caches and lengths, the workspace, the slot
+        # row and the positions row of this length; the rest is the layout of
+        # the caller's tensors.
+        reuse_key = (query.shape, query.stride(), key.shape, key.stride(), value.shape, value.stride(),
+                     output.shape, output.stride(), query.dtype, key.dtype, value.dtype, output.dtype, rows,
+                     positions is None, float(scale), workspace.data_ptr())
         _attention.draft_linear_attention(
             query, key, value, output, self.working_key, self.working_value, self.working_lens,
             slot_rows, positions, scale=scale, workspace=workspace, reuse=self._attention_reuse,
+            reuse_key=reuse_key if rows else None,
         )
         self._pending_request_indices = None
         self._pending_local_positions = None
@@ -749,6 +792,19 @@ class DiffSpecDraftCache:
             q, lse, kc, bt = snapshot.query, snapshot.lse, snapshot.key_cache, snapshot.block_table
             key += (q.shape, q.stride(), q.dtype, kc.shape, kc.stride(), kc.dtype, bt.shape, bt.stride(), bt.dtype,
                     None if lse is None else (lse.shape, lse.stride(), lse.dtype))
+        hit = self._step_descs.get(key)
+        if hit is not None:
+            # The descriptor validated for this layout: only the verifier
+            # snapshot's addresses, its scale and the committed counts change
+            # (what retrieval_step(fixed_buffers=True) refreshes).
+            desc, device = hit
+            if snapshot is not None and stages & (_step.SCORE | _step.SELECT):
+                desc.query, desc.lse = snapshot.query.data_ptr(), _lib.ptr(snapshot.lse)
+                desc.key_cache, desc.block_table = snapshot.key_cache.data_ptr(), snapshot.block_table.data_ptr()
+                desc.scale = float(snapshot.scale)
+                desc.counts = rows.counts.data_ptr()
+            _step.launch(desc, device)
+            return
         _step.retrieval_step(
             reuse=self._step_descs, reuse_key=key, fixed_buffers=True,
             stages=stages, snapshot=snapshot, rows=rows,

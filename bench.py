@@ -572,8 +572,9 @@ def workload_leg(name, seed, device, steps=20, with_cpu=True):
         "algorithmic_bytes": chain_bytes,
         "achieved_gbps": round(gbps, 1),
         "frac": round(gbps / HBM_PEAK_GBPS, 4),
-        "mall": "cold" if min(step_bytes, gather_bytes) * len(copies) > MALL_BYTES
-                else f"warm ({len(copies)} copies of {step_bytes / 1e6:.0f} MB stay inside the 256 MB MALL)",
+        "mall": (f"step {'cold' if step_bytes * len(copies) > MALL_BYTES else 'warm'}, compact prefill "
+                 f"{'cold' if gather_bytes * len(copies) > MALL_BYTES else 'warm'} ({len(copies)} rotated copies "
+                 f"of {step_bytes / 1e6:.0f} MB and {gather_bytes / 1e6:.0f} MB against the 256 MB MALL)"),
         "copies": len(copies),
         "runtime_two_calls_us": {"score_select": round(score_select_us, 2), "compact_prefill": round(prefill_us, 2),
                                  "total": round(two_call, 2),

@@ -80,14 +80,22 @@ class _Staging:
     """Ring of pinned host buffers for small int32 row arrays (non-blocking H2D).
 
     On a GPU the copy and the ring's events go straight to the HIP runtime
-    (a few microseconds less per upload than torch's copy and Event); a
-    buffer is refilled only after its previous copy has run (its event)."""
+    (a few microseconds less per upload than torch's copy and Event).  The
+    ring is cut into groups of ``group`` buffers with one event each,
+    recorded after the group's last copy: the first buffer of a group is
+    refilled only once the group's copies of the previous lap have run, so
+    one upload in ``group`` records an event and the others record none.
+    Uploads go to one device buffer, so consumers are ordered by the stream.
+    """
 
-    def __init__(self, fields: int, rows: int, device: torch.device, depth: int = 4) -> None:
+    def __init__(self, fields: int, rows: int, device: torch.device, depth: int = 32, group: int = 8) -> None:
+        if depth % group:
+            raise ValueError("the ring depth must be a multiple of the group size")
         pin = device.type == "cuda"
         self.host = [torch.zeros((fields, rows), dtype=torch.int32, pin_memory=pin) for _ in range(depth)]
         self.host_np = [h.numpy() for h in self.host]  # list -> pinned buffer without a temporary tensor
-        self.recorded = [False] * depth
+        self.group = group
+        self.recorded = [False] * (depth // group)
         self.device = torch.zeros((fields, rows), dtype=torch.int32, device=device)
         self.index = 0
         self.hip = None
@@ -95,7 +103,7 @@ class _Staging:
             self.hip = _lib.hip_runtime()
             self.torch_device = device if device.index is not None else torch.device("cuda", torch.cuda.current_device())
             self.events = []
-            for _ in range(depth):
+            for _ in range(depth // group):
                 ev = ctypes.c_void_p()
                 _lib.hip_check(self.hip.hipEventCreateWithFlags(ctypes.byref(ev), _lib.HIP_EVENT_DISABLE_TIMING),
                                "hipEventCreateWithFlags")
@@ -113,10 +121,11 @@ class _Staging:
     def upload(self, columns: list[list[int]]) -> torch.Tensor:
         i = self.index
         self.index = (i + 1) % len(self.host)
+        g, k = divmod(i, self.group)
         hip = self.hip
-        if hip is not None and self.recorded[i]:
+        if hip is not None and k == 0 and self.recorded[g]:
             # Only waits if the GPU is a full ring behind.
-            _lib.hip_check(hip.hipEventSynchronize(self.events[i]), "hipEventSynchronize")
+            _lib.hip_check(hip.hipEventSynchronize(self.events[g]), "hipEventSynchronize")
         buf = self.host_np[i]
         for f, values in enumerate(columns):
             if len(values):
@@ -127,8 +136,9 @@ class _Staging:
         stream = _lib.stream_handle(self.torch_device)
         _lib.hip_check(hip.hipMemcpyAsync(self.device_ptr, self.host_ptr[i], self.nbytes,
                                           _lib.HIP_MEMCPY_HOST_TO_DEVICE, stream), "hipMemcpyAsync")
-        _lib.hip_check(hip.hipEventRecord(self.events[i], stream), "hipEventRecord")
-        self.recorded[i] = True
+        if k == self.group - 1:
+            _lib.hip_check(hip.hipEventRecord(self.events[g], stream), "hipEventRecord")
+            self.recorded[g] = True
         return self.device
 
 
@@ -458,19 +468,29 @@ class DiffSpecDraftCache:
                 or counts.numel() < batch_size):
             counts = self._view("counts", batch_size, lambda: staged[4, :batch_size])
             counts.copy_(valid_sampled_token_count.reshape(-1)[:batch_size])  # device-side cast, no sync
-        rows = _step.VerifierRows(
-            counts=counts, query_start=self._view("qs", 0, lambda: staged[0]),
-            query_len=self._view("ql", 0, lambda: staged[1]), target_len=self._view("tl", 0, lambda: staged[2]),
-            batch_size=batch_size,
-        )
-        snapshot = _step.VerifierSnapshot(
-            query=self._target_query, lse=self._target_lse, key_cache=self._target_key_cache,
-            block_table=self._target_block_tables, scale=self._target_scale,
-        )
         started = time.perf_counter()
-        self._launch(_step.SCORE | _step.SELECT, batch_size, snapshot=snapshot, rows=rows,
-                     slots=self._view("rs", batch_size, lambda: staged[3, :batch_size]),
-                     committed=self._view("rc", batch_size, lambda: staged[2, :batch_size]))
+        q, lse, kc, bt = self._target_query, self._target_lse, self._target_key_cache, self._target_block_tables
+        stages = _step.SCORE | _step.SELECT
+        hit = self._step_descs.get(self._step_key(stages, batch_size, batch_size, self._cos_sin_cache(), q, lse, kc,
+                                                  bt))
+        if hit is not None:
+            # The descriptor validated for this layout (what _launch refreshes).
+            desc, device = hit
+            desc.query, desc.lse, desc.key_cache, desc.block_table = (q.data_ptr(), _lib.ptr(lse), kc.data_ptr(),
+                                                                      bt.data_ptr())
+            desc.scale = float(self._target_scale)
+            desc.counts = counts.data_ptr()
+            _step.launch(desc, device)
+        else:
+            rows = _step.VerifierRows(
+                counts=counts, query_start=self._view("qs", 0, lambda: staged[0]),
+                query_len=self._view("ql", 0, lambda: staged[1]), target_len=self._view("tl", 0, lambda: staged[2]),
+                batch_size=batch_size,
+            )
+            snapshot = _step.VerifierSnapshot(query=q, lse=lse, key_cache=kc, block_table=bt, scale=self._target_scale)
+            self._launch(stages, batch_size, snapshot=snapshot, rows=rows,
+                         slots=self._view("rs", batch_size, lambda: staged[3, :batch_size]),
+                         committed=self._view("rc", batch_size, lambda: staged[2, :batch_size]))
         self.metrics.observe_retrieval(time.perf_counter() - started)
 
     # -- rebuild (runtime.py:1349-1371, 1683-1765) ------------------------------------------------
@@ -771,6 +791,7 @@ class DiffSpecDraftCache:
                 self._score_partials = torch.zeros((self.max_batch_rows, self.max_chunks, kv_heads),
                                                    dtype=torch.float32, device=self.device)
                 self._views = {k: v for k, v in self._views.items() if k[0] != "partials"}
+                self._step_descs.clear()  # they hold the old buffer's address
             partials = self._view("partials", batch_rows, lambda: self._score_partials[:batch_rows])
         lse_partials = lse_out = None
         if stages & _step.SCORE and snapshot.lse is None:
@@ -781,17 +802,14 @@ class DiffSpecDraftCache:
                 self.scored_lse = torch.zeros((self.max_batch_rows, q_heads), dtype=torch.float32,
                                               device=self.device)
                 self._views = {k: v for k, v in self._views.items() if k[0] not in ("pairs", "lse_out")}
+                self._step_descs.clear()
             lse_partials = self._view("pairs", batch_rows, lambda: self._lse_partials[:batch_rows])
             lse_out = self._view("lse_out", batch_rows, lambda: self.scored_lse[:batch_rows])
-        # Everything but buffer addresses that the validated descriptor depends
-        # on: the cache's own buffers keep their shapes, so the key is the
-        # stage mask, the batch and the verifier snapshot's layout.
-        key = (stages, batch_rows, None if rows is None else rows.batch_size, cos_sin.shape, cos_sin.stride(0),
-               rotary.rotary_dim, bool(rotary.is_neox_style))
-        if snapshot is not None:
-            q, lse, kc, bt = snapshot.query, snapshot.lse, snapshot.key_cache, snapshot.block_table
-            key += (q.shape, q.stride(), q.dtype, kc.shape, kc.stride(), kc.dtype, bt.shape, bt.stride(), bt.dtype,
-                    None if lse is None else (lse.shape, lse.stride(), lse.dtype))
+        key = self._step_key(stages, batch_rows, None if rows is None else rows.batch_size, cos_sin,
+                             snapshot.query if snapshot is not None else None,
+                             snapshot.lse if snapshot is not None else None,
+                             snapshot.key_cache if snapshot is not None else None,
+                             snapshot.block_table if snapshot is not None else None)
         hit = self._step_descs.get(key)
         if hit is not None:
             # The descriptor validated for this layout: only the verifier
@@ -819,6 +837,20 @@ class DiffSpecDraftCache:
             chunk_size=self.settings.chunk_size, history_budget=self.history_budget,
             recent_window=self.recent_window, lse_partials=lse_partials, lse_out=lse_out,
         )
+
+    def _step_key(self, stages: int, batch_rows: int, batch_size: int | None, cos_sin: torch.Tensor,
+                  q: torch.Tensor | None, lse: torch.Tensor | None, kc: torch.Tensor | None,
+                  bt: torch.Tensor | None) -> tuple:
+        """Everything but buffer addresses that a validated step descriptor
+        depends on: the cache's own buffers keep their shapes, so the key is
+        the stage mask, the batch and the verifier snapshot's layout."""
+        rotary = self.rotary_embedding
+        key = (stages, batch_rows, batch_size, cos_sin.shape, cos_sin.stride(0), rotary.rotary_dim,
+               bool(rotary.is_neox_style))
+        if q is not None:
+            key += (q.shape, q.stride(), q.dtype, kc.shape, kc.stride(), kc.dtype, bt.shape, bt.stride(), bt.dtype,
+                    None if lse is None else (lse.shape, lse.stride(), lse.dtype))
+        return key
 
     def _cos_sin_cache(self) -> torch.Tensor:
         rotary = self.rotary_embedding

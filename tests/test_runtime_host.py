@@ -369,3 +369,34 @@ def test_retrieval_with_host_counts_and_no_committed_rows_is_skipped(launches):
     assert status["retrieval_skipped_no_committed_tokens"] == 1 and status["retrieval_count"] == 0
     cache.accept_target_queries(torch.tensor([0, 1]), is_prefill=False)
     assert len(launches) == 1 and cache.retrieval_status()["retrieval_count"] == 1
+
+
+def test_cached_step_descriptors_follow_the_partial_buffers(monkeypatch):
+    """A validated descriptor is reused for its layout, and dropped when the buffers it points to are replaced."""
+    built, launched = [], []
+
+    def record(**kw):
+        built.append(kw["score_partials"].data_ptr())
+        desc = SimpleNamespace(partials=kw["score_partials"].data_ptr())
+        kw["reuse"][kw["reuse_key"]] = (desc, torch.device("cpu"))
+
+    monkeypatch.setattr(step, "retrieval_step", record)
+    monkeypatch.setattr(step, "launch", lambda desc, device, stages=None: launched.append(desc))
+    cache = _cache(settings=dict(retrieval_interval=1))
+    q = torch.ones((2, 2, 2))
+    lse = torch.zeros((2, 2))
+
+    def retrieve(kv_heads, counts):
+        cache.begin_target_forward(["r0", "r1"])
+        cache.capture_target_attention(q, lse, torch.zeros((1, 2, kv_heads, 2)), _metadata([1, 2], [6, 4], False), 0.5)
+        cache.accept_target_queries(counts, is_prefill=False)
+
+    retrieve(1, torch.tensor([1, 1], dtype=torch.int32))
+    retrieve(1, torch.tensor([1, 2], dtype=torch.int32))  # same layout: the cached descriptor, refreshed
+    assert len(built) == 1 and len(launched) == 1
+    assert launched[0].counts != 0 and launched[0].scale == 0.5
+    assert launched[0].query == cache._target_query.data_ptr()
+    retrieve(2, torch.tensor([1, 1], dtype=torch.int32))  # two KV heads: new partial buffer, new descriptor
+    retrieve(1, torch.tensor([1, 1], dtype=torch.int32))  # back to one head: rebuilt, not the stale descriptor
+    assert len(built) == 3 and len(launched) == 1
+    assert built[2] == cache._score_partials.data_ptr()

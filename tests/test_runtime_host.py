@@ -400,3 +400,37 @@ def test_cached_step_descriptors_follow_the_partial_buffers(monkeypatch):
     retrieve(1, torch.tensor([1, 1], dtype=torch.int32))  # back to one head: rebuilt, not the stale descriptor
     assert len(built) == 3 and len(launched) == 1
     assert built[2] == cache._score_partials.data_ptr()
+
+
+def test_rows_staged_with_the_snapshot_follow_the_active_slots(monkeypatch):
+    """Rows uploaded when the snapshot is taken are used unless the active slots changed since."""
+    seen = []
+
+    def record(**kw):
+        seen.append(("built", kw["rows"].query_start[:2].tolist(), kw["rows"].query_len[:2].tolist(),
+                     kw["rows"].target_len[:2].tolist(), kw["slots"][:2].tolist()))
+        kw["reuse"][kw["reuse_key"]] = (SimpleNamespace(), torch.device("cpu"))
+
+    def launch(desc, device, stages=None):
+        rows = cache._rows_staging.device
+        seen.append(("launched", rows[0, :2].tolist(), rows[1, :2].tolist(), rows[2, :2].tolist(),
+                     rows[3, :2].tolist()))
+
+    monkeypatch.setattr(step, "retrieval_step", record)
+    monkeypatch.setattr(step, "launch", launch)
+    cache = _cache(settings=dict(retrieval_interval=1))
+    q, lse, kc = torch.ones((3, 2, 2)), torch.zeros((3, 2)), torch.zeros((1, 2, 1, 2))
+    cache.begin_target_forward(["a", "b"])
+    cache.capture_target_attention(q, lse, kc, _metadata([1, 3], [6, 4], False), 0.5)
+    cache.accept_target_queries(torch.tensor([1, 2], dtype=torch.int32), is_prefill=False)
+    slots_ab = list(cache._active_slots)
+    assert seen[-1] == ("built", [0, 1], [1, 2], [6, 4], slots_ab)
+    cache.begin_target_forward(["a", "b"])
+    cache.capture_target_attention(q, lse, kc, _metadata([2, 3], [9, 5], False), 0.5)
+    cache.accept_target_queries(torch.tensor([1, 1], dtype=torch.int32), is_prefill=False)
+    assert seen[-1] == ("launched", [0, 2], [2, 1], [9, 5], slots_ab)
+    cache.begin_target_forward(["a", "b"])
+    cache.capture_target_attention(q, lse, kc, _metadata([1, 2], [7, 8], False), 0.5)
+    cache.set_active_requests(["b", "a"])  # reordered after the snapshot: the rows are staged again
+    cache.accept_target_queries(torch.tensor([1, 1], dtype=torch.int32), is_prefill=False)
+    assert seen[-1] == ("launched", [0, 1], [1, 1], [7, 8], slots_ab[::-1])

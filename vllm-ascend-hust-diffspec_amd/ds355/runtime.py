@@ -257,6 +257,7 @@ class DiffSpecDraftCache:
         self._capture_status = torch.zeros((1,), dtype=torch.int32, device=self.device)
         self._token_staging: _Staging | None = None  # token -> slot rows of populate_prefill
         self._step_descs: dict = {}  # validated step descriptors, reused while the shapes stay
+        self._retrieval_rows: tuple | None = None  # verifier rows staged with the snapshot
         self._views: dict = {}  # slices of the cache's own buffers per batch size (slicing costs microseconds)
         self._attention_reuse: dict = {}
         self._capture_reuse: dict = {}
@@ -323,6 +324,7 @@ class DiffSpecDraftCache:
         self._target_query_ends = []
         self._target_seq_lens = []
         self.target_is_prefill = True
+        self._retrieval_rows = None
 
     def prepare_target_batch(self, request_ids: list[str], scheduled_spec_token_ids: dict[str, list[int]]) -> None:
         """Slots for the verifier batch; verification stays linear (runtime.py:795-813).
@@ -402,6 +404,32 @@ class DiffSpecDraftCache:
         self._target_seq_lens = seq_lens
         self._target_scale = scale
         self.target_is_prefill = is_prefill
+        self._retrieval_rows = None if is_prefill else self._stage_retrieval_rows()
+
+    def _stage_retrieval_rows(self) -> tuple | None:
+        """Upload the verifier rows and compute the step key as soon as the snapshot exists.
+
+        Both depend only on the snapshot and the active slots, so they run
+        while the verifier's forward is still on the GPU, and the retrieval
+        call only adds the committed counts and launches.  None where the
+        retrieval call's own checks decide.
+        """
+        batch_size = len(self._active_slots)
+        ends, seq_lens = self._target_query_ends, self._target_seq_lens
+        if (batch_size == 0 or batch_size > self.max_batch_rows or len(ends) < batch_size
+                or len(seq_lens) < batch_size or self._target_block_tables.shape[0] < batch_size
+                or self.target_tensor_parallel_size > 1):
+            return None
+        ends = ends[:batch_size]
+        starts = [0, *ends[:-1]]
+        if max(seq_lens[:batch_size]) > self.max_chunks * self.settings.chunk_size:
+            return None
+        staged = self._rows_staging.upload([
+            starts, [e - s for s, e in zip(starts, ends)], seq_lens[:batch_size], self._active_slots, [],
+        ])
+        key = self._step_key(_step.SCORE | _step.SELECT, batch_size, batch_size, self._cos_sin_cache(),
+                             self._target_query, self._target_lse, self._target_key_cache, self._target_block_tables)
+        return self._active_slots, staged, key
 
     # -- retrieval (runtime.py:1170-1334) ---------------------------------------------------------
     def accept_target_queries(self, valid_sampled_token_count: torch.Tensor, *, is_prefill: bool) -> None:
@@ -453,14 +481,21 @@ class DiffSpecDraftCache:
                                and int(valid_sampled_token_count.reshape(-1)[:batch_size].max()) <= 0):
             self.metrics.retrieval_skipped_no_committed_tokens += 1
             return
-        ends = self._target_query_ends[:batch_size]
-        starts = [0, *ends[:-1]]
-        lens = [e - s for s, e in zip(starts, ends)]
-        if max(self._target_seq_lens[:batch_size]) > self.max_chunks * self.settings.chunk_size:
-            raise ValueError("verifier length exceeds the score buffer (max_model_len)")
-        staged = self._rows_staging.upload([
-            starts, lens, self._target_seq_lens[:batch_size], self._active_slots, [],
-        ])
+        # The rows and the key staged with this snapshot, unless the active
+        # slots changed since.
+        prepared, self._retrieval_rows = self._retrieval_rows, None
+        if prepared is not None and prepared[0] is self._active_slots:
+            staged, key = prepared[1], prepared[2]
+        else:
+            ends = self._target_query_ends[:batch_size]
+            starts = [0, *ends[:-1]]
+            lens = [e - s for s, e in zip(starts, ends)]
+            if max(self._target_seq_lens[:batch_size]) > self.max_chunks * self.settings.chunk_size:
+                raise ValueError("verifier length exceeds the score buffer (max_model_len)")
+            staged = self._rows_staging.upload([
+                starts, lens, self._target_seq_lens[:batch_size], self._active_slots, [],
+            ])
+            key = None
         # Whole staging rows serve any batch size (the kernels read the first
         # batch_size entries); int32 device counts are read where they are.
         counts = valid_sampled_token_count
@@ -471,8 +506,9 @@ class DiffSpecDraftCache:
         started = time.perf_counter()
         q, lse, kc, bt = self._target_query, self._target_lse, self._target_key_cache, self._target_block_tables
         stages = _step.SCORE | _step.SELECT
-        hit = self._step_descs.get(self._step_key(stages, batch_size, batch_size, self._cos_sin_cache(), q, lse, kc,
-                                                  bt))
+        if key is None:
+            key = self._step_key(stages, batch_size, batch_size, self._cos_sin_cache(), q, lse, kc, bt)
+        hit = self._step_descs.get(key)
         if hit is not None:
             # The descriptor validated for this layout (what _launch refreshes).
             desc, device = hit

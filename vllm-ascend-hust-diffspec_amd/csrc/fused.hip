@@ -92,6 +92,7 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kSelectors = 16;     // selecting workgroups (fewer when the batch has fewer rows)
 constexpr int kFusedKeys = 8192;   // candidate keys a selector keeps in LDS
 constexpr int kFusedRows = 256;    // batch rows per fused launch
+static_assert(kFusedRows <= kThreads, "the prologue loads one row per thread");
 // Fewer rows than this run the chain: the single launch gains by hiding
 // rows' selections and gathers behind other rows' scoring, and with a few
 // long rows the last selection dominates (measured: 4 rows of 128k tokens
@@ -424,19 +425,28 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
     const uint32_t t = (coherent_load(f.header + kEpoch) + 1u) & ~kSkipped;
     s_tag = t == 0u ? 1u : t;
   }
-  // Gather tasks of row r: its history length is at most
+  // One round of row loads serves both work lists (rows <= kThreads: thread
+  // r loads row r).  Gather tasks of row r: its history length is at most
   // min(committed - 1, pos_limit) (plan construction bounds it by the
-  // history end), so the task list is known before any plan exists.
+  // history end), so the task list is known before any plan exists.  The
+  // scoring workgroups also take row r's scored length and query row.
   const int ppw = 64 / ga.lanes_per_row;
-  build_row_prefix(rows, s_task_prefix, s_scratch, [&](int r) {
-    const int slot = f.p.slots[r];
-    if ((ga.row_active != nullptr && ga.row_active[r] == 0) || slot < 0 || slot >= ga.num_slots) return 0;
-    return (min(max(f.p.committed_lens[r] - 1, 0), ga.pos_limit) + ppw - 1) / ppw;
-  });
-  const uint32_t tag = s_tag;
   const int first_selector = static_cast<int>(gridDim.x) - f.selectors;
+  const bool selector = static_cast<int>(blockIdx.x) >= first_selector;
+  const int tr = static_cast<int>(threadIdx.x);
+  int row_tasks = 0;
+  RowDesc own{0, 0, 0};
+  if (tr < rows) {
+    const int slot = f.p.slots[tr];
+    const bool gathered = (ga.row_active == nullptr || ga.row_active[tr] != 0) && slot >= 0 && slot < ga.num_slots;
+    const int committed = f.p.committed_lens[tr];
+    if (!selector) own = row_desc(f.s.src, tr);
+    row_tasks = gathered ? (min(max(committed - 1, 0), ga.pos_limit) + ppw - 1) / ppw : 0;
+  }
+  build_row_prefix(rows, s_task_prefix, s_scratch, [&](int) { return row_tasks; });
+  const uint32_t tag = s_tag;
 
-  if (static_cast<int>(blockIdx.x) >= first_selector) {
+  if (selector) {
     const int s = static_cast<int>(blockIdx.x) - first_selector;
     for (int b = s; b < rows; b += f.selectors) select_row(f, b, tag, lds.sel);
     const gather::GatherLane L = gather::gather_lane<DT, NEOX>(ga);
@@ -446,10 +456,9 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
   } else {
     WorkShared& w = lds.w;
     const score::ScoreArgs& sa = f.s;
-    for (int r = threadIdx.x; r < rows; r += kThreads) {
-      const RowDesc d = row_desc(sa.src, r);
-      w.len[r] = d.active ? d.len : 0;
-      w.qrow[r] = static_cast<int>(d.qrow);
+    if (tr < rows) {
+      w.len[tr] = own.active ? own.len : 0;
+      w.qrow[tr] = static_cast<int>(own.qrow);
     }
     __syncthreads();
     build_row_prefix(rows, w.unit_prefix, w.scratch, [&](int r) { return (w.len[r] + sa.U - 1) / sa.U * sa.Hkv; });

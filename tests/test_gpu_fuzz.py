@@ -1,0 +1,59 @@
+"""GPU: seeded random batches through both implementations of the step.
+
+Each seed draws one batch shape from the ranges the reference's own tests
+span (tests/test_runtime.py, tests/test_retrieval_npu.py,
+tests/test_linear_attention_batch_npu.py): rows 8-24 (the single launch's
+range), ragged lengths from a few tokens to a few thousand, query lengths 1,
+2 or 4 with committed counts 0..qlen (rows with 0 keep the previous
+selection), graph padding rows, permuted slots among spare ones, chunk 16-64,
+token budget 512-1024, GQA groups 1-8, head_dim 64 or 128, page sizes 16-128,
+recent windows of one chunk or more, bf16 or fp16, neox or GPT-J rotation.
+The chain is compared with the oracle (scores to the relative bar, the rest
+bit-exact) and the single launch with the chain bit for bit.
+"""
+
+import random
+
+import pytest
+import torch
+
+from test_gpu_fused import _same
+from test_gpu_step import build_case, check_step, run_gpu
+
+pytestmark = pytest.mark.gpu
+
+
+def _draw(seed):
+    rnd = random.Random(1000 + seed)
+    rows = rnd.randint(8, 24)
+    pad = rnd.choice([0, 0, 3])
+    chunk = rnd.choice([16, 32, 64])
+    budget = rnd.choice([512, 1024])
+    hkv, group = rnd.choice([(1, 8), (2, 4), (4, 8), (4, 2), (8, 1)])
+    head_dim = rnd.choice([64, 128])
+    block = rnd.choice([16, 64, 128])
+    qlen = rnd.choice([1, 1, 2, 4])
+    lens = [rnd.randint(qlen + 1, 6000) for _ in range(rows)]
+    counts = [rnd.randint(0, qlen) if rnd.random() < 0.25 else rnd.randint(1, qlen) for _ in range(rows)]
+    num_slots = rows + rnd.randint(0, 6)
+    slots = rnd.sample(range(num_slots), rows)
+    window = rnd.choice([None, chunk, 4 * chunk, 256])
+    dtype = rnd.choice([torch.bfloat16, torch.float16])
+    neox = rnd.random() < 0.7
+    case = build_case(seed, real_rows=rows, pad_rows=pad, target_lens=lens, query_len=qlen, counts=counts,
+                      hq=hkv * group, hkv=hkv, head_dim=head_dim, chunk=chunk, token_budget=budget,
+                      block_size=block, lmax=max(lens) + 8, slots=slots, num_slots=num_slots, dtype=dtype,
+                      neox=neox)
+    label = (f"seed {seed}: rows {rows}+{pad}, qlen {qlen}, chunk {chunk}, budget {budget}, {group * hkv}/{hkv} "
+             f"heads x {head_dim}, block {block}, window {window}, {dtype}, {'neox' if neox else 'gptj'}")
+    return case, window, label
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_random_batches_chain_oracle_and_single_launch(cuda, seed):
+    case, window, label = _draw(seed)
+    print(label, flush=True)
+    chain = run_gpu(case, cuda, path="chain", recent_window=window)
+    check_step(case, chain, recent_window=window)
+    fused = run_gpu(case, cuda, path="fused", recent_window=window)
+    _same(chain, fused)

@@ -59,7 +59,7 @@ def path(request):
 
 
 def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="chain", single_launch=None,
-            lse_free=False, flags=0, expect_status=0):
+            lse_free=False, flags=0, expect_status=0, recent_window=None):
     from ds355 import step
 
     i32 = lambda xs: torch.tensor(xs, dtype=torch.int32, device=device)  # noqa: E731
@@ -100,7 +100,7 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="cha
         raw_key=state["raw_k"], raw_value=state["raw_v"], working_key=state["work_k"],
         working_value=state["work_v"], cos_sin_cache=state["cos_sin"], rotary_dim=case["head_dim"],
         is_neox_style=case["neox"], chunk_size=case["chunk"], history_budget=case["budget"],
-        row_active=None if row_active is None else i32(row_active),
+        recent_window=recent_window, row_active=None if row_active is None else i32(row_active),
         workspace=state.get("workspace") if fused else None,
         lse_partials=state.get("lse_partials") if lse_free else None,
         lse_out=state.get("lse_out") if lse_free else None, flags=flags,
@@ -117,7 +117,7 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="cha
     return state
 
 
-def check_step(case, state, *, previous=None, row_active=None):
+def check_step(case, state, *, previous=None, row_active=None, recent_window=None):
     chunk, budget = case["chunk"], case["budget"]
     real = case["real_rows"]
     rows_idx, q_index, lengths = O.retrieval_rows(case["counts"], case["ends"], case["tlens"], real)
@@ -147,7 +147,8 @@ def check_step(case, state, *, previous=None, row_active=None):
             assert state["plan"][b].abs().sum().item() == 0
             plans.append([0, 0, 0, 0, 0])
             continue
-        plans.append(O.history_plan(slot, selections.get(slot), max(0, case["committed"][b] - 1), chunk, budget))
+        plans.append(O.history_plan(slot, selections.get(slot), max(0, case["committed"][b] - 1), chunk, budget,
+                                    recent_window))
     expected_plan = O.pad_plan(plans, case["token_budget"], chunk)
     assert torch.equal(state["plan"].cpu(), expected_plan)
     # Working cache.

@@ -103,3 +103,35 @@ def assert_scores_close(actual: torch.Tensor, expected: torch.Tensor, rtol: floa
 
 __all__ = ["O", "gen", "randn", "rope_table_recipe", "paged_keys", "lse_for", "uniform_lengths",
            "max_ulp_bf16", "default_scale", "assert_scores_close", "SCORE_RTOL"]
+
+
+def attention_terms(q, work_k, work_v, slots, positions, scale) -> torch.Tensor:
+    """sum_t softmax(scale q.k_t) |v_t| per (row, query head, d) in fp32, over positions 0..p
+    of each row's slot in caches that already hold the new rows: the size of the terms a
+    draft-attention output sums, which bounds its arithmetic error."""
+    rows, hq, dim = q.shape
+    group = hq // work_k.shape[1]
+    out = torch.zeros((rows, hq, dim))
+    for r, (slot, pos) in enumerate(zip(slots, positions)):
+        k = work_k[slot, :, : pos + 1].float().repeat_interleave(group, dim=0)
+        v = work_v[slot, :, : pos + 1].float().abs().repeat_interleave(group, dim=0)
+        w = (torch.einsum("hd,hnd->hn", q[r].float(), k) * scale).softmax(-1)
+        out[r] = torch.einsum("hn,hnd->hd", w, v)
+    return out
+
+
+def assert_attention_close(actual: torch.Tensor, expected: torch.Tensor, terms: torch.Tensor) -> None:
+    """Each output within 2 ulps of its dtype of the oracle's fp32 result plus 2^-13 of its
+    summed terms (``attention_terms``).
+
+    The kernel multiplies V by the fp32 probabilities split into two 16-bit parts (within
+    about 2^-15 of the fp32 product) and accumulates in fp32 in another order than the
+    oracle, so an output that cancels to near zero carries the error of its terms.
+    """
+    rtol = 2 ** -7 if actual.dtype == torch.bfloat16 else 2 ** -10
+    a, e = actual.float(), expected.float()
+    assert torch.equal(a.isnan(), e.isnan())
+    excess = (a - e).abs() - (rtol * e.abs() + 2 ** -13 * terms)
+    worst = float(torch.nan_to_num(excess, nan=-1.0).max())
+    err = float(torch.nan_to_num((a - e).abs(), nan=0.0).max())
+    assert worst <= 0, f"output off by {worst:.3g} beyond the bound (max |error| {err:.3g})"

@@ -13,7 +13,7 @@ reference's own tolerance (rtol 0.03, atol 0.02) of its expectation.
 import pytest
 import torch
 
-from helpers import gen, randn
+from helpers import assert_attention_close, attention_terms, gen, randn
 from oracle import diffspec_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -24,38 +24,6 @@ REF_RTOL, REF_ATOL = 0.03, 0.02
 def _same_bits(a, b):
     assert torch.equal(a.isnan(), b.isnan())
     assert torch.equal(torch.nan_to_num(a), torch.nan_to_num(b))
-
-
-def _weighted_abs_v(q, work_k, work_v, slots, positions, scale):
-    """sum_t softmax(scale q.k_t) |v_t| per (row, query head, d) in fp32: the size of the
-    terms the output sums, which bounds its arithmetic error (outputs that cancel to near
-    zero carry the error of their terms, not of their value)."""
-    rows, hq, dim = q.shape
-    group = hq // work_k.shape[1]
-    out = torch.zeros((rows, hq, dim))
-    for r, (slot, pos) in enumerate(zip(slots, positions)):
-        k = work_k[slot, :, : pos + 1].float().repeat_interleave(group, dim=0)
-        v = work_v[slot, :, : pos + 1].float().abs().repeat_interleave(group, dim=0)
-        w = (torch.einsum("hd,hnd->hn", q[r].float(), k) * scale).softmax(-1)
-        out[r] = torch.einsum("hn,hnd->hd", w, v)
-    return out
-
-
-def _output_close(actual, expected, terms):
-    """One rounding of the output dtype (2 ulps of slack) plus 2^-13 of the summed terms.
-
-    The kernel multiplies V by the fp32 probabilities split into two 16-bit parts (the
-    product is within about 2^-15 of the fp32 one) and accumulates in fp32 in another
-    order than the oracle, so an output's error scales with sum_t w_t |v_t| (``terms``).
-    """
-    rtol = 2 ** -7 if actual.dtype == torch.bfloat16 else 2 ** -10
-    a, e = actual.float(), expected.float()
-    bound = rtol * e.abs() + 2 ** -13 * terms
-    excess = (a - e).abs() - bound
-    assert torch.equal(a.isnan(), e.isnan())
-    worst = torch.nan_to_num(excess, nan=-1.0).max()
-    err = float((a - e).abs().max())
-    assert worst <= 0, f"output off by {float(worst):.3g} beyond the bound (max |error| {err:.3g})"
 
 
 class Case:
@@ -112,8 +80,8 @@ def _step(case, dev, cuda, slots, positions, tokens, scale, device_positions=Fal
     torch.cuda.synchronize()
     actual = out.cpu()
     rows = len(slots)
-    terms = _weighted_abs_v(q[:rows], case.work_k, case.work_v, slots, host_pos, scale)
-    _output_close(actual[:rows], expected[:rows], terms)
+    terms = attention_terms(q[:rows], case.work_k, case.work_v, slots, host_pos, scale)
+    assert_attention_close(actual[:rows], expected[:rows], terms)
     assert actual[rows:].count_nonzero() == 0
     _same_bits(dev.k.cpu(), case.work_k)
     _same_bits(dev.v.cpu(), case.work_v)
@@ -218,8 +186,8 @@ def test_out_of_range_position_zeroes_the_row_and_sets_status(cuda):
     O.draft_linear_attention(q[[0, 2]], k[[0, 2]], v[[0, 2]], 0.1, expected[:2], case.work_k, case.work_v, lens,
                              [0, 2], [40, 42])
     actual = out.cpu()
-    terms = _weighted_abs_v(q[[0, 2]], case.work_k, case.work_v, [0, 2], [40, 42], 0.1)
-    _output_close(actual[[0, 2]], expected[:2], terms)
+    terms = attention_terms(q[[0, 2]], case.work_k, case.work_v, [0, 2], [40, 42], 0.1)
+    assert_attention_close(actual[[0, 2]], expected[:2], terms)
     assert actual[1].count_nonzero() == 0
     assert dev.lens.cpu().tolist() == [41, 41, 43]
     _same_bits(dev.k.cpu(), case.work_k)
@@ -268,8 +236,8 @@ def test_runtime_forward_attention_after_compact_prefill(cuda):
         assert not cache.has_pending_attention()
         torch.cuda.synchronize()
         terms = torch.zeros((4, 8, 128))
-        terms[: len(slots)] = _weighted_abs_v(q[: len(slots)], work_k, work_v, slots, positions, 0.088)
-        _output_close(out.view(4, 8, 128).cpu(), expected, terms)
+        terms[: len(slots)] = attention_terms(q[: len(slots)], work_k, work_v, slots, positions, 0.088)
+        assert_attention_close(out.view(4, 8, 128).cpu(), expected, terms)
         assert cache.working_lens.cpu().tolist() == lens
         _same_bits(cache.working_key.cpu(), work_k)
         _same_bits(cache.working_value.cpu(), work_v)

@@ -14,7 +14,7 @@ from types import SimpleNamespace
 import pytest
 import torch
 
-from helpers import gen, randn
+from helpers import assert_attention_close, attention_terms, gen, randn
 from oracle import diffspec_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -213,7 +213,9 @@ def test_draft_cycle_capture_attention_against_oracle(cuda):
         O.draft_linear_attention(q, key.view(4, heads, d), value.view(4, heads, d), d ** -0.5, expected, work_k,
                                  work_v, lens, slots, local)
         torch.cuda.synchronize()
-        torch.testing.assert_close(out.cpu().float(), expected.float(), rtol=2 ** -7, atol=1e-5)
+        terms = torch.zeros((4, hq, d))
+        terms[: len(slots)] = attention_terms(q[: len(slots)], work_k, work_v, slots, local, d ** -0.5)
+        assert_attention_close(out.cpu(), expected, terms)
         assert torch.equal(cache.raw_key.cpu(), raw_k) and torch.equal(cache.raw_value.cpu(), raw_v)
         assert cache.working_lens.cpu().tolist() == lens
     cache.end_cycle()

@@ -15,7 +15,7 @@ working lengths, slots and the workspaces' epochs are read on the device.
 import pytest
 import torch
 
-from helpers import gen, randn
+from helpers import assert_attention_close, attention_terms, gen, randn
 from oracle import diffspec_oracle as O
 from test_gpu_step import build_case, check_step
 
@@ -94,7 +94,8 @@ def test_draft_steps_replayed_from_a_graph(cuda):
         expected = torch.empty((rows, hq, d), dtype=dt)
         O.draft_linear_attention(q[:rows].cpu(), k[:rows].cpu(), v[:rows].cpu(), d ** -0.5, expected, host_k, host_v,
                                  host_lens, s, pos)
-        torch.testing.assert_close(graphed["out"][:rows].cpu().float(), expected.float(), rtol=2 ** -7, atol=1e-5)
+        terms = attention_terms(q[:rows].cpu(), host_k, host_v, s, pos, d ** -0.5)
+        assert_attention_close(graphed["out"][:rows].cpu(), expected, terms)
         assert graphed["lens"].cpu().tolist() == host_lens
         assert graphed["rope"][:rows].cpu().tolist() == pos
         for r, x in enumerate(s):

@@ -9,7 +9,9 @@ selection), graph padding rows, permuted slots among spare ones, chunk 16-64,
 token budget 512-1024, GQA groups 1-8, head_dim 64 or 128, page sizes 16-128,
 recent windows of one chunk or more, bf16 or fp16, neox or GPT-J rotation.
 The chain is compared with the oracle (scores to the relative bar, the rest
-bit-exact) and the single launch with the chain bit for bit.
+bit-exact), the single launch with the chain bit for bit, and the compact
+prefill alone (plan + gather in one launch, from the chain's selections) with
+the chain's plans and working caches bit for bit.
 """
 
 import random
@@ -57,3 +59,17 @@ def test_random_batches_chain_oracle_and_single_launch(cuda, seed):
     check_step(case, chain, recent_window=window)
     fused = run_gpu(case, cuda, path="fused", recent_window=window)
     _same(chain, fused)
+    # The compact prefill alone (plan + gather in one launch) from the chain's selections.
+    from ds355 import step
+
+    prefill = dict(chain)
+    prefill.update(plan=torch.zeros_like(chain["plan"]), working_lens=torch.zeros_like(chain["working_lens"]),
+                   work_k=torch.full_like(chain["work_k"], float("nan")),
+                   work_v=torch.full_like(chain["work_v"], float("nan")),
+                   sel_ids=chain["sel_ids"].clone(), sel_count=chain["sel_count"].clone())
+    run_gpu(case, cuda, stages=step.PLAN, state=prefill, recent_window=window)
+    for key in ("plan", "working_lens", "work_k", "work_v"):
+        x, y = chain[key], prefill[key]
+        if x.dtype.is_floating_point:
+            x, y = torch.nan_to_num(x), torch.nan_to_num(y)
+        assert torch.equal(x, y), key

@@ -231,8 +231,8 @@ typedef struct ds_step_desc {
  * ds_step_desc.flags, for tests of the single launch's rare paths; 0 in
  * normal use.
  *   DS_STEP_SELECTORS_GATHER: the scoring waves leave every gather task to
- *     the selecting workgroups, the path a task takes when its scoring wave
- *     gave up waiting for the plan.  Same results, slower.
+ *     the last workgroup to finish, the path a task takes when its scoring
+ *     wave gave up waiting for the plan.  Same results, slower.
  *   DS_STEP_EXPIRE_WAITS: every selector reports an expired wait (status
  *     bit 0), so the launch's bounded waits stop early and its results are
  *     not valid; every wave still finishes.  Tests that one launch's expiry
@@ -246,7 +246,7 @@ int ds_retrieval_step(ds_stream_t stream, const ds_step_desc* desc);
  * Workspace of the single-launch step for these buffer sizes (0 when one of
  * them is not positive).  No reference counterpart: it holds the stages'
  * hand-over state (64 header bytes; a tagged copy of each plan row, 128
- * 8-byte columns per row; a 4-byte state per gather task,
+ * 8-byte columns per row; a 4-byte skip mark per gather task,
  * ceil(token_budget / 8) per row, rounded up to 256 bytes; tagged score
  * partials [batch_rows, max_chunks, num_kv_heads] x 8 bytes).  A workspace
  * serves one launch at a time.  Word 2 of its header is the owner's status

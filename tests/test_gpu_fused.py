@@ -101,8 +101,9 @@ def test_fused_fp16_and_gptj(cuda, dtype, neox, head_dim):
 def test_selectors_gather_every_task(cuda):
     """The recovery path of the single launch, for every gather task: a scoring
     wave that stops waiting for its row's plan marks the task skipped and the
-    row's selector does it.  Forced from the host (no scorer waits at all);
-    the bytes equal the chain's and the status stays 0."""
+    last workgroup to finish does it.  Forced from the host (no scorer waits
+    at all); the bytes equal the chain's and the status stays 0.  The next
+    launch on the same workspace, without the flag, finds no stale skips."""
     from ds355 import step
 
     case = _ragged(17, 12, 1000, 20000)
@@ -110,6 +111,11 @@ def test_selectors_gather_every_task(cuda):
     fused = run_gpu(case, cuda, path="fused", flags=step.SELECTORS_GATHER)
     _same(chain, fused)
     check_step(case, fused)
+    for key in ("work_k", "work_v"):
+        fused[key].fill_(float("nan"))
+    fused["sel_count"].fill_(-1)
+    run_gpu(case, cuda, state=fused, path="fused")
+    _same(chain, fused)
 
 
 def test_expired_wait_stays_with_its_launch(cuda):

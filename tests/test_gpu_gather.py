@@ -226,3 +226,72 @@ def test_validation_messages_match_reference(cuda):
     with pytest.raises(ValueError, match="KV plan must be a contiguous 2-D int64"):
         rebuild_compact_kv_from_plan(k, k, w, w, plan.int(), cs, chunk_size=2, max_width=4, rotary_dim=16,
                                      is_neox_style=True)
+
+
+def _special_keys(g, n, heads, dim, cos_sin, rot):
+    """bf16 keys that probe the rotation's rounding: ordinary values, signed
+    zeros, NaN and infinities, values near the top of the range, tiny normal
+    values, near-cancelling pairs (x1*c ~ x2*s) and a wide exponent spread."""
+    x = torch.randn((n, heads, dim), generator=g)
+    kind = torch.arange(n) % 8
+    half = rot // 2
+    sign = torch.where(torch.rand((n, heads, dim), generator=g) < 0.5, -1.0, 1.0)
+    for p in range(n):
+        k = int(kind[p])
+        if k == 1:
+            x[p][torch.rand((heads, dim), generator=g) < 0.5] = 0.0
+            x[p] *= sign[p]
+        elif k == 2:
+            pick = torch.randint(0, 4, (heads, dim), generator=g)
+            x[p][pick == 1] = float("nan")
+            x[p][pick == 2] = float("inf")
+            x[p][pick == 3] = float("-inf")
+        elif k == 3:
+            x[p] = sign[p] * torch.empty((heads, dim)).uniform_(1e37, 3.3e38, generator=g)
+        elif k == 4:
+            x[p] = sign[p] * torch.empty((heads, dim)).uniform_(1e-30, 1e-28, generator=g)
+        elif k == 5:
+            c = cos_sin[p, :half].float()
+            s = cos_sin[p, half:rot].float()
+            first = x[p, :, :half].to(torch.bfloat16).float()
+            ok = s.abs() > 1e-3
+            second = torch.where(ok, first * c / torch.where(ok, s, torch.ones_like(s)), x[p, :, half:rot])
+            x[p, :, half:rot] = second
+        elif k == 7:
+            x[p] = sign[p] * torch.exp2(torch.empty((heads, dim)).uniform_(-60, 60, generator=g))
+    return x.to(torch.bfloat16)
+
+
+def test_rotation_special_values_bit_exact(cuda):
+    """Every rotated word that is not a NaN equals the oracle's bit for bit
+    (signed zeros included), and NaNs sit in the same places, for neox and
+    GPT-J pairs, on keys built to probe the fp32 rotation's rounding
+    (_special_keys).  NaN payloads are not compared: the oracle's conversion
+    keeps whatever NaN bits the host CPU produced, the kernel writes 0x7fc0."""
+    from ds355.compact_kv import rebuild_compact_kv_from_plan
+
+    chunk, token_budget, heads, dim, n = 64, 2048, 4, 128, 512
+    budget = O.history_budget(token_budget, 4, chunk)
+    g = gen(29)
+    cos_sin = O.rope_cos_sin_cache(dim, token_budget)
+    for neox in (True, False):
+        raw_k = _special_keys(g, n + 1, heads, dim, cos_sin, dim).unsqueeze(0)
+        raw_v = randn((1, n + 1, heads, dim), torch.bfloat16, g)
+        plan = O.pad_plan([O.history_plan(0, None, n, chunk, budget)], token_budget, chunk)
+        width = int(plan[0, 1])
+        exp_k = torch.zeros((1, heads, token_budget, dim), dtype=torch.bfloat16)
+        exp_v = exp_k.clone()
+        O.rebuild_compact_kv_from_plan(raw_k, raw_v, exp_k, exp_v, plan, cos_sin, chunk_size=chunk,
+                                       max_width=width, rotary_dim=dim, is_neox_style=neox)
+        work_k = torch.zeros_like(exp_k).to(cuda)
+        work_v = torch.zeros_like(exp_v).to(cuda)
+        rebuild_compact_kv_from_plan(raw_k.to(cuda), raw_v.to(cuda), work_k, work_v, plan.to(cuda),
+                                     cos_sin.to(cuda), chunk_size=chunk, max_width=width, rotary_dim=dim,
+                                     is_neox_style=neox)
+        got_nan, want_nan = work_k.cpu().isnan(), exp_k.isnan()
+        assert torch.equal(got_nan, want_nan), neox
+        got = work_k.cpu().view(torch.int16).masked_fill(got_nan, 0)
+        want = exp_k.view(torch.int16).masked_fill(want_nan, 0)
+        bad = (got != want).nonzero()
+        assert bad.numel() == 0, (neox, bad[:8].tolist(), got[tuple(bad[0])].item(), want[tuple(bad[0])].item())
+        assert torch.equal(work_v.cpu().view(torch.int16), exp_v.view(torch.int16))

@@ -10,8 +10,7 @@
 //     gather tasks, (row, ppw local positions) numbered row-major and dealt
 //     round-robin, each once its row's plan is published;
 //   - the last S workgroups select: selector s takes rows s, s + S, ... in
-//     order, publishes each row's plan, and finally makes sure every gather
-//     task of its rows has been done.
+//     order and publishes each row's plan.
 //
 // Hand-over is by value through device-scope (coherent) accesses, with no
 // cache write-back on either side:
@@ -26,8 +25,8 @@
 //     wave-wide load (lane l, columns l and 64 + l): it is valid once every
 //     column carries the tag, so no flag, and no wait for the stores to
 //     complete, stands between a plan and its gathers;
-//   - after each gather task its wave stores state[row][task] = tag (done),
-//     or tag | kSkipped when it gave up waiting for the plan.
+//   - a wave that gave up waiting for a plan stores state[row][task] =
+//     tag | kSkipped for each task it left, and sets the launch's skip word.
 // Polling is the costly part of this design: every poll is a device-scope
 // request to one memory channel, and thousands of waves polling one line
 // slow every stream that shares the channel.  So each row's tagged plan has
@@ -37,11 +36,11 @@
 // Forward progress does not depend on all workgroups being resident at once
 // (the launch is an ordinary one).  Workgroups are dispatched in index order
 // on each XCD, and a workgroup waits without a deadline only on lower-indexed
-// ones: selectors on scorers (partials, task states) and on nobody else.
-// Scorers wait for plans, held by higher-indexed selectors, only up to
-// kOwnerSpins polls; a task they give up on is marked skipped and redone by
-// the row's selector.  A gather task writes fixed bytes that depend only on
-// the published plan, so doing one twice is harmless.  The waits without a
+// ones: selectors on scorers (partials) and on nobody else.  Scorers wait
+// for plans, held by higher-indexed selectors, only up to kOwnerSpins polls;
+// a task they give up on is marked skipped and redone by the last workgroup
+// to finish, when every plan is published.  A gather task writes fixed bytes
+// that depend only on the published plan, so doing one twice is harmless.  The waits without a
 // deadline still end after kSpinLimit polls (then a status bit is set and
 // the results are not valid), so every wave of the launch finishes.
 //
@@ -57,9 +56,9 @@
 // launch's expiry never shortens the waits of the next.
 //
 // Workspace (zero-filled once by its owner; one launch at a time):
-//   uint32 header[16]               epoch, done counter, status, launch status
+//   uint32 header[16]               epoch, done counter, status, launch status, skips
 //   uint64 plans[rows][kPlanCols]   tagged plan copies
-//   uint32 state[rows][task_cap]    gather task done / skipped
+//   uint32 state[rows][task_cap]    gather tasks skipped by their scoring wave
 //   uint64 partials[rows, max_chunks, Hkv]
 #include "gather_body.h"
 #include "score_body.h"
@@ -107,7 +106,7 @@ constexpr uint32_t kOwnerSpins = 1u << 12;  // polls before a scorer leaves a ta
 constexpr uint32_t kSkipped = 0x80000000u;
 constexpr int kSleep = 8;          // s_sleep units (64 cycles each) between polls
 
-enum { kEpoch = 0, kDone = 1, kStatus = 2, kLaunchStatus = 3, kHeaderWords = 16 };
+enum { kEpoch = 0, kDone = 1, kStatus = 2, kLaunchStatus = 3, kSkips = 4, kHeaderWords = 16 };
 enum { kStatusPartials = 1u, kStatusTasks = 2u };
 constexpr int kLine = 256;
 constexpr int kPlanCols = 128;     // tagged plan columns per row (plan_width <= 128)
@@ -332,7 +331,10 @@ __device__ __forceinline__ void run_task(const gather::GatherArgs& ga, const gat
 // A scoring wave's gather tasks: task numbers gw, gw + tw, ... of the
 // row-major numbering in task_prefix (exclusive prefix of the rows' task
 // counts).  Each waits for its row's plan at most kOwnerSpins polls; a task
-// whose plan did not come in time is marked skipped for the selector.
+// whose plan did not come in time is marked skipped, and the launch's skip
+// word is set, for the last workgroup to finish.  Both writes are
+// read-modify-writes the wave waits for, so they are in memory before its
+// workgroup counts itself done.
 template <int DT, bool NEOX>
 __device__ __forceinline__ void gather_owned(const FusedArgs& f, const int* task_prefix, int gw, int tw,
                                              uint32_t tag) {
@@ -356,47 +358,51 @@ __device__ __forceinline__ void gather_owned(const FusedArgs& f, const int* task
       published = poll_plan(f, r, tag, f.owner_spins, v);
     }
     const int t = __builtin_amdgcn_readfirstlane(task - task_prefix[r]);
-    if (published) run_task<DT, NEOX>(ga, L, v, t);
-    if ((threadIdx.x & 63) == 0) {
-      coherent_store(f.state + static_cast<int64_t>(r) * f.task_cap + t, published ? tag : (tag | kSkipped));
+    if (published) {
+      run_task<DT, NEOX>(ga, L, v, t);
+    } else if ((threadIdx.x & 63) == 0) {
+      __hip_atomic_exchange(f.state + static_cast<int64_t>(r) * f.task_cap + t, tag | kSkipped, __ATOMIC_ACQUIRE,
+                            __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_exchange(f.header + kSkips, tag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
 
-// A selector's last duty: every gather task of row b is done or skipped by
-// its scoring wave (lower-indexed workgroups); skipped ones are done here.
-// Each wave checks 64 tasks at a time.
+// The gather tasks their scoring waves skipped, done by the last workgroup
+// to finish: every other workgroup has counted itself done, so every plan is
+// published and every skip mark is in memory.  Each wave checks 64 tasks of
+// a row at a time.  A bit a wait raises here goes straight to the owner's
+// words, since the launch's status word has already been handed over.
 template <int DT, bool NEOX>
-__device__ __forceinline__ void finish_row_tasks(const FusedArgs& f, const gather::GatherLane& L, int b, int tasks,
-                                                 uint32_t tag) {
+__device__ __forceinline__ void redo_skipped(const FusedArgs& f, const int* task_prefix, uint32_t tag) {
   const int lane = threadIdx.x & 63;
-  const uint32_t* st = f.state + static_cast<int64_t>(b) * f.task_cap;
-  bool have_plan = false;
-  PlanView v{};
-  for (int t0 = static_cast<int>(threadIdx.x >> 6) * 64; t0 < tasks; t0 += kThreads) {
-    const int t = t0 + lane;
-    uint32_t s = 0;
-    for (uint32_t spin = 0;; ++spin) {
-      s = t < tasks ? coherent_load(st + t) : tag;
-      if (__ballot((s & ~kSkipped) != tag) == 0) break;
-      if (give_up(spin, f.header)) {
-        raise_status(f.header, kStatusTasks);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(kSleep);
-    }
-    uint64_t skipped = __ballot(t < tasks && s == (tag | kSkipped));
-    while (skipped != 0) {
-      const int k = __builtin_ctzll(skipped);
-      skipped &= skipped - 1;
-      if (!have_plan) {
-        have_plan = poll_plan(f, b, tag, kSpinLimit, v);  // published by this workgroup
+  const gather::GatherLane L = gather::gather_lane<DT, NEOX>(f.g);
+  for (int b = 0; b < f.p.batch; ++b) {
+    const int tasks = task_prefix[b + 1] - task_prefix[b];
+    const uint32_t* st = f.state + static_cast<int64_t>(b) * f.task_cap;
+    bool have_plan = false;
+    PlanView v{};
+    for (int t0 = static_cast<int>(threadIdx.x >> 6) * 64; t0 < tasks; t0 += kThreads) {
+      const int t = t0 + lane;
+      const uint32_t s = t < tasks ? coherent_load(st + t) : 0u;
+      uint64_t skipped = __ballot(s == (tag | kSkipped));
+      while (skipped != 0) {
+        const int k = __builtin_ctzll(skipped);
+        skipped &= skipped - 1;
         if (!have_plan) {
-          raise_status(f.header, kStatusTasks);
-          break;
+          have_plan = poll_plan(f, b, tag, kSpinLimit, v);
+          if (!have_plan) {
+            if (lane == 0) {
+              __hip_atomic_fetch_or(f.header + kStatus, kStatusTasks, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              if (f.status_out != nullptr) {
+                __hip_atomic_fetch_or(f.status_out, kStatusTasks, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              }
+            }
+            break;
+          }
         }
+        run_task<DT, NEOX>(f.g, L, v, t0 + k);
       }
-      run_task<DT, NEOX>(f.g, L, v, t0 + k);
     }
   }
 }
@@ -418,6 +424,7 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
   __shared__ int s_task_prefix[kFusedRows + 1];
   __shared__ int s_scratch[4];
   __shared__ uint32_t s_tag;
+  __shared__ uint32_t s_last;
 
   const int rows = f.p.batch;
   const gather::GatherArgs& ga = f.g;
@@ -449,10 +456,6 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
   if (selector) {
     const int s = static_cast<int>(blockIdx.x) - first_selector;
     for (int b = s; b < rows; b += f.selectors) select_row(f, b, tag, lds.sel);
-    const gather::GatherLane L = gather::gather_lane<DT, NEOX>(ga);
-    for (int b = s; b < rows; b += f.selectors) {
-      finish_row_tasks<DT, NEOX>(f, L, b, s_task_prefix[b + 1] - s_task_prefix[b], tag);
-    }
   } else {
     WorkShared& w = lds.w;
     const score::ScoreArgs& sa = f.s;
@@ -471,23 +474,38 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
   }
 
   // The last workgroup to finish hands this launch's status bits to the
-  // owner's word, clears them for the next launch and publishes the tag as
-  // the epoch.  Every raise of a workgroup has returned before that
-  // workgroup's count (the barrier below orders them), so the last count
-  // comes after every raise.  The atomics are relaxed: a release here would
-  // write back the XCD's L2 in every workgroup.
+  // owner's word, clears them for the next launch, redoes the gather tasks
+  // their scoring waves skipped, and publishes the tag as the epoch.  Every
+  // raise and skip mark of a workgroup has returned before that workgroup's
+  // count (the barrier below orders them), so the last count comes after all
+  // of them.  The atomics are relaxed: a release here would write back the
+  // XCD's L2 in every workgroup.
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t prev = __hip_atomic_fetch_add(f.header + kDone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t last = 0u;
     if (prev == gridDim.x - 1) {
       const uint32_t bits =
           __hip_atomic_exchange(f.header + kLaunchStatus, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t skips = __hip_atomic_exchange(f.header + kSkips, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (bits != 0u) {
         __hip_atomic_fetch_or(f.header + kStatus, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (f.status_out != nullptr) {
           __hip_atomic_fetch_or(f.status_out, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
+      last = skips == tag ? 3u : 1u;
+      if (last == 1u) {
+        coherent_store(f.header + kDone, 0u);
+        coherent_store(f.header + kEpoch, tag);
+      }
+    }
+    s_last = last;
+  }
+  __syncthreads();
+  if (s_last == 3u) {
+    redo_skipped<DT, NEOX>(f, s_task_prefix, tag);
+    if (threadIdx.x == 0) {
       coherent_store(f.header + kDone, 0u);
       coherent_store(f.header + kEpoch, tag);
     }

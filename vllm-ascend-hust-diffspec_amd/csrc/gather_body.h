@@ -81,6 +81,32 @@ __device__ __forceinline__ void rotate_pair(float x1, float x2, float c, float s
   o2 = d + e;
 }
 
+// The same rotation for bf16 values with one fused multiply-add per output:
+// o1 = fma(x1, c, -(x2 * s)), o2 = fma(x1, s, x2 * c).  A product of two
+// bf16 values has at most 16 significant bits, so it is exact in fp32
+// unless it is nonzero and below fp32's smallest normal, 2^-126 (a key
+// below 2^-100 against a table value below 2^-26, far from any model's
+// keys).  Then x1 * c and x2 * s need no rounding, and the fma rounds the
+// same exact sum once, as the oracle's subtraction does, signed zeros
+// included (IEEE fma: a zero sum is -0 only when both terms are -0).
+__device__ __forceinline__ void rotate_pair_bf16(float x1, float x2, float c, float s, float& o1, float& o2) {
+  o1 = __builtin_fmaf(x1, c, -(x2 * s));
+  o2 = __builtin_fmaf(x1, s, x2 * c);
+}
+// bf16 halves of a word widened to fp32.
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+// Two fp32 values rounded to bf16 (round to nearest even, v_cvt_pk_bf16_f32)
+// and packed lo | hi << 16; NaN becomes 0x7fc0, the oracle's rule.
+typedef __bf16 BF2 __attribute__((ext_vector_type(2)));
+typedef float F2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  lo = lo == lo ? lo : __uint_as_float(0x7fc00000u);
+  hi = hi == hi ? hi : __uint_as_float(0x7fc00000u);
+  const F2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, BF2));
+}
+
 // 16-byte and 8-byte vectors carried as 32-bit words.  Native vector types
 // (not arrays in a struct) keep arrays of them in registers.
 typedef uint32_t W4 __attribute__((ext_vector_type(4)));
@@ -276,7 +302,44 @@ __device__ __forceinline__ void gather_task(const GatherArgs& a, const GatherLan
     for (int u = 0; u < HG; ++u) {
       if (h0 + u >= H) break;  // wave-uniform
       W4 ok0 = k0[u], ok1 = k1[u];
-      if (NEOX) {
+      if constexpr (DT == DS_BF16) {
+        if (NEOX) {
+          // Word w of k0 / k1 holds x1 / x2 of elements 2w and 2w + 1.
+          if (rot0) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              float a0, a1, b0, b1;
+              rotate_pair_bf16(bf16_lo(k0[u][w]), bf16_lo(k1[u][w]), bf16_lo(c16[w]), bf16_lo(s16[w]), a0, b0);
+              rotate_pair_bf16(bf16_hi(k0[u][w]), bf16_hi(k1[u][w]), bf16_hi(c16[w]), bf16_hi(s16[w]), a1, b1);
+              ok0[w] = pack_bf16(a0, a1);
+              ok1[w] = pack_bf16(b0, b1);
+            }
+          }
+        } else {
+          // Word e holds the pair (x1, x2); its cos/sin are element e of the
+          // 8-byte table vectors.
+          if (rot0) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t c = c8a[e >> 1], sn = s8a[e >> 1];
+              float o1, o2;
+              rotate_pair_bf16(bf16_lo(k0[u][e]), bf16_hi(k0[u][e]), (e & 1) ? bf16_hi(c) : bf16_lo(c),
+                               (e & 1) ? bf16_hi(sn) : bf16_lo(sn), o1, o2);
+              ok0[e] = pack_bf16(o1, o2);
+            }
+          }
+          if (rot1) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const uint32_t c = c8b[e >> 1], sn = s8b[e >> 1];
+              float o1, o2;
+              rotate_pair_bf16(bf16_lo(k1[u][e]), bf16_hi(k1[u][e]), (e & 1) ? bf16_hi(c) : bf16_lo(c),
+                               (e & 1) ? bf16_hi(sn) : bf16_lo(sn), o1, o2);
+              ok1[e] = pack_bf16(o1, o2);
+            }
+          }
+        }
+      } else if (NEOX) {
         if (rot0) {
           float f1[V], f2[V];
 #pragma unroll

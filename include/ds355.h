@@ -168,7 +168,28 @@ int ds_rebuild_compact_kv(ds_stream_t stream, int dtype,
  * 8 to 256 batch rows, 16-token-aligned pages) run as one launch with the
  * same results.
  */
-enum ds_stage { DS_STAGE_SCORE = 1, DS_STAGE_SELECT = 2, DS_STAGE_PLAN = 4, DS_STAGE_ALL = 7 };
+enum ds_stage { DS_STAGE_SCORE = 1, DS_STAGE_SELECT = 2, DS_STAGE_PLAN = 4, DS_STAGE_ALL = 7, DS_STAGE_PREFIX = 8 };
+
+/*
+ * DS_STAGE_PREFIX (in place of DS_STAGE_PLAN): plan rows and working_lens as
+ * DS_STAGE_PLAN writes them, but only the gather tasks wholly inside each
+ * row's history prefix, the positions before the rolling tail, are moved.
+ * Those read raw rows well before the committed root, which the draft's
+ * prefill does not rewrite, so the retrieval call can move them before
+ * populate_prefill and the compact prefill then moves only the rest.  Needs
+ * gather records (below).  SCORE | SELECT | PREFIX with a workspace runs as
+ * the single launch.
+ *
+ * Gather records (sel_gen and gather_rec, both or neither): per slot, the
+ * selection generation, which every stored selection increments (the caller
+ * increments it too when a different request takes the slot), and per
+ * (slot, gather task of the plan's local positions) what the working cache
+ * holds: (generation << 32) | (prefix drop + 1) for a task wholly inside the
+ * history prefix, else 0.  A PLAN or PREFIX gather leaves out every task
+ * whose record already matches the plan, since its bytes would not change,
+ * and keeps the records.  Raw rows before a request's committed root must
+ * not change while the request holds its slot.  Zero-filled by the owner.
+ */
 
 typedef struct ds_step_desc {
   /* verifier snapshot (scoring) */
@@ -225,6 +246,10 @@ typedef struct ds_step_desc {
   float* lse_out;                    /* [batch_rows, Hq] natural-log LSE of each scored row; required when lse == NULL */
   int64_t lse_out_stride;            /* elements between rows of lse_out */
   int flags;                         /* DS_STEP_* bits; 0 for normal use */
+  /* gather records (see DS_STAGE_PREFIX), or both NULL */
+  int32_t* sel_gen;                  /* [num_slots] selection generations     */
+  uint64_t* gather_rec;              /* [num_slots, rec_stride], rec_stride >= token_budget */
+  int64_t rec_stride;
 } ds_step_desc;
 
 /*

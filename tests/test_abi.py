@@ -26,7 +26,7 @@ def _step_desc_fields():
         decl = " ".join(decl.split())
         if not decl:
             continue
-        m = re.match(r"(const )?(int64_t|int32_t|int|float|void|size_t)\s*(\*?)\s*(.*)", decl)
+        m = re.match(r"(const )?(int64_t|uint64_t|int32_t|int|float|void|size_t)\s*(\*?)\s*(.*)", decl)
         assert m, decl
         kind = "ptr" if m.group(3) else m.group(2)
         for name in m.group(4).split(","):
@@ -105,7 +105,7 @@ def test_c_side_validation_reports_reference_messages():
     assert rc == _lib.DS_ERR_INVALID
     assert lib.ds_last_error().decode() == "token_budget must be a positive chunk-size multiple"
     desc = _lib.StepDesc()
-    desc.stages = 8
+    desc.stages = 16
     assert lib.ds_retrieval_step(None, desc) == _lib.DS_ERR_INVALID
     assert "unknown stage bits" in lib.ds_last_error().decode()
 

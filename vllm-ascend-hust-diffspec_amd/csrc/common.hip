@@ -50,4 +50,4 @@ int device_cu_count() {
 
 extern "C" const char* ds_last_error(void) { return ds355::g_error; }
 
-extern "C" int ds_abi_version(void) { return 6; }
+extern "C" int ds_abi_version(void) { return 7; }

@@ -136,6 +136,14 @@ __device__ __forceinline__ void coherent_store(T* p, T v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// A wave-uniform 64-bit value made scalar (both halves through readfirstlane).
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint64_t u = static_cast<uint64_t>(v);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 // Workgroup barrier for LDS hand-offs only.  Unlike __syncthreads it does
 // not wait for the wave's outstanding global loads, stores and atomics, which
 // the other waves of the workgroup do not read.

@@ -124,7 +124,14 @@ struct FusedArgs {
   uint32_t owner_spins;  // polls a scorer waits for a plan (0: every task goes to the selectors)
   int expire;            // test flag: every selector raises kStatusPartials as if a wait had expired
   uint32_t* status_out;  // optional caller word that also receives the launch's status bits
+  int32_t* gen;          // [num_slots] selection generations, or nullptr (no gather records)
+  uint64_t* rec;         // [num_slots, rec_stride] gather records (gather_body.h), or nullptr
+  int64_t rec_stride;
+  int prefix_only;       // gather only the tasks wholly in each row's history prefix
 };
+// With gather records, the tagged plan copy carries the slot's selection
+// generation in its last column (plan_width < kPlanCols then).
+constexpr int kGenCol = 127;
 
 // The read-modify-write completes before the thread goes on (acquire: the
 // wave waits for its return), so the bit is in memory before the workgroup
@@ -138,12 +145,6 @@ __device__ __forceinline__ bool give_up(uint32_t spin, const uint32_t* header) {
   return spin >= kSpinLimit ||
          (spin % kStatusEvery == kStatusEvery - 1 &&
           __builtin_amdgcn_readfirstlane(coherent_load(header + kLaunchStatus)) != 0u);
-}
-__device__ __forceinline__ int64_t uniform64(int64_t v) {
-  const uint64_t u = static_cast<uint64_t>(v);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
-  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
 // Waits (one load per wave and poll) until *p carries the tag.
@@ -208,8 +209,9 @@ __device__ __forceinline__ void select_row(const FusedArgs& f, int b, uint32_t t
   const RowDesc d = row_desc(a.src, b);
   const int slot = a.slots[b];
   const bool slot_ok = slot >= 0 && slot < a.num_slots;
-  const int committed = a.committed_lens[b];
+  const int committed = committed_of(a.committed_lens, a.src, b);
   const int stored_count = slot_ok ? a.counts[slot] : 0;
+  uint32_t gen = (f.rec != nullptr && slot_ok) ? static_cast<uint32_t>(f.gen[slot]) : 0u;
   // The previous row's plan columns are read from sh.ids up to its end.
   lds_barrier();
   if (f.expire && tid == 0) raise_status(f.header, kStatusPartials);
@@ -264,9 +266,14 @@ __device__ __forceinline__ void select_row(const FusedArgs& f, int b, uint32_t t
     lds_barrier();
     int32_t* out = a.ids + static_cast<int64_t>(slot) * a.ids_stride;
     for (int j = tid; j < n_sel; j += kThreads) out[j] = sh.ids[j];
-    if (tid == 0) a.counts[slot] = n_sel;
+    ++gen;
+    if (tid == 0) {
+      a.counts[slot] = n_sel;
+      if (f.rec != nullptr) f.gen[slot] = static_cast<int32_t>(gen);
+    }
   }
   uint64_t* tagged = f.plans + static_cast<int64_t>(b) * kPlanCols;
+  if (f.rec != nullptr && tid == 0) coherent_store(tagged + kGenCol, (static_cast<uint64_t>(tag) << 32) | gen);
   if (slot_ok) {
     write_plan_row(a, b, slot, committed, n_sel, stored_count, sh, tagged, tag);
   } else {
@@ -283,6 +290,7 @@ __device__ __forceinline__ void select_row(const FusedArgs& f, int b, uint32_t t
 struct PlanView {
   int64_t slot, len, tail_start, prefix_len, drop;
   uint32_t lo, hi;
+  uint32_t gen;  // the slot's selection generation (with gather records)
 };
 
 // Polls row r's tagged plan until every column carries the tag, at most
@@ -292,7 +300,7 @@ __device__ __forceinline__ bool poll_plan(const FusedArgs& f, int r, uint32_t ta
   const int lane = threadIdx.x & 63;
   const uint64_t* row = f.plans + static_cast<int64_t>(r) * kPlanCols;
   const bool has_lo = lane < ga.plan_width;
-  const bool has_hi = lane + 64 < ga.plan_width;
+  const bool has_hi = lane + 64 < ga.plan_width || (f.rec != nullptr && lane + 64 == kGenCol);
   for (uint32_t spin = 0; spin < spins; ++spin) {
     const uint64_t a = has_lo ? coherent_load(row + lane) : static_cast<uint64_t>(tag) << 32;
     const uint64_t b = has_hi ? coherent_load(row + 64 + lane) : static_cast<uint64_t>(tag) << 32;
@@ -305,6 +313,7 @@ __device__ __forceinline__ bool poll_plan(const FusedArgs& f, int r, uint32_t ta
       v.tail_start = static_cast<int32_t>(__builtin_amdgcn_readlane(v.lo, 2));
       v.prefix_len = static_cast<int32_t>(__builtin_amdgcn_readlane(v.lo, 3));
       v.drop = static_cast<int32_t>(__builtin_amdgcn_readlane(v.lo, 4));
+      v.gen = static_cast<uint32_t>(__builtin_amdgcn_readlane(v.hi, kGenCol - 64));
       if (v.slot < 0 || v.slot >= ga.num_slots) v.len = 0;
       return true;
     }
@@ -326,6 +335,29 @@ __device__ __forceinline__ void run_task(const gather::GatherArgs& ga, const gat
         const int hi = __builtin_amdgcn_ds_bpermute((col & 63) << 2, static_cast<int>(v.hi));
         return static_cast<int64_t>(col < 64 ? lo : hi);
       });
+}
+
+// Gather task t of the row in `v`, keeping its gather record: a task whose
+// record shows the working cache already holds its bytes is left out, and
+// with prefix_only so is every task not wholly in the history prefix.
+template <int DT, bool NEOX>
+__device__ __forceinline__ void gather_recorded(const FusedArgs& f, const gather::GatherLane& L, const PlanView& v,
+                                                int r, int t) {
+  const int ppw = 64 / f.g.lanes_per_row;
+  const int p0 = t * ppw;
+  // Before the draft's prefill, only a row whose prefix sources (all below
+  // tail_start) precede the rows that prefill rewrites is moved.
+  const bool early_ok = !f.prefix_only || v.tail_start <= first_rewritten(f.p.src, r);
+  const uint64_t want =
+      p0 + ppw <= v.len && early_ok ? gather::prefix_record(p0, ppw, v.prefix_len, v.drop, v.gen) : 0u;
+  bool move = !f.prefix_only || want != 0u;
+  if (f.rec != nullptr && v.slot >= 0 && v.slot < f.g.num_slots) {
+    uint64_t* rec = f.rec + v.slot * f.rec_stride + t;
+    const uint64_t have = static_cast<uint64_t>(uniform64(static_cast<int64_t>(*rec)));
+    if (want != 0u && have == want) move = false;
+    if ((threadIdx.x & 63) == 0 && have != want) *rec = want;
+  }
+  if (move) run_task<DT, NEOX>(f.g, L, v, t);
 }
 
 // A scoring wave's gather tasks: task numbers gw, gw + tw, ... of the
@@ -359,7 +391,7 @@ __device__ __forceinline__ void gather_owned(const FusedArgs& f, const int* task
     }
     const int t = __builtin_amdgcn_readfirstlane(task - task_prefix[r]);
     if (published) {
-      run_task<DT, NEOX>(ga, L, v, t);
+      gather_recorded<DT, NEOX>(f, L, v, r, t);
     } else if ((threadIdx.x & 63) == 0) {
       __hip_atomic_exchange(f.state + static_cast<int64_t>(r) * f.task_cap + t, tag | kSkipped, __ATOMIC_ACQUIRE,
                             __HIP_MEMORY_SCOPE_AGENT);
@@ -401,7 +433,7 @@ __device__ __forceinline__ void redo_skipped(const FusedArgs& f, const int* task
             break;
           }
         }
-        run_task<DT, NEOX>(f.g, L, v, t0 + k);
+        gather_recorded<DT, NEOX>(f, L, v, b, t0 + k);
       }
     }
   }
@@ -446,7 +478,7 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
   if (tr < rows) {
     const int slot = f.p.slots[tr];
     const bool gathered = (ga.row_active == nullptr || ga.row_active[tr] != 0) && slot >= 0 && slot < ga.num_slots;
-    const int committed = f.p.committed_lens[tr];
+    const int committed = committed_of(f.p.committed_lens, f.p.src, tr);
     if (!selector) own = row_desc(f.s.src, tr);
     row_tasks = gathered ? (min(max(committed - 1, 0), ga.pos_limit) + ppw - 1) / ppw : 0;
   }
@@ -564,7 +596,8 @@ int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource
                       bool& launched) {
   launched = false;
   // Without a supplied LSE a row's scores need all of its chunks first: the chain runs.
-  if (d->workspace == nullptr || d->stages != DS_STAGE_ALL || d->lse == nullptr) return clear_error();
+  const bool prefix = d->stages == (DS_STAGE_SCORE | DS_STAGE_SELECT | DS_STAGE_PREFIX);
+  if (d->workspace == nullptr || (d->stages != DS_STAGE_ALL && !prefix) || d->lse == nullptr) return clear_error();
   const size_t need = fused_workspace_bytes(d->batch_rows, d->max_chunks, d->num_kv_heads, d->token_budget);
   DS_REQUIRE(need > 0 && d->workspace_bytes >= need,
              "step workspace too small: need %zu bytes for %d rows, %d chunks, %d KV heads, token budget %d", need,
@@ -600,7 +633,8 @@ int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource
                     (d->head_dim == 64 || d->head_dim == 128) && d->num_kv_heads <= kMaxHkv &&
                     d->batch_rows >= kMinFusedRows && d->batch_rows <= kFusedRows && uniform_page && vec &&
                     scalar_grid > 0 && d->slots != nullptr && d->plan_width <= kPlanCols &&
-                    64 / f.g.lanes_per_row >= kMinTaskPositions;
+                    64 / f.g.lanes_per_row >= kMinTaskPositions &&
+                    (d->gather_rec == nullptr || d->plan_width < kGenCol + 1);
   if (!fits) return clear_error();
 
   char* ws = static_cast<char*>(d->workspace);
@@ -616,6 +650,13 @@ int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource
   f.owner_spins = (d->flags & DS_STEP_SELECTORS_GATHER) != 0 ? 0u : kOwnerSpins;
   f.expire = (d->flags & DS_STEP_EXPIRE_WAITS) != 0 ? 1 : 0;
   f.status_out = status_out;
+  if (d->gather_rec != nullptr) {
+    f.gen = d->sel_gen;
+    f.rec = d->gather_rec;
+    f.rec_stride = d->rec_stride;
+  }
+  f.prefix_only = prefix ? 1 : 0;
+  if (prefix) f.p.working_lens = nullptr;  // the compact prefill sets them
   const int ppw = 64 / f.g.lanes_per_row;
   const int64_t upper_tasks = static_cast<int64_t>(d->batch_rows) * ((f.g.pos_limit + ppw - 1) / ppw);
   const bool neox = d->is_neox_style != 0;

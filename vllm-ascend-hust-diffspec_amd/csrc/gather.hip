@@ -12,6 +12,7 @@
 // neox pairs (x[i], x[i + rot/2]) or GPT-J pairs in registers, and reuses the
 // position's cos/sin for every head.
 #include "gather_body.h"
+#include "rowdesc.h"
 
 namespace ds355 {
 namespace {
@@ -126,6 +127,11 @@ struct PlanSource {
   int64_t* plan;             // [rows, plan_width] output
   int32_t* working_lens;     // [num_slots] output, or nullptr
   int hb, window, cap;       // history budget, rolling tail, chunk ids per plan row (<= 128)
+  const int32_t* gen;        // [num_slots] selection generations, or nullptr (no records)
+  uint64_t* rec;             // [num_slots, rec_stride] gather records (gather_body.h), or nullptr
+  int64_t rec_stride;
+  int prefix_only;           // move only tasks wholly in the history prefix
+  RowSource src;             // committed lengths from the verifier rows when `committed` is nullptr
 };
 
 // Plan and gather of one row in one launch (the compact prefill of
@@ -147,15 +153,16 @@ __global__ __launch_bounds__(kThreads) void plan_gather_kernel(GatherArgs a, Pla
   const int p0 = (static_cast<int>(blockIdx.x) * (kThreads / 64) + wave) * ppw;
 
   const int slot = scalar_load(ps.slots + r);
-  const int committed = scalar_load(ps.committed + r);
+  const int committed = ps.committed != nullptr ? scalar_load(ps.committed + r) : committed_of(nullptr, ps.src, r);
   const bool active = a.row_active == nullptr || scalar_load(a.row_active + r) != 0;
   const bool slot_ok = slot >= 0 && slot < a.num_slots;
   const bool writer = blockIdx.x == 0 && wave == 0;
   int count = -1;
-  uint32_t lo = 0, hi = 0;
+  uint32_t lo = 0, hi = 0, gen = 0;
   if (slot_ok) {
     const int32_t* ids = ps.sel_ids + static_cast<int64_t>(slot) * ps.sel_stride;
     count = scalar_load(ps.sel_count + slot);
+    if (ps.rec != nullptr) gen = static_cast<uint32_t>(scalar_load(ps.gen + slot));
     lo = lane < ps.cap ? static_cast<uint32_t>(ids[lane]) : 0u;
     hi = lane + 64 < ps.cap ? static_cast<uint32_t>(ids[lane + 64]) : 0u;
   }
@@ -212,7 +219,22 @@ __global__ __launch_bounds__(kThreads) void plan_gather_kernel(GatherArgs a, Pla
     if (lane == 0 && ps.working_lens != nullptr) ps.working_lens[slot] = static_cast<int32_t>(len);
   }
   const int64_t limit = min(len, static_cast<int64_t>(a.pos_limit));
-  if (!active || p0 >= limit) return;
+  if (!active) return;
+  // The wave's record (its own entry: read before it is rewritten, by this
+  // wave only), and whether its task is moved at all.
+  // A task cut by the position limit is not moved whole: no record.
+  // Before the draft's prefill, only a row whose prefix sources (all below
+  // tail_start) precede the rows that prefill rewrites is moved.
+  const bool early_ok = !ps.prefix_only || tail_start <= first_rewritten(ps.src, r);
+  const uint64_t want = p0 + ppw <= limit && early_ok ? prefix_record(p0, ppw, prefix_len, drop, gen) : 0u;
+  bool move = p0 < limit && (!ps.prefix_only || want != 0u);
+  if (ps.rec != nullptr) {
+    uint64_t* rec = ps.rec + static_cast<int64_t>(slot) * ps.rec_stride + p0 / ppw;
+    const uint64_t have = static_cast<uint64_t>(uniform64(static_cast<int64_t>(*rec)));
+    if (want != 0u && have == want) move = false;
+    if (lane == 0 && have != want) *rec = want;
+  }
+  if (!move) return;
   const GatherLane L = gather_lane<DT, NEOX>(a);
   gather_task<DT, NEOX, HG>(a, L, p0, slot, limit, tail_start, prefix_len, drop, [&](int64_t c) {
     const int col = static_cast<int>(c);
@@ -220,6 +242,18 @@ __global__ __launch_bounds__(kThreads) void plan_gather_kernel(GatherArgs a, Pla
     const int h = __builtin_amdgcn_ds_bpermute((col & 63) << 2, static_cast<int>(hi));
     return static_cast<int64_t>(col < 64 ? l : h);
   });
+}
+
+// Gather records of the rows' slots set to 0 (nothing known held): one
+// workgroup per row, for rebuilds that keep no records.
+__global__ __launch_bounds__(kThreads) void clear_records_kernel(const int32_t* slots, int num_slots,
+                                                                 const int32_t* row_active, uint64_t* rec,
+                                                                 int64_t rec_stride, int64_t entries) {
+  const int r = static_cast<int>(blockIdx.x);
+  if (row_active != nullptr && row_active[r] == 0) return;
+  const int slot = slots[r];
+  if (slot < 0 || slot >= num_slots) return;
+  for (int64_t i = threadIdx.x; i < entries; i += kThreads) rec[slot * rec_stride + i] = 0u;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -402,7 +436,8 @@ int launch_plan_gather(hipStream_t stream, int dtype, const void* raw_key, const
                        int token_budget, int chunk_size, int rotary_dim, int is_neox_style, int history_budget,
                        const int32_t* row_active, const int32_t* sel_ids, int64_t sel_stride,
                        const int32_t* sel_count, const int32_t* slots, const int32_t* committed_lens, int64_t* plan,
-                       int32_t* working_lens, int recent_window, bool& launched) {
+                       int32_t* working_lens, int recent_window, const int32_t* gen, uint64_t* rec,
+                       int64_t rec_stride, bool prefix_only, const RowSource& src, bool& launched) {
   launched = false;
   GatherArgs a;
   bool vec = false;
@@ -413,7 +448,7 @@ int launch_plan_gather(hipStream_t stream, int dtype, const void* raw_key, const
   if (rc != DS_OK) return rc;
   const int64_t cap = std::min<int64_t>(plan_width - 5, sel_stride);
   if (rows == 0 || !vec || cap > 128 || grid <= 0) return clear_error();
-  DS_REQUIRE(sel_ids && sel_count && slots && committed_lens && plan, "null plan pointer");
+  DS_REQUIRE(sel_ids && sel_count && slots && plan && (committed_lens || src.counts), "null plan pointer");
   DS_REQUIRE(recent_window > 0, "recent_window must be positive");
   DS_REQUIRE(history_budget >= chunk_size && history_budget % chunk_size == 0,
              "history_budget must be a positive chunk-size multiple");
@@ -428,6 +463,15 @@ int launch_plan_gather(hipStream_t stream, int dtype, const void* raw_key, const
   ps.hb = history_budget;
   ps.window = recent_window;
   ps.cap = static_cast<int>(cap);
+  if (rec != nullptr) {
+    DS_REQUIRE(gen != nullptr, "gather records need the selection generations");
+    DS_REQUIRE(rec_stride >= token_budget, "gather record row stride is smaller than token_budget");
+  }
+  ps.gen = gen;
+  ps.rec = rec;
+  ps.rec_stride = rec_stride;
+  ps.prefix_only = prefix_only ? 1 : 0;
+  ps.src = src;
   const bool neox = is_neox_style != 0;
   switch (dtype) {
     case DS_BF16: rc = launch_plan_gather_dt<DS_BF16>(stream, a, ps, neox); break;
@@ -436,6 +480,14 @@ int launch_plan_gather(hipStream_t stream, int dtype, const void* raw_key, const
   }
   launched = rc == DS_OK;
   return rc;
+}
+
+int clear_gather_records(hipStream_t stream, const int32_t* slots, int rows, int num_slots,
+                         const int32_t* row_active, uint64_t* rec, int64_t rec_stride, int64_t entries) {
+  if (rows <= 0) return clear_error();
+  DS_SUPPORTED(rows <= 65535, "at most 65535 rows per launch");
+  clear_records_kernel<<<rows, kThreads, 0, stream>>>(slots, num_slots, row_active, rec, rec_stride, entries);
+  return check_launch("clear gather records");
 }
 
 }  // namespace ds355

@@ -378,5 +378,19 @@ __device__ __forceinline__ void gather_task(const GatherArgs& a, const GatherLan
   }
 }
 
+// Gather records: what the working cache holds per (slot, task of ppw local
+// positions), so a rebuild can leave out tasks whose bytes it would rewrite
+// unchanged.  A task of local positions [p0, p0 + ppw) lying wholly in the
+// plan's history prefix (p0 + ppw <= prefix_len) holds bytes that depend only
+// on the slot's chunk ids, the prefix drop and the raw rows they point to,
+// so its record is (selection generation << 32) | (drop + 1); every other
+// task's record is 0.  Raw rows before a request's committed root are not
+// rewritten while the request holds its slot (the draft only appends), and
+// a slot's generation changes with every stored selection and every change
+// of the request holding it, so an equal record means equal bytes.
+__device__ __forceinline__ uint64_t prefix_record(int p0, int ppw, int64_t prefix_len, int64_t drop, uint32_t gen) {
+  return p0 + ppw <= prefix_len ? (static_cast<uint64_t>(gen) << 32) | static_cast<uint64_t>(drop + 1) : 0u;
+}
+
 }  // namespace gather
 }  // namespace ds355

@@ -51,4 +51,20 @@ __device__ __forceinline__ RowDesc row_desc(const RowSource& s, int b) {
   return d;
 }
 
+// First raw position the draft's prefill of this step rewrites for row b
+// (its first verifier query token), for a history gather that runs before
+// that prefill: positions below it are final.
+__device__ __forceinline__ int first_rewritten(const RowSource& s, int b) {
+  return s.target_len[b] - s.q_len[b];
+}
+
+// Committed length (root position + 1) of row b for its plan: given per
+// row, or, without that array, the scored length of a row that committed
+// tokens this step and 0 for any other row (no history to move yet).
+__device__ __forceinline__ int committed_of(const int32_t* committed_lens, const RowSource& s, int b) {
+  if (committed_lens != nullptr) return committed_lens[b];
+  const RowDesc d = row_desc(s, b);
+  return d.active ? d.len : 0;
+}
+
 }  // namespace ds355

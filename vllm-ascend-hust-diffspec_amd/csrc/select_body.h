@@ -32,6 +32,7 @@ struct SelectArgs {
   int32_t* working_lens;
   int recent_window;
   int num_slots;
+  int32_t* gen;  // [num_slots] selection generation, +1 with every stored selection; or nullptr
 };
 
 // LDS of one selecting workgroup of NT threads.  KEYS = candidates whose

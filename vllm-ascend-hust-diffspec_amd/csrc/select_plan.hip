@@ -40,7 +40,7 @@ __global__ __launch_bounds__(NT) void select_plan_kernel(SelectArgs a) {
   const RowDesc d = a.do_select ? row_desc(a.src, b) : RowDesc{0, 0, 0};
   const int slot = a.slots != nullptr ? a.slots[b] : b;
   const bool slot_ok = slot >= 0 && slot < a.num_slots;
-  const int committed = a.do_plan ? a.committed_lens[b] : 0;
+  const int committed = a.do_plan ? committed_of(a.committed_lens, a.src, b) : 0;
   const int stored_count = (a.do_plan && slot_ok) ? a.counts[slot] : 0;
   const float* part = a.partials + static_cast<int64_t>(b) * a.max_chunks * a.hkv;
   float pre[kPre];
@@ -123,7 +123,10 @@ __global__ __launch_bounds__(NT) void select_plan_kernel(SelectArgs a) {
     lds_barrier();
     int32_t* out = a.ids + static_cast<int64_t>(slot) * a.ids_stride;
     for (int j = tid; j < n_sel; j += NT) out[j] = sh.ids[j];
-    if (tid == 0) a.counts[slot] = n_sel;
+    if (tid == 0) {
+      a.counts[slot] = n_sel;
+      if (a.gen != nullptr) a.gen[slot] += 1;  // one row per slot: no other writer
+    }
   }
 
   if (!a.do_plan) return;
@@ -155,7 +158,7 @@ int make_select_args(SelectArgs& a, float* scores, int64_t score_stride, const f
   }
   if (batch == 0) return clear_error();
   if (do_select) DS_REQUIRE(scores && ids && counts && (src.seq_lens || src.counts), "null selection pointer");
-  if (do_plan) DS_REQUIRE(ids && counts && committed_lens && plan, "null plan pointer");
+  if (do_plan) DS_REQUIRE(ids && counts && plan && (committed_lens || src.counts), "null plan pointer");
 
   if (do_select && partials != nullptr) DS_REQUIRE(hkv > 0 && hq > 0 && max_chunks > 0, "bad score partial shape");
   a.scores = scores;
@@ -202,12 +205,13 @@ int launch_select_plan(hipStream_t stream, float* scores, int64_t score_stride, 
                        int batch, int chunk, int budget, int do_select, int do_plan, int32_t* ids,
                        int64_t ids_stride, int32_t* counts, const int32_t* slots, int num_slots,
                        const int32_t* committed_lens, int64_t* plan, int plan_width, int32_t* working_lens,
-                       int recent_window) {
+                       int recent_window, int32_t* gen) {
   SelectArgs a;
   const int rc = make_select_args(a, scores, score_stride, partials, max_chunks, hkv, hq, src, batch, chunk, budget,
                                   do_select, do_plan, ids, ids_stride, counts, slots, num_slots, committed_lens, plan,
                                   plan_width, working_lens, recent_window);
   if (rc != DS_OK || batch == 0) return rc;
+  a.gen = gen;
   // Rows of kLongRow chunks or more are selected by 1024-thread workgroups
   // (four times the waves for the per-candidate sweeps), shorter ones by 256.
   const int64_t row_chunks = (static_cast<int64_t>(src.max_len) + chunk - 1) / chunk;
@@ -228,7 +232,7 @@ extern "C" int ds_select_chunks(ds_stream_t stream, const float* scores, int64_t
   return ds355::launch_select_plan(reinterpret_cast<hipStream_t>(stream), const_cast<float*>(scores), score_stride,
                                    nullptr, 0, 0, 0, src, batch,
                                    chunk_size, history_budget, 1, 0, ids, ids_stride, counts, nullptr, batch,
-                                   nullptr, nullptr, 0, nullptr, chunk_size);
+                                   nullptr, nullptr, 0, nullptr, chunk_size, nullptr);
 }
 
 extern "C" int ds_build_plan(ds_stream_t stream, const int32_t* sel_ids, int64_t sel_stride,
@@ -244,5 +248,5 @@ extern "C" int ds_build_plan(ds_stream_t stream, const int32_t* sel_ids, int64_t
                                    chunk_size,
                                    history_budget, 0, 1, const_cast<int32_t*>(sel_ids), sel_stride,
                                    const_cast<int32_t*>(sel_count), slots, num_slots, committed_lens, plan,
-                                   plan_width, working_lens, recent_window);
+                                   plan_width, working_lens, recent_window, nullptr);
 }

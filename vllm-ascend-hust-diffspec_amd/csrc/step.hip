@@ -23,7 +23,7 @@ int launch_select_plan(hipStream_t stream, float* scores, int64_t score_stride, 
                        int batch, int chunk, int budget, int do_select, int do_plan, int32_t* ids,
                        int64_t ids_stride, int32_t* counts, const int32_t* slots, int num_slots,
                        const int32_t* committed_lens, int64_t* plan, int plan_width, int32_t* working_lens,
-                       int recent_window);
+                       int recent_window, int32_t* gen);
 
 int rebuild_compact_kv_impl(hipStream_t stream, int dtype, const void* raw_key, const void* raw_value,
                             void* working_key, void* working_value, const int64_t* plan, int rows,
@@ -41,16 +41,30 @@ int launch_plan_gather(hipStream_t stream, int dtype, const void* raw_key, const
                        int token_budget, int chunk_size, int rotary_dim, int is_neox_style, int history_budget,
                        const int32_t* row_active, const int32_t* sel_ids, int64_t sel_stride,
                        const int32_t* sel_count, const int32_t* slots, const int32_t* committed_lens, int64_t* plan,
-                       int32_t* working_lens, int recent_window, bool& launched);
+                       int32_t* working_lens, int recent_window, const int32_t* gen, uint64_t* rec,
+                       int64_t rec_stride, bool prefix_only, const RowSource& src, bool& launched);
+
+int clear_gather_records(hipStream_t stream, const int32_t* slots, int rows, int num_slots,
+                         const int32_t* row_active, uint64_t* rec, int64_t rec_stride, int64_t entries);
 
 // The step for a descriptor whose scratch buffers are already set.
 // status_out (optional): a single launch ORs its status bits into it.
 int retrieval_step(hipStream_t stream, const ds_step_desc* d, uint32_t* status_out) {
   DS_REQUIRE(d != nullptr, "null step descriptor");
+  DS_REQUIRE((d->stages & ~(DS_STAGE_ALL | DS_STAGE_PREFIX)) == 0, "unknown stage bits 0x%x", d->stages);
   const bool score = (d->stages & DS_STAGE_SCORE) != 0;
   const bool select = (d->stages & DS_STAGE_SELECT) != 0;
-  const bool rebuild = (d->stages & DS_STAGE_PLAN) != 0;
-  DS_REQUIRE((d->stages & ~DS_STAGE_ALL) == 0, "unknown stage bits 0x%x", d->stages);
+  const bool full = (d->stages & DS_STAGE_PLAN) != 0;
+  const bool prefix = !full && (d->stages & DS_STAGE_PREFIX) != 0;
+  const bool rebuild = full || prefix;
+  const bool records = d->gather_rec != nullptr;
+  // A prefix-only rebuild leaves the working lengths to the compact prefill.
+  int32_t* const working_lens = prefix ? nullptr : d->working_lens;
+  DS_REQUIRE(!rebuild || d->committed_lens != nullptr || (prefix && d->counts != nullptr),
+             "the plan needs committed_lens (or, for DS_STAGE_PREFIX, the verifier rows)");
+  DS_REQUIRE(records == (d->sel_gen != nullptr), "sel_gen and gather_rec come together");
+  DS_REQUIRE(!prefix || records, "DS_STAGE_PREFIX needs gather records (sel_gen, gather_rec)");
+  if (records) DS_REQUIRE(d->rec_stride >= d->token_budget, "gather record row stride is smaller than token_budget");
   DS_REQUIRE(d->batch_rows >= 0 && d->batch_size >= 0 && d->batch_size <= d->batch_rows,
              "batch_size must be between zero and batch_rows");
   DS_REQUIRE(d->chunk_size > 0 && d->history_budget >= d->chunk_size && d->history_budget % d->chunk_size == 0,
@@ -90,24 +104,46 @@ int retrieval_step(hipStream_t stream, const ds_step_desc* d, uint32_t* status_o
                              d->lse_out_stride);
     if (rc != DS_OK) return rc;
   }
-  if (rebuild && !select) {
-    // The compact prefill alone: plans and gather in one launch when the
-    // gather's vector path covers the shapes.
+  // The rebuild as one plan + gather launch (the compact prefill's kernel)
+  // when the gather's vector path covers the shapes and nothing needs the
+  // plan kernel's selection: always alone, and after a selection when the
+  // gather keeps records.
+  if (rebuild && (!select || records)) {
+    if (select) {
+      rc = launch_select_plan(stream, d->scores, d->max_chunks, d->score_partials, d->max_chunks, d->num_kv_heads,
+                              d->num_q_heads, src, d->batch_rows, d->chunk_size, d->history_budget, 1, 0,
+                              d->sel_ids, d->sel_stride, d->sel_count, d->slots, d->num_slots, d->committed_lens,
+                              d->plan, d->plan_width, working_lens, d->recent_window, d->sel_gen);
+      if (rc != DS_OK) return rc;
+    }
     bool one = false;
     rc = launch_plan_gather(stream, d->kv_dtype, d->raw_key, d->raw_value, d->working_key, d->working_value,
                             d->batch_rows, d->plan_width, d->cos_sin, d->cs_stride, d->cs_rows, d->num_slots,
                             d->max_model_len, d->draft_heads, d->draft_head_dim, d->token_budget, d->chunk_size,
                             d->rotary_dim, d->is_neox_style, d->history_budget, d->row_active, d->sel_ids,
-                            d->sel_stride, d->sel_count, d->slots, d->committed_lens, d->plan, d->working_lens,
-                            d->recent_window, one);
+                            d->sel_stride, d->sel_count, d->slots, d->committed_lens, d->plan, working_lens,
+                            d->recent_window, d->sel_gen, d->gather_rec, d->rec_stride, prefix, src, one);
     if (rc != DS_OK || one) return rc;
-  }
-  if (select || rebuild) {
+    // Shapes the one-launch rebuild does not cover: the plan kernel, then
+    // (not for a prefix-only rebuild) the gather below moves every
+    // position, and the records are cleared.
+    if (records) {
+      DS_REQUIRE(d->slots != nullptr, "gather records need the slots of the plan rows");
+      rc = clear_gather_records(stream, d->slots, d->batch_rows, d->num_slots, d->row_active, d->gather_rec,
+                                d->rec_stride, d->token_budget);
+      if (rc != DS_OK) return rc;
+    }
+    rc = launch_select_plan(stream, d->scores, d->max_chunks, d->score_partials, d->max_chunks, d->num_kv_heads,
+                            d->num_q_heads, src, d->batch_rows, d->chunk_size, d->history_budget, 0, 1, d->sel_ids,
+                            d->sel_stride, d->sel_count, d->slots, d->num_slots, d->committed_lens, d->plan,
+                            d->plan_width, working_lens, d->recent_window, nullptr);
+    if (rc != DS_OK || prefix) return rc;
+  } else if (select || rebuild) {
     rc = launch_select_plan(stream, d->scores, d->max_chunks, d->score_partials, d->max_chunks, d->num_kv_heads,
                             d->num_q_heads, src, d->batch_rows, d->chunk_size, d->history_budget,
                             select ? 1 : 0, rebuild ? 1 : 0, d->sel_ids, d->sel_stride, d->sel_count, d->slots,
                             d->num_slots, d->committed_lens, d->plan, d->plan_width, d->working_lens,
-                            d->recent_window);
+                            d->recent_window, d->sel_gen);
     if (rc != DS_OK) return rc;
   }
   if (!rebuild) return clear_error();

@@ -18,11 +18,11 @@ LIBRARY_PATH = Path(__file__).resolve().parent / "libds355.so"
 DS_OK, DS_ERR_INVALID, DS_ERR_UNSUPPORTED, DS_ERR_HIP = 0, 1, 2, 3
 DS_BF16, DS_FP16, DS_FP32 = 0, 1, 2
 DS_HEAD_MEAN, DS_HEAD_MAX = 0, 1
-DS_STAGE_SCORE, DS_STAGE_SELECT, DS_STAGE_PLAN, DS_STAGE_ALL = 1, 2, 4, 7
+DS_STAGE_SCORE, DS_STAGE_SELECT, DS_STAGE_PLAN, DS_STAGE_ALL, DS_STAGE_PREFIX = 1, 2, 4, 7, 8
 DS_STEP_SELECTORS_GATHER, DS_STEP_EXPIRE_WAITS = 1, 2
 # Regions of the static scratch of ds_retrieval_step_static (include/ds355.h).
 DS_STATIC_FUSED_BYTES, DS_STATIC_PARTIALS_BYTES, DS_STATIC_PAIRS_BYTES = 8 << 20, 4 << 20, 12 << 20
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 EXPORTED_SYMBOLS = (
     "ds_last_error",
@@ -88,6 +88,7 @@ class StepDesc(ctypes.Structure):
         ("workspace", _p), ("workspace_bytes", ctypes.c_size_t),
         ("lse_partials", _p), ("lse_out", _p), ("lse_out_stride", _i64),
         ("flags", _i32),
+        ("sel_gen", _p), ("gather_rec", _p), ("rec_stride", _i64),
     ]
 
 

@@ -143,6 +143,8 @@ class _Staging:
 
 
 WORKING_LENS = "working_lens"  # pending positions = the slots' device working lengths
+# The retrieval call: score, select, and gather each row's history prefix.
+RETRIEVAL_STAGES = _step.SCORE | _step.SELECT | _step.PREFIX
 
 
 class DiffSpecDraftCache:
@@ -206,6 +208,17 @@ class DiffSpecDraftCache:
         self.sel_ids = torch.zeros((max_num_reqs, capacity), dtype=torch.int32, device=self.device)
         self.sel_count = torch.full((max_num_reqs,), -1, dtype=torch.int32, device=self.device)
         self.working_lens = torch.zeros((max_num_reqs,), dtype=torch.int32, device=self.device)
+        # Gather records (include/ds355.h): each slot's selection generation,
+        # and per gather task of its working cache what the cache holds, so
+        # a rebuild moves only what changed.  The retrieval call moves each
+        # row's history prefix (raw rows well before the committed root,
+        # final by then), and the compact prefill after populate_prefill the
+        # rest; between retrievals only the rolling tail moves.
+        self.sel_gen = torch.zeros((max_num_reqs,), dtype=torch.int32, device=self.device)
+        self.gather_records = torch.zeros((max_num_reqs, settings.token_budget), dtype=torch.int64,
+                                          device=self.device)
+        self._workspace: torch.Tensor | None = None  # single-launch retrieval, on first use
+        self._workspace_heads = 0
 
         self.max_batch_rows = max_batch_rows or max_num_reqs
         self.max_chunks = (max_model_len + settings.chunk_size - 1) // settings.chunk_size
@@ -301,9 +314,10 @@ class DiffSpecDraftCache:
             if request_id not in active:
                 freed.append(self._request_slots.pop(request_id))
         if freed:
-            index = torch.tensor(freed, dtype=torch.long)
-            self.sel_count[index.to(self.device)] = -1
-            self.working_lens[index.to(self.device)] = 0
+            index = torch.tensor(freed, dtype=torch.long).to(self.device)
+            self.sel_count[index] = -1
+            self.working_lens[index] = 0
+            self.sel_gen[index] += 1  # the slot's records describe the request that left
         used = set(self._request_slots.values())
         free = iter(sorted(set(range(self.max_num_reqs)) - used))
         for request_id in request_ids:
@@ -427,7 +441,7 @@ class DiffSpecDraftCache:
         staged = self._rows_staging.upload([
             starts, [e - s for s, e in zip(starts, ends)], seq_lens[:batch_size], self._active_slots, [],
         ])
-        key = self._step_key(_step.SCORE | _step.SELECT, batch_size, batch_size, self._cos_sin_cache(),
+        key = self._step_key(RETRIEVAL_STAGES, batch_size, batch_size, self._cos_sin_cache(),
                              self._target_query, self._target_lse, self._target_key_cache, self._target_block_tables)
         return self._active_slots, staged, key
 
@@ -505,7 +519,7 @@ class DiffSpecDraftCache:
             counts.copy_(valid_sampled_token_count.reshape(-1)[:batch_size])  # device-side cast, no sync
         started = time.perf_counter()
         q, lse, kc, bt = self._target_query, self._target_lse, self._target_key_cache, self._target_block_tables
-        stages = _step.SCORE | _step.SELECT
+        stages = RETRIEVAL_STAGES
         if key is None:
             key = self._step_key(stages, batch_size, batch_size, self._cos_sin_cache(), q, lse, kc, bt)
         hit = self._step_descs.get(key)
@@ -525,8 +539,7 @@ class DiffSpecDraftCache:
             )
             snapshot = _step.VerifierSnapshot(query=q, lse=lse, key_cache=kc, block_table=bt, scale=self._target_scale)
             self._launch(stages, batch_size, snapshot=snapshot, rows=rows,
-                         slots=self._view("rs", batch_size, lambda: staged[3, :batch_size]),
-                         committed=self._view("rc", batch_size, lambda: staged[2, :batch_size]))
+                         slots=self._view("rs", batch_size, lambda: staged[3, :batch_size]), committed=None)
         self.metrics.observe_retrieval(time.perf_counter() - started)
 
     # -- rebuild (runtime.py:1349-1371, 1683-1765) ------------------------------------------------
@@ -814,7 +827,7 @@ class DiffSpecDraftCache:
         batch_rows: int,
         *,
         slots: torch.Tensor,
-        committed: torch.Tensor,
+        committed: torch.Tensor | None,
         snapshot: _step.VerifierSnapshot | None = None,
         rows: _step.VerifierRows | None = None,
     ) -> None:
@@ -841,6 +854,17 @@ class DiffSpecDraftCache:
                 self._step_descs.clear()
             lse_partials = self._view("pairs", batch_rows, lambda: self._lse_partials[:batch_rows])
             lse_out = self._view("lse_out", batch_rows, lambda: self.scored_lse[:batch_rows])
+        workspace = None
+        if stages & _step.SCORE and stages & _step.PREFIX and snapshot.lse is not None:
+            # Score, selection and the prefix gather as one launch where the
+            # batch suits it (the library picks; the workspace allows it).
+            kv_heads = snapshot.key_cache.shape[2]
+            if self._workspace is None or self._workspace_heads != kv_heads:
+                self._workspace = _step.new_workspace(self.max_batch_rows, self.max_chunks, kv_heads,
+                                                      self.settings.token_budget, self.device)
+                self._workspace_heads = kv_heads
+                self._step_descs.clear()
+            workspace = self._workspace
         key = self._step_key(stages, batch_rows, None if rows is None else rows.batch_size, cos_sin,
                              snapshot.query if snapshot is not None else None,
                              snapshot.lse if snapshot is not None else None,
@@ -871,7 +895,8 @@ class DiffSpecDraftCache:
             working_key=self.working_key, working_value=self.working_value,
             cos_sin_cache=cos_sin, rotary_dim=rotary.rotary_dim, is_neox_style=rotary.is_neox_style,
             chunk_size=self.settings.chunk_size, history_budget=self.history_budget,
-            recent_window=self.recent_window, lse_partials=lse_partials, lse_out=lse_out,
+            recent_window=self.recent_window, lse_partials=lse_partials, lse_out=lse_out, workspace=workspace,
+            gather_records=(self.sel_gen, self.gather_records),
         )
 
     def _step_key(self, stages: int, batch_rows: int, batch_size: int | None, cos_sin: torch.Tensor,

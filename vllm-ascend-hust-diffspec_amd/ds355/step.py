@@ -61,6 +61,7 @@ class VerifierRows:
 
 
 SCORE, SELECT, PLAN, ALL = _lib.DS_STAGE_SCORE, _lib.DS_STAGE_SELECT, _lib.DS_STAGE_PLAN, _lib.DS_STAGE_ALL
+PREFIX = _lib.DS_STAGE_PREFIX
 SELECTORS_GATHER, EXPIRE_WAITS = _lib.DS_STEP_SELECTORS_GATHER, _lib.DS_STEP_EXPIRE_WAITS
 
 
@@ -149,7 +150,7 @@ def build_step_desc(
     sel_ids: torch.Tensor,
     sel_count: torch.Tensor,
     slots: torch.Tensor,
-    committed_lens: torch.Tensor,
+    committed_lens: torch.Tensor | None,
     plan: torch.Tensor,
     working_lens: torch.Tensor | None,
     raw_key: torch.Tensor,
@@ -167,6 +168,7 @@ def build_step_desc(
     lse_partials: torch.Tensor | None = None,
     lse_out: torch.Tensor | None = None,
     flags: int = 0,
+    gather_records: tuple[torch.Tensor, torch.Tensor] | None = None,
 ) -> tuple[_lib.StepDesc, torch.device]:
     """Validate and pack a step descriptor for ``stages`` (``SCORE | SELECT | PLAN``; ``ALL`` = one step).
 
@@ -184,13 +186,25 @@ def build_step_desc(
     natural-log LSE is written); such a step runs as the kernel chain.
 
     ``flags`` (tests only): ``SELECTORS_GATHER`` makes the single launch's
-    selecting workgroups do every gather task (the path of a task whose
-    scoring wave stopped waiting for its plan; same results);
-    ``EXPIRE_WAITS`` makes every selector report an expired wait (status bit
-    0, results not valid).
+    scoring waves leave every gather task to the last workgroup to finish
+    (the path of a task whose scoring wave stopped waiting for its plan; same
+    results); ``EXPIRE_WAITS`` makes every selector report an expired wait
+    (status bit 0, results not valid).
+
+    ``gather_records`` = (``sel_gen`` ``[num_slots]`` int32, ``records``
+    ``[num_slots, >= token_budget]`` int64, both zero-filled by the owner)
+    lets a rebuild leave out the gather tasks whose working-cache bytes would
+    not change (include/ds355.h: gather records): every stored selection
+    increments the slot's generation, and the caller increments it when a
+    different request takes the slot.  ``PREFIX`` in place of ``PLAN`` moves
+    only the tasks wholly inside each row's history prefix (needs the
+    records): the retrieval call can do that before the draft's prefill
+    rewrites the rolling tail's raw rows.
     """
-    if stages & ~ALL:
+    if stages & ~(ALL | PREFIX):
         raise ValueError(f"unknown stage bits {stages:#x}")
+    if stages & PREFIX and gather_records is None:
+        raise ValueError("the PREFIX stage needs gather records")
     uses_rows = bool(stages & (SCORE | SELECT))
     batch_rows = slots.numel()
     num_slots, max_model_len, heads, head_dim = raw_key.shape
@@ -208,7 +222,10 @@ def build_step_desc(
     if cos_sin_cache.shape[0] < history_budget:
         raise ValueError("cos/sin cache must contain all local positions and rotary dimensions")
     _i32("slots", slots)
-    _i32("committed_lens", committed_lens, batch_rows)
+    if committed_lens is not None:
+        _i32("committed_lens", committed_lens, batch_rows)
+    elif not (stages & PREFIX and stages & (SCORE | SELECT)):
+        raise ValueError("committed_lens is required (only a PREFIX rebuild with the verifier rows derives it)")
     _i32("sel_ids", sel_ids)
     _i32("sel_count", sel_count, num_slots)
     if sel_ids.shape[0] < num_slots:
@@ -299,7 +316,15 @@ def build_step_desc(
                   workspace=workspace, lse_partials=lse_partials, lse_out=lse_out)
     if flags & ~(SELECTORS_GATHER | EXPIRE_WAITS):
         raise ValueError(f"unknown step flags {flags:#x}")
-    if _lib.DEBUG_CHECKS and stages & PLAN:
+    if gather_records is not None:
+        gen, records = gather_records
+        _i32("sel_gen", gen, num_slots)
+        if (records.dtype != torch.int64 or records.ndim != 2 or records.shape[0] < num_slots
+                or records.shape[1] < token_budget or records.stride(1) != 1):
+            raise ValueError("gather records must be int64 [num_slots, >= token_budget] with unit last stride")
+        _lib.require_gpu(gen, records)
+        desc.sel_gen, desc.gather_rec, desc.rec_stride = gen.data_ptr(), records.data_ptr(), records.stride(0)
+    if _lib.DEBUG_CHECKS and stages & (PLAN | PREFIX):
         check_distinct_slots(slots, num_slots, row_active)
     desc.flags = flags
     return desc, device
@@ -348,7 +373,7 @@ def _set_pointers(desc: _lib.StepDesc, *, snapshot=None, rows=None, scores=None,
     else:
         desc.batch_size = desc.batch_rows
     desc.sel_ids, desc.sel_count, desc.slots = sel_ids.data_ptr(), sel_count.data_ptr(), slots.data_ptr()
-    desc.committed_lens, desc.plan, desc.working_lens = committed_lens.data_ptr(), plan.data_ptr(), p(working_lens)
+    desc.committed_lens, desc.plan, desc.working_lens = p(committed_lens), plan.data_ptr(), p(working_lens)
     desc.raw_key, desc.raw_value = raw_key.data_ptr(), raw_value.data_ptr()
     desc.working_key, desc.working_value = working_key.data_ptr(), working_value.data_ptr()
     desc.cos_sin, desc.row_active, desc.workspace = cos_sin_cache.data_ptr(), p(row_active), p(workspace)

@@ -381,16 +381,22 @@ def run(args):
         status = [step.workspace_status(st["workspace"]) for st in states]
         if any(status):
             raise RuntimeError(f"single-launch status words {status} after the stage timings: results not valid")
-    # The runtime's own path: its two calls (retrieval, then compact prefill).
-    two_call_us = score_select_us + plan_gather_us
-    runtime_step = {
-        "what": "DiffSpecDraftCache's two calls per retrieval step: accept_target_queries (SCORE | SELECT) and "
-                "prepare_compact_prefill (plans + gather as one launch), kernel time",
-        "score_select_us": round(score_select_us, 2), "compact_prefill_us": round(plan_gather_us, 2),
-        "total_us": round(two_call_us, 2), "algorithmic_bytes": chain_bytes,
+    # The runtime's own path: its two calls (retrieval, then compact prefill),
+    # with gather records as DiffSpecDraftCache keeps them.
+    runtime_step = runtime_path(copies, states, rows_t, rows, cos_sin, spec, hb, row_active, device, reps)
+    two_call_us = runtime_step["total_us"]
+    runtime_step.update({
+        "what": "DiffSpecDraftCache's calls per retrieval step, kernel time: accept_target_queries "
+                "(SCORE | SELECT) and prepare_compact_prefill (PLAN with gather records); and a "
+                "compact prefill between retrievals",
+        "algorithmic_bytes": chain_bytes,
         "achieved_gbps": round(chain_bytes / (two_call_us * 1e-6) / 1e9, 1),
         "frac": round(chain_bytes / (two_call_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
-    }
+        "without_records": runtime_path(copies, states, rows_t, rows, cos_sin, spec, hb, row_active, device, reps,
+                                        records=False),
+        "prefix_at_retrieval": runtime_path(copies, states, rows_t, rows, cos_sin, spec, hb, row_active, device,
+                                            reps, prefix=True),
+    })
     n_copies = len(copies)
     del copies, states, descs, gather_args
     torch.cuda.empty_cache()
@@ -462,6 +468,81 @@ def run(args):
 
 
 ATTENTION_COPIES = 6  # working caches rotated per launch: 6 x 67 MB exceeds the 256 MB MALL
+
+
+def runtime_path(copies, states, rows_t, rows, cos_sin, spec, hb, row_active, device, reps, prefix=False,
+                 records=True):
+    """The plugin's own calls with gather records, as DiffSpecDraftCache makes
+    them: the retrieval call (SCORE | SELECT; with ``prefix`` also each row's
+    history prefix, one launch for 8+ rows) and the compact prefill after it
+    (PLAN: plans and the gather of what the records do not hold), then the
+    compact prefill of a cycle between retrievals (selections unchanged: the
+    rolling tail).  HIP events around each launch, input copies rotated; per
+    copy its own selection generations and records (``records=False``: the
+    same calls without them, every compact prefill moving every row)."""
+    import torch
+
+    from ds355 import _lib, step
+
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    chunk, token_budget, d = spec["chunk"], spec["budget"], spec["d"]
+    pairs = []
+    for c, st in zip(copies, states):
+        held_state = (torch.zeros((rows,), dtype=torch.int32, device=device),
+                      torch.zeros((rows, token_budget), dtype=torch.int64, device=device)) if records else None
+        common = dict(
+            sel_ids=st["sel_ids"], sel_count=st["sel_count"], slots=rows_t["slots"], plan=st["plan"],
+            working_lens=st["working_lens"], raw_key=c["raw_k"], raw_value=c["raw_v"], working_key=st["work_k"],
+            working_value=st["work_v"], cos_sin_cache=cos_sin, rotary_dim=d, is_neox_style=True, chunk_size=chunk,
+            history_budget=hb, recent_window=spec.get("window", RECENT_WINDOW), row_active=row_active,
+            gather_records=held_state)
+        retrieve, _ = step.build_step_desc(
+            stages=step.SCORE | step.SELECT | (step.PREFIX if prefix else 0),
+            snapshot=step.VerifierSnapshot(c["query"], c["lse"], c["key_cache"], c["table"], c["scale"]),
+            rows=step.VerifierRows(rows_t["counts"], rows_t["starts"], rows_t["qlens"], rows_t["tlens"], rows),
+            scores=st["scores"], score_partials=st["partials"], committed_lens=None if prefix else rows_t["committed"],
+            workspace=st.get("workspace") if prefix else None, **common)
+        prefill, _ = step.build_step_desc(stages=step.PLAN, snapshot=None, rows=None, scores=None,
+                                          committed_lens=rows_t["committed"], **common)
+        pairs.append((retrieve, prefill, held_state))
+    run = lambda desc: _lib.check(lib.ds_retrieval_step(stream, desc))  # noqa: E731
+    epochs = [step.workspace_epoch(st["workspace"]) for st in states if "workspace" in st]
+    for r, p, _ in pairs:
+        run(r)
+        run(p)
+    torch.cuda.synchronize()
+    single = bool(epochs) and [step.workspace_epoch(st["workspace"]) for st in states if "workspace" in st] != epochs
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(reps)]
+    for i in range(reps):
+        r, p, _ = pairs[i % len(pairs)]
+        ev[i][0].record()
+        run(r)
+        ev[i][1].record()
+        run(p)
+        ev[i][2].record()
+    torch.cuda.synchronize()
+    retrieval_us = statistics.mean(e[0].elapsed_time(e[1]) for e in ev) * 1e3
+    prefill_us = statistics.mean(e[1].elapsed_time(e[2]) for e in ev) * 1e3
+    held = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for i in range(reps):
+        held[i][0].record()
+        run(pairs[i % len(pairs)][1])
+        held[i][1].record()
+    torch.cuda.synchronize()
+    held_us = statistics.mean(a.elapsed_time(b) for a, b in held) * 1e3
+    if single and any(step.workspace_status(st["workspace"]) for st in states):
+        raise RuntimeError("single-launch status words set after the retrieval calls: results not valid")
+    held_tasks = sum(int((rec[1] != 0).sum()) for _, _, rec in pairs if rec is not None) // len(pairs)
+    del pairs
+    return {
+        "retrieval_path": "single launch" if single else "chain",
+        "retrieval_us": round(retrieval_us, 2), "compact_prefill_us": round(prefill_us, 2),
+        "total_us": round(retrieval_us + prefill_us, 2),
+        "compact_prefill_between_retrievals_us": round(held_us, 2),
+        "cycle_us_retrieval_every_4": round((retrieval_us + prefill_us + 3 * held_us) / 4, 2),
+        "held_tasks_per_copy": held_tasks,
+    }
 
 
 def traffic_of(key, spec):
@@ -556,12 +637,11 @@ def workload_leg(name, seed, device, steps=20, with_cpu=True):
     status = [step.workspace_status(st["workspace"]) for st in keep]
     if any(status):
         raise RuntimeError(f"{name}: single-launch status words {status}: results not valid")
-    score_select_us = timed(step.SCORE | step.SELECT, steps)
-    prefill_us = timed(step.PLAN, steps)
     plan_lens = keep[0]["plan"][:, 1].tolist()
     score_bytes, gather_bytes, chain_bytes = algorithmic_bytes(spec, inp, plan_lens, active)
     gbps = chain_bytes / (step_us * 1e-6) / 1e9
-    two_call = score_select_us + prefill_us
+    rt = runtime_path(copies, keep, rows_t, rows, cos_sin, spec, hb, row_active, device, max(10, steps // 2))
+    two_call = rt["total_us"]
     leg = {
         "config": f"{rows} requests" + (f" + {spec['pad']} padding rows" if spec.get("pad") else "")
                   + f", context {spec['lens']}, Hq {spec['hq']} / Hkv {hkv} x {d}, chunk {chunk}, token budget "
@@ -576,9 +656,10 @@ def workload_leg(name, seed, device, steps=20, with_cpu=True):
                  f"{'cold' if gather_bytes * len(copies) > MALL_BYTES else 'warm'} ({len(copies)} rotated copies "
                  f"of {step_bytes / 1e6:.0f} MB and {gather_bytes / 1e6:.0f} MB against the 256 MB MALL)"),
         "copies": len(copies),
-        "runtime_two_calls_us": {"score_select": round(score_select_us, 2), "compact_prefill": round(prefill_us, 2),
-                                 "total": round(two_call, 2),
-                                 "frac": round(chain_bytes / (two_call * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)},
+        "runtime_two_calls_us": dict(rt, frac=round(chain_bytes / (two_call * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                                     without_records=runtime_path(copies, keep, rows_t, rows, cos_sin, spec, hb,
+                                                                  row_active, device, max(10, steps // 2),
+                                                                  records=False)),
     }
     if with_cpu:
         leg["cpu_baseline"] = cpu_sample(spec, inp, cos_sin, hb, active)

@@ -2,10 +2,11 @@
 
 The reference rebuilds every row's working cache from the raw cache at every
 compact prefill (diffspec/runtime.py:1737-1765).  ds355 keeps per-task gather
-records (include/ds355.h) and moves only what changed: the retrieval call
-moves each row's history prefix before the draft's prefill
-(diffspec/proposer.py:211-220, then :256-307), and between retrievals only
-the rolling tail moves.  These tests run whole draft cycles through
+records (include/ds355.h) and moves only what changed: after a retrieval
+every row, between retrievals only the rolling tail.  Optionally the
+retrieval call moves each row's history prefix itself, before the draft's
+prefill (diffspec/proposer.py:211-220, then :256-307), and the compact
+prefill after it the rest.  These tests run whole draft cycles through
 ``DiffSpecDraftCache`` and compare every cycle's working cache with the
 oracle's full per-request rebuild (runtime.py:1683-1711) on the same raw
 cache, bit for bit; draft steps are simulated by writing garbage past each
@@ -32,7 +33,7 @@ class _Rotary:
         self.cos_sin_cache = cos_sin
 
 
-def _cache(cuda, rows, lmax, interval, cos_sin):
+def _cache(cuda, rows, lmax, interval, cos_sin, prefix_at_retrieval=False):
     from ds355 import runtime
 
     settings = runtime.DiffSpecSettings(chunk_size=CHUNK, token_budget=BUDGET, retrieval_interval=interval,
@@ -40,7 +41,8 @@ def _cache(cuda, rows, lmax, interval, cos_sin):
                                         adaptive_profile=False, recent_window=WINDOW)
     return runtime.DiffSpecDraftCache(settings, max_num_reqs=rows, max_model_len=lmax, num_kv_heads=HKV, head_dim=D,
                                       target_num_layers=2, dtype=torch.bfloat16, device=cuda,
-                                      rotary_embedding=_Rotary(cos_sin.to(cuda)))
+                                      rotary_embedding=_Rotary(cos_sin.to(cuda)),
+                                      prefix_at_retrieval=prefix_at_retrieval)
 
 
 def _expected(raw_k, raw_v, slots, committed, selections, cos_sin, shape):
@@ -62,12 +64,14 @@ def _same_history(cache, exp_k, exp_v, slots, roots):
             assert torch.equal(torch.nan_to_num(a), torch.nan_to_num(b)), slot
 
 
-@pytest.mark.parametrize("rows", [10, 4], ids=["single-launch-retrieval", "chain-retrieval"])
-def test_draft_cycles_match_full_rebuilds(cuda, rows):
+@pytest.mark.parametrize("rows,prefix", [(10, True), (4, True), (10, False)],
+                         ids=["prefix-single-launch", "prefix-chain", "rebuild-at-prefill"])
+def test_draft_cycles_match_full_rebuilds(cuda, rows, prefix):
     """Eight draft cycles, retrieval every second one, and a request replaced
     in a reused slot halfway: each cycle's working cache equals the oracle's
     full rebuild of every row, and between retrievals the prefix tasks are
-    recorded as held."""
+    recorded as held.  With ``prefix`` the retrieval call moves each row's
+    history prefix (as one launch with the scoring at 8+ rows)."""
     budget = O.history_budget(BUDGET, 4, CHUNK)
     g = gen(41 + rows)
     lmax = 9000
@@ -75,7 +79,7 @@ def test_draft_cycles_match_full_rebuilds(cuda, rows):
     raw_k = torch.randn((rows, lmax, HKV, D), generator=g).to(torch.bfloat16)
     raw_v = torch.randn((rows, lmax, HKV, D), generator=g).to(torch.bfloat16)
     cos_sin = O.rope_cos_sin_cache(D, BUDGET)
-    cache = _cache(cuda, rows, lmax, 2, cos_sin)
+    cache = _cache(cuda, rows, lmax, 2, cos_sin, prefix_at_retrieval=prefix)
     cache.raw_key.copy_(raw_k)
     cache.raw_value.copy_(raw_v)
     cache.working_key.fill_(float("nan"))

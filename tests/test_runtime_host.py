@@ -101,7 +101,7 @@ def test_retrieval_skips_prefill_snapshot_and_interval(launches):
     cache.accept_target_queries(torch.tensor([1, 1]), is_prefill=False)
     assert len(launches) == 1
     call = launches[0]
-    assert call["stages"] == step.SCORE | step.SELECT | step.PREFIX  # score, select, and the history prefix gather
+    assert call["stages"] == step.SCORE | step.SELECT
     assert _first(call["rows"].counts, call["rows"].batch_size) == [1, 1]
     assert _first(call["rows"].query_start, call["rows"].batch_size) == [0, 1]
     assert _first(call["rows"].query_len, call["rows"].batch_size) == [1, 1]
@@ -323,7 +323,7 @@ def test_linear_call_sequence_of_the_plugin(launches, attention_calls, capture_c
     cache.clear_proposed_tree()
     assert cache.proposed_token_ids is None and cache.proposed_depths_cpu == []
     cache.accept_target_queries(torch.tensor([2, 4]), is_prefill=cache.target_is_prefill)
-    assert launches[-1]["stages"] == step.SCORE | step.SELECT | step.PREFIX
+    assert launches[-1]["stages"] == step.SCORE | step.SELECT
     assert _first(launches[-1]["rows"].counts, 2) == [2, 4]
     assert not cache.target_tree_active  # prepare_inputs_padded returns its result unchanged
     with pytest.raises(RuntimeError, match="tree has not been verified"):

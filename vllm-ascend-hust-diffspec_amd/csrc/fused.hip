@@ -337,12 +337,19 @@ __device__ __forceinline__ void run_task(const gather::GatherArgs& ga, const gat
       });
 }
 
+// Gather record of task t of the row whose slot is `slot` (0 without records
+// or for a slot out of range), requested before the row's plan arrives.
+__device__ __forceinline__ uint64_t task_record(const FusedArgs& f, int slot, int t) {
+  return (f.rec != nullptr && slot >= 0 && slot < f.g.num_slots) ? f.rec[static_cast<int64_t>(slot) * f.rec_stride + t]
+                                                                  : 0u;
+}
+
 // Gather task t of the row in `v`, keeping its gather record: a task whose
 // record shows the working cache already holds its bytes is left out, and
 // with prefix_only so is every task not wholly in the history prefix.
 template <int DT, bool NEOX>
 __device__ __forceinline__ void gather_recorded(const FusedArgs& f, const gather::GatherLane& L, const PlanView& v,
-                                                int r, int t) {
+                                                int r, int t, uint64_t have) {
   const int ppw = 64 / f.g.lanes_per_row;
   const int p0 = t * ppw;
   // Before the draft's prefill, only a row whose prefix sources (all below
@@ -352,10 +359,9 @@ __device__ __forceinline__ void gather_recorded(const FusedArgs& f, const gather
       p0 + ppw <= v.len && early_ok ? gather::prefix_record(p0, ppw, v.prefix_len, v.drop, v.gen) : 0u;
   bool move = !f.prefix_only || want != 0u;
   if (f.rec != nullptr && v.slot >= 0 && v.slot < f.g.num_slots) {
-    uint64_t* rec = f.rec + v.slot * f.rec_stride + t;
-    const uint64_t have = static_cast<uint64_t>(uniform64(static_cast<int64_t>(*rec)));
+    have = static_cast<uint64_t>(uniform64(static_cast<int64_t>(have)));
     if (want != 0u && have == want) move = false;
-    if ((threadIdx.x & 63) == 0 && have != want) *rec = want;
+    if ((threadIdx.x & 63) == 0 && have != want) f.rec[v.slot * f.rec_stride + t] = want;
   }
   if (move) run_task<DT, NEOX>(f.g, L, v, t);
 }
@@ -368,8 +374,8 @@ __device__ __forceinline__ void gather_recorded(const FusedArgs& f, const gather
 // read-modify-writes the wave waits for, so they are in memory before its
 // workgroup counts itself done.
 template <int DT, bool NEOX>
-__device__ __forceinline__ void gather_owned(const FusedArgs& f, const int* task_prefix, int gw, int tw,
-                                             uint32_t tag) {
+__device__ __forceinline__ void gather_owned(const FusedArgs& f, const int* task_prefix, const int* row_slot, int gw,
+                                             int tw, uint32_t tag) {
   const gather::GatherArgs& ga = f.g;
   const int rows = f.p.batch;
   const gather::GatherLane L = gather::gather_lane<DT, NEOX>(ga);
@@ -385,13 +391,14 @@ __device__ __forceinline__ void gather_owned(const FusedArgs& f, const int* task
     }
     hint = lo;
     const int r = __builtin_amdgcn_readfirstlane(lo);
+    const int t = __builtin_amdgcn_readfirstlane(task - task_prefix[r]);
+    const uint64_t have = task_record(f, row_slot[r], t);
     if (r != cur) {
       cur = r;
       published = poll_plan(f, r, tag, f.owner_spins, v);
     }
-    const int t = __builtin_amdgcn_readfirstlane(task - task_prefix[r]);
     if (published) {
-      gather_recorded<DT, NEOX>(f, L, v, r, t);
+      gather_recorded<DT, NEOX>(f, L, v, r, t, have);
     } else if ((threadIdx.x & 63) == 0) {
       __hip_atomic_exchange(f.state + static_cast<int64_t>(r) * f.task_cap + t, tag | kSkipped, __ATOMIC_ACQUIRE,
                             __HIP_MEMORY_SCOPE_AGENT);
@@ -433,7 +440,7 @@ __device__ __forceinline__ void redo_skipped(const FusedArgs& f, const int* task
             break;
           }
         }
-        gather_recorded<DT, NEOX>(f, L, v, b, t0 + k);
+        gather_recorded<DT, NEOX>(f, L, v, b, t0 + k, task_record(f, static_cast<int>(v.slot), t0 + k));
       }
     }
   }
@@ -454,6 +461,7 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
     WorkShared w;
   } lds;
   __shared__ int s_task_prefix[kFusedRows + 1];
+  __shared__ int s_slot[kFusedRows];  // each row's slot (gather records are per slot)
   __shared__ int s_scratch[4];
   __shared__ uint32_t s_tag;
   __shared__ uint32_t s_last;
@@ -477,6 +485,7 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
   RowDesc own{0, 0, 0};
   if (tr < rows) {
     const int slot = f.p.slots[tr];
+    s_slot[tr] = slot;
     const bool gathered = (ga.row_active == nullptr || ga.row_active[tr] != 0) && slot >= 0 && slot < ga.num_slots;
     const int committed = committed_of(f.p.committed_lens, f.p.src, tr);
     if (!selector) own = row_desc(f.s.src, tr);
@@ -502,7 +511,7 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
     const int tw = first_selector * kWaves;
     score::score_stream<DT, STEPS, KB, false, true, true>(sa, w.unit_prefix, w.len, w.qrow, w.unit_prefix[rows], gw,
                                                           tw, tag);
-    gather_owned<DT, NEOX>(f, s_task_prefix, gw, tw, tag);
+    gather_owned<DT, NEOX>(f, s_task_prefix, s_slot, gw, tw, tag);
   }
 
   // The last workgroup to finish hands this launch's status bits to the

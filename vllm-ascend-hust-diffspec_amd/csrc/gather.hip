@@ -159,10 +159,14 @@ __global__ __launch_bounds__(kThreads) void plan_gather_kernel(GatherArgs a, Pla
   const bool writer = blockIdx.x == 0 && wave == 0;
   int count = -1;
   uint32_t lo = 0, hi = 0, gen = 0;
+  uint64_t have = 0;  // the wave's gather record, requested with the selection
   if (slot_ok) {
     const int32_t* ids = ps.sel_ids + static_cast<int64_t>(slot) * ps.sel_stride;
     count = scalar_load(ps.sel_count + slot);
-    if (ps.rec != nullptr) gen = static_cast<uint32_t>(scalar_load(ps.gen + slot));
+    if (ps.rec != nullptr) {
+      gen = static_cast<uint32_t>(scalar_load(ps.gen + slot));
+      have = ps.rec[static_cast<int64_t>(slot) * ps.rec_stride + p0 / ppw];
+    }
     lo = lane < ps.cap ? static_cast<uint32_t>(ids[lane]) : 0u;
     hi = lane + 64 < ps.cap ? static_cast<uint32_t>(ids[lane + 64]) : 0u;
   }
@@ -229,10 +233,9 @@ __global__ __launch_bounds__(kThreads) void plan_gather_kernel(GatherArgs a, Pla
   const uint64_t want = p0 + ppw <= limit && early_ok ? prefix_record(p0, ppw, prefix_len, drop, gen) : 0u;
   bool move = p0 < limit && (!ps.prefix_only || want != 0u);
   if (ps.rec != nullptr) {
-    uint64_t* rec = ps.rec + static_cast<int64_t>(slot) * ps.rec_stride + p0 / ppw;
-    const uint64_t have = static_cast<uint64_t>(uniform64(static_cast<int64_t>(*rec)));
+    have = static_cast<uint64_t>(uniform64(static_cast<int64_t>(have)));
     if (want != 0u && have == want) move = false;
-    if (lane == 0 && have != want) *rec = want;
+    if (lane == 0 && have != want) ps.rec[static_cast<int64_t>(slot) * ps.rec_stride + p0 / ppw] = want;
   }
   if (!move) return;
   const GatherLane L = gather_lane<DT, NEOX>(a);

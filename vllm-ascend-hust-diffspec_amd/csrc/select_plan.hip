@@ -42,6 +42,7 @@ __global__ __launch_bounds__(NT) void select_plan_kernel(SelectArgs a) {
   const bool slot_ok = slot >= 0 && slot < a.num_slots;
   const int committed = a.do_plan ? committed_of(a.committed_lens, a.src, b) : 0;
   const int stored_count = (a.do_plan && slot_ok) ? a.counts[slot] : 0;
+  const int32_t gen0 = (a.gen != nullptr && a.do_select && slot_ok) ? a.gen[slot] : 0;
   const float* part = a.partials + static_cast<int64_t>(b) * a.max_chunks * a.hkv;
   float pre[kPre];
   if (a.do_select && a.partials != nullptr) {
@@ -125,7 +126,7 @@ __global__ __launch_bounds__(NT) void select_plan_kernel(SelectArgs a) {
     for (int j = tid; j < n_sel; j += NT) out[j] = sh.ids[j];
     if (tid == 0) {
       a.counts[slot] = n_sel;
-      if (a.gen != nullptr) a.gen[slot] += 1;  // one row per slot: no other writer
+      if (a.gen != nullptr) a.gen[slot] = gen0 + 1;  // one row per slot: no other writer
     }
   }
 

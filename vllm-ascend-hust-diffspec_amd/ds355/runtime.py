@@ -143,8 +143,10 @@ class _Staging:
 
 
 WORKING_LENS = "working_lens"  # pending positions = the slots' device working lengths
-# The retrieval call: score, select, and gather each row's history prefix.
-RETRIEVAL_STAGES = _step.SCORE | _step.SELECT | _step.PREFIX
+# The retrieval call: score and select; with prefix_at_retrieval also each
+# row's history prefix (one launch for 8+ rows with a supplied LSE).
+RETRIEVAL_STAGES = _step.SCORE | _step.SELECT
+PREFIX_RETRIEVAL_STAGES = _step.SCORE | _step.SELECT | _step.PREFIX
 
 
 class DiffSpecDraftCache:
@@ -178,6 +180,7 @@ class DiffSpecDraftCache:
         target_tensor_parallel_size: int = 1,
         max_batch_rows: int | None = None,
         lse_free_scoring: bool = False,
+        prefix_at_retrieval: bool = False,
     ) -> None:
         if target_tensor_parallel_size < 1:
             raise ValueError("Target tensor parallel size must be positive")
@@ -210,15 +213,19 @@ class DiffSpecDraftCache:
         self.working_lens = torch.zeros((max_num_reqs,), dtype=torch.int32, device=self.device)
         # Gather records (include/ds355.h): each slot's selection generation,
         # and per gather task of its working cache what the cache holds, so
-        # a rebuild moves only what changed.  The retrieval call moves each
-        # row's history prefix (raw rows well before the committed root,
-        # final by then), and the compact prefill after populate_prefill the
-        # rest; between retrievals only the rolling tail moves.
+        # a compact prefill moves only what changed: after a retrieval every
+        # row, between retrievals only the rolling tail.  prefix_at_retrieval
+        # moves each row's history prefix (raw rows well before the committed
+        # root, final by then) in the retrieval call instead, which leaves
+        # the compact prefill after it the tail; measured at 16 rows x 40k
+        # tokens it is about 3% slower over the two calls (the compact
+        # prefill keeps a latency floor of about 8 us), so it is off.
         self.sel_gen = torch.zeros((max_num_reqs,), dtype=torch.int32, device=self.device)
         self.gather_records = torch.zeros((max_num_reqs, settings.token_budget), dtype=torch.int64,
                                           device=self.device)
         self._workspace: torch.Tensor | None = None  # single-launch retrieval, on first use
         self._workspace_heads = 0
+        self.retrieval_stages = PREFIX_RETRIEVAL_STAGES if prefix_at_retrieval else RETRIEVAL_STAGES
 
         self.max_batch_rows = max_batch_rows or max_num_reqs
         self.max_chunks = (max_model_len + settings.chunk_size - 1) // settings.chunk_size
@@ -441,7 +448,7 @@ class DiffSpecDraftCache:
         staged = self._rows_staging.upload([
             starts, [e - s for s, e in zip(starts, ends)], seq_lens[:batch_size], self._active_slots, [],
         ])
-        key = self._step_key(RETRIEVAL_STAGES, batch_size, batch_size, self._cos_sin_cache(),
+        key = self._step_key(self.retrieval_stages, batch_size, batch_size, self._cos_sin_cache(),
                              self._target_query, self._target_lse, self._target_key_cache, self._target_block_tables)
         return self._active_slots, staged, key
 
@@ -519,7 +526,7 @@ class DiffSpecDraftCache:
             counts.copy_(valid_sampled_token_count.reshape(-1)[:batch_size])  # device-side cast, no sync
         started = time.perf_counter()
         q, lse, kc, bt = self._target_query, self._target_lse, self._target_key_cache, self._target_block_tables
-        stages = RETRIEVAL_STAGES
+        stages = self.retrieval_stages
         if key is None:
             key = self._step_key(stages, batch_size, batch_size, self._cos_sin_cache(), q, lse, kc, bt)
         hit = self._step_descs.get(key)

@@ -224,7 +224,7 @@ def build_step_desc(
     _i32("slots", slots)
     if committed_lens is not None:
         _i32("committed_lens", committed_lens, batch_rows)
-    elif not (stages & PREFIX and stages & (SCORE | SELECT)):
+    elif stages & PLAN or (stages & PREFIX and not stages & (SCORE | SELECT)):
         raise ValueError("committed_lens is required (only a PREFIX rebuild with the verifier rows derives it)")
     _i32("sel_ids", sel_ids)
     _i32("sel_count", sel_count, num_slots)

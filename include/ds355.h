@@ -177,8 +177,10 @@ enum ds_stage { DS_STAGE_SCORE = 1, DS_STAGE_SELECT = 2, DS_STAGE_PLAN = 4, DS_S
  * Those read raw rows well before the committed root, which the draft's
  * prefill does not rewrite, so the retrieval call can move them before
  * populate_prefill and the compact prefill then moves only the rest.  Needs
- * gather records (below).  SCORE | SELECT | PREFIX with a workspace runs as
- * the single launch.
+ * gather records (below) and DS_STAGE_SELECT in the same call (it reads the
+ * verifier rows); committed_lens may be NULL (each row's scored length is
+ * used, 0 for rows that committed nothing).  SCORE | SELECT | PREFIX with a
+ * workspace runs as the single launch.
  *
  * Gather records (sel_gen and gather_rec, both or neither): per slot, the
  * selection generation, which every stored selection increments (the caller

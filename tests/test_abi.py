@@ -108,6 +108,17 @@ def test_c_side_validation_reports_reference_messages():
     desc.stages = 16
     assert lib.ds_retrieval_step(None, desc) == _lib.DS_ERR_INVALID
     assert "unknown stage bits" in lib.ds_last_error().decode()
+    # The prefix stage needs gather records, and the selection in the same call.
+    desc.stages = _lib.DS_STAGE_PREFIX
+    assert lib.ds_retrieval_step(None, desc) == _lib.DS_ERR_INVALID
+    assert "needs gather records" in lib.ds_last_error().decode()
+    desc.sel_gen, desc.gather_rec, desc.rec_stride = 64, 64, 1 << 20  # never dereferenced: refused first
+    assert lib.ds_retrieval_step(None, desc) == _lib.DS_ERR_INVALID
+    assert "runs with DS_STAGE_SELECT" in lib.ds_last_error().decode()
+    desc.gather_rec = None
+    desc.stages = _lib.DS_STAGE_PLAN
+    assert lib.ds_retrieval_step(None, desc) == _lib.DS_ERR_INVALID
+    assert "come together" in lib.ds_last_error().decode()
 
 
 def test_lse_free_validation_without_gpu():

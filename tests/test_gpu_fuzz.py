@@ -11,7 +11,10 @@ recent windows of one chunk or more, bf16 or fp16, neox or GPT-J rotation.
 The chain is compared with the oracle (scores to the relative bar, the rest
 bit-exact), the single launch with the chain bit for bit, and the compact
 prefill alone (plan + gather in one launch, from the chain's selections) with
-the chain's plans and working caches bit for bit.
+the chain's plans and working caches bit for bit.  With gather records, the
+retrieval call moving each row's history prefix (the single launch) and the
+compact prefill after it give the chain's plans and working caches bit for
+bit, and a second compact prefill (everything held) changes nothing.
 """
 
 import random
@@ -68,8 +71,23 @@ def test_random_batches_chain_oracle_and_single_launch(cuda, seed):
                    work_v=torch.full_like(chain["work_v"], float("nan")),
                    sel_ids=chain["sel_ids"].clone(), sel_count=chain["sel_count"].clone())
     run_gpu(case, cuda, stages=step.PLAN, state=prefill, recent_window=window)
+    _same_rebuild(chain, prefill)
+    # Gather records: the prefix in the retrieval call, the rest in the compact prefill.
+    records = (torch.zeros((case["num_slots"],), dtype=torch.int32, device=cuda),
+               torch.zeros((case["num_slots"], case["token_budget"]), dtype=torch.int64, device=cuda))
+    held = run_gpu(case, cuda, path="fused", stages=step.SCORE | step.SELECT | step.PREFIX, records=records,
+                   derive_committed=True, recent_window=window)
+    run_gpu(case, cuda, stages=step.PLAN, state=held, records=records, recent_window=window)
+    _same_rebuild(chain, held)
+    assert int((records[1] != 0).sum()) > 0 or max(case["committed"]) < 4 * case["chunk"]
+    again = {k: v.clone() for k, v in held.items() if k in ("plan", "working_lens", "work_k", "work_v")}
+    run_gpu(case, cuda, stages=step.PLAN, state=held, records=records, recent_window=window)
+    _same_rebuild(again, held)
+
+
+def _same_rebuild(want, got):
     for key in ("plan", "working_lens", "work_k", "work_v"):
-        x, y = chain[key], prefill[key]
+        x, y = want[key], got[key]
         if x.dtype.is_floating_point:
             x, y = torch.nan_to_num(x), torch.nan_to_num(y)
         assert torch.equal(x, y), key

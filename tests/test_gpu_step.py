@@ -59,7 +59,7 @@ def path(request):
 
 
 def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="chain", single_launch=None,
-            lse_free=False, flags=0, expect_status=0, recent_window=None):
+            lse_free=False, flags=0, expect_status=0, recent_window=None, records=None, derive_committed=False):
     from ds355 import step
 
     i32 = lambda xs: torch.tensor(xs, dtype=torch.int32, device=device)  # noqa: E731
@@ -84,7 +84,7 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="cha
     if lse_free and "lse_partials" not in state:
         state["lse_partials"] = torch.zeros((rows, case["hq"], max_chunks, 2), dtype=torch.float32, device=device)
         state["lse_out"] = torch.full((rows, case["hq"]), float("nan"), dtype=torch.float32, device=device)
-    fused = path == "fused" and (stages is None or stages == step.ALL)
+    fused = path == "fused" and (stages is None or stages in (step.ALL, step.SCORE | step.SELECT | step.PREFIX))
     if fused and "workspace" not in state:
         state["workspace"] = step.new_workspace(rows, state["scores"].shape[1], case["hkv"], case["token_budget"],
                                                 device)
@@ -96,14 +96,15 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="cha
         rows=step.VerifierRows(i32(case["counts"]), i32(case["starts"]), i32(case["qlens"]), i32(case["tlens"]),
                                case["real_rows"]),
         scores=state["scores"], score_partials=state["partials"], sel_ids=state["sel_ids"], sel_count=state["sel_count"], slots=i32(case["slots"]),
-        committed_lens=i32(case["committed"]), plan=state["plan"], working_lens=state["working_lens"],
+        committed_lens=None if derive_committed else i32(case["committed"]), plan=state["plan"],
+        working_lens=state["working_lens"],
         raw_key=state["raw_k"], raw_value=state["raw_v"], working_key=state["work_k"],
         working_value=state["work_v"], cos_sin_cache=state["cos_sin"], rotary_dim=case["head_dim"],
         is_neox_style=case["neox"], chunk_size=case["chunk"], history_budget=case["budget"],
         recent_window=recent_window, row_active=None if row_active is None else i32(row_active),
         workspace=state.get("workspace") if fused else None,
         lse_partials=state.get("lse_partials") if lse_free else None,
-        lse_out=state.get("lse_out") if lse_free else None, flags=flags,
+        lse_out=state.get("lse_out") if lse_free else None, flags=flags, gather_records=records,
     )
     torch.cuda.synchronize()
     if fused:  # the single launch ran (epoch + 1) or, for other shapes, the chain did

@@ -60,11 +60,14 @@ int retrieval_step(hipStream_t stream, const ds_step_desc* d, uint32_t* status_o
   const bool records = d->gather_rec != nullptr;
   // A prefix-only rebuild leaves the working lengths to the compact prefill.
   int32_t* const working_lens = prefix ? nullptr : d->working_lens;
-  DS_REQUIRE(!rebuild || d->committed_lens != nullptr || (prefix && d->counts != nullptr),
-             "the plan needs committed_lens (or, for DS_STAGE_PREFIX, the verifier rows)");
   DS_REQUIRE(records == (d->sel_gen != nullptr), "sel_gen and gather_rec come together");
   DS_REQUIRE(!prefix || records, "DS_STAGE_PREFIX needs gather records (sel_gen, gather_rec)");
+  // The prefix stage reads each row's verifier rows (which raw rows the
+  // draft's prefill rewrites): it comes with the selection, in the retrieval call.
+  DS_REQUIRE(!prefix || select, "DS_STAGE_PREFIX runs with DS_STAGE_SELECT (it needs the verifier rows)");
   if (records) DS_REQUIRE(d->rec_stride >= d->token_budget, "gather record row stride is smaller than token_budget");
+  DS_REQUIRE(!rebuild || d->committed_lens != nullptr || prefix,
+             "the plan needs committed_lens (or, for DS_STAGE_PREFIX, the verifier rows)");
   DS_REQUIRE(d->batch_rows >= 0 && d->batch_size >= 0 && d->batch_size <= d->batch_rows,
              "batch_size must be between zero and batch_rows");
   DS_REQUIRE(d->chunk_size > 0 && d->history_budget >= d->chunk_size && d->history_budget % d->chunk_size == 0,

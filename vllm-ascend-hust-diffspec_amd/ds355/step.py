@@ -205,6 +205,8 @@ def build_step_desc(
         raise ValueError(f"unknown stage bits {stages:#x}")
     if stages & PREFIX and gather_records is None:
         raise ValueError("the PREFIX stage needs gather records")
+    if stages & PREFIX and not stages & SELECT:
+        raise ValueError("the PREFIX stage runs with SELECT (it needs the verifier rows)")
     uses_rows = bool(stages & (SCORE | SELECT))
     batch_rows = slots.numel()
     num_slots, max_model_len, heads, head_dim = raw_key.shape
@@ -224,7 +226,7 @@ def build_step_desc(
     _i32("slots", slots)
     if committed_lens is not None:
         _i32("committed_lens", committed_lens, batch_rows)
-    elif stages & PLAN or (stages & PREFIX and not stages & (SCORE | SELECT)):
+    elif stages & PLAN:
         raise ValueError("committed_lens is required (only a PREFIX rebuild with the verifier rows derives it)")
     _i32("sel_ids", sel_ids)
     _i32("sel_count", sel_count, num_slots)

@@ -434,3 +434,25 @@ def test_rows_staged_with_the_snapshot_follow_the_active_slots(monkeypatch):
     cache.set_active_requests(["b", "a"])  # reordered after the snapshot: the rows are staged again
     cache.accept_target_queries(torch.tensor([1, 1], dtype=torch.int32), is_prefill=False)
     assert seen[-1] == ("launched", [0, 1], [1, 1], [7, 8], slots_ab[::-1])
+
+
+def test_gather_records_follow_the_slot_map(launches):
+    """A request leaving its slot changes that slot's selection generation (its
+    gather records describe the request that left); slots that keep their
+    request keep theirs.  Every rebuild passes the cache's records, and the
+    retrieval call moves the history prefix only with prefix_at_retrieval."""
+    cache = _cache()
+    cache.set_active_requests(["a", "b", "c"])
+    assert cache.sel_gen.tolist() == [0, 0, 0, 0]
+    cache.sel_gen[:] = torch.tensor([5, 6, 7, 0], dtype=torch.int32)
+    cache.set_active_requests(["c", "a"])  # b leaves slot 1
+    assert cache.sel_gen.tolist() == [5, 7, 7, 0]
+    assert cache.sel_count[1].item() == -1
+    cache.set_active_requests(["c", "a", "d"])  # d takes the freed slot with a new generation
+    assert cache._request_slots["d"] == 1 and cache.sel_gen.tolist() == [5, 7, 7, 0]
+    cache.prepare_compact_prefill(None, 3, committed_seq_lens=[9, 9, 9])
+    gen, records = launches[-1]["gather_records"]
+    assert launches[-1]["stages"] == step.PLAN
+    assert gen.tolist() == cache.sel_gen.tolist() and records.shape == cache.gather_records.shape
+    assert runtime.RETRIEVAL_STAGES == step.SCORE | step.SELECT
+    assert _cache(prefix_at_retrieval=True).retrieval_stages == step.SCORE | step.SELECT | step.PREFIX

@@ -473,13 +473,17 @@ ATTENTION_COPIES = 6  # working caches rotated per launch: 6 x 67 MB exceeds the
 def runtime_path(copies, states, rows_t, rows, cos_sin, spec, hb, row_active, device, reps, prefix=False,
                  records=True):
     """The plugin's own calls with gather records, as DiffSpecDraftCache makes
-    them: the retrieval call (SCORE | SELECT; with ``prefix`` also each row's
-    history prefix, one launch for 8+ rows) and the compact prefill after it
-    (PLAN: plans and the gather of what the records do not hold), then the
-    compact prefill of a cycle between retrievals (selections unchanged: the
-    rolling tail).  HIP events around each launch, input copies rotated; per
-    copy its own selection generations and records (``records=False``: the
-    same calls without them, every compact prefill moving every row)."""
+    them at the reference's cadence: a retrieval call (SCORE | SELECT; with
+    ``prefix`` also each row's history prefix, one launch for 8+ rows) and
+    the compact prefill after it (PLAN: plans and the gather of what the
+    records do not hold), then the compact prefills of the three cycles up to
+    the next retrieval, each at roots advanced by 0-4 tokens per row (the
+    accepted drafts; seeded).  The selections stay; the rolling tail moves,
+    and a row whose history prefix shifts (its prefix drop changes as the
+    window slides over a selected chunk) moves whole.  HIP events around each
+    launch, input copies rotated; per copy its own selection generations and
+    records (``records=False``: the same calls without them, every compact
+    prefill moving every row)."""
     import torch
 
     from ds355 import _lib, step
@@ -513,24 +517,27 @@ def runtime_path(copies, states, rows_t, rows, cos_sin, spec, hb, row_active, de
         run(p)
     torch.cuda.synchronize()
     single = bool(epochs) and [step.workspace_epoch(st["workspace"]) for st in states if "workspace" in st] != epochs
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(reps)]
+    # Roots of the three cycles after a retrieval: + 0-4 accepted tokens per cycle and row.
+    g = torch.Generator().manual_seed(11)
+    base = rows_t["committed"]
+    step_len = torch.randint(0, DRAFT_TOKENS + 1, (base.numel(),), generator=g).to(base.device, base.dtype)
+    roots = [base] + [base + k * step_len for k in (1, 2, 3)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(reps)]
     for i in range(reps):
         r, p, _ = pairs[i % len(pairs)]
         ev[i][0].record()
         run(r)
-        ev[i][1].record()
-        run(p)
-        ev[i][2].record()
+        for k, root in enumerate(roots):
+            ev[i][k + 1].record()
+            p.committed_lens = root.data_ptr()
+            run(p)
+        ev[i][5].record()
     torch.cuda.synchronize()
+    for _, p, _ in pairs:
+        p.committed_lens = base.data_ptr()
     retrieval_us = statistics.mean(e[0].elapsed_time(e[1]) for e in ev) * 1e3
     prefill_us = statistics.mean(e[1].elapsed_time(e[2]) for e in ev) * 1e3
-    held = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    for i in range(reps):
-        held[i][0].record()
-        run(pairs[i % len(pairs)][1])
-        held[i][1].record()
-    torch.cuda.synchronize()
-    held_us = statistics.mean(a.elapsed_time(b) for a, b in held) * 1e3
+    held_us = statistics.mean(e[k].elapsed_time(e[k + 1]) for e in ev for k in (2, 3, 4)) * 1e3
     if single and any(step.workspace_status(st["workspace"]) for st in states):
         raise RuntimeError("single-launch status words set after the retrieval calls: results not valid")
     held_tasks = sum(int((rec[1] != 0).sum()) for _, _, rec in pairs if rec is not None) // len(pairs)
@@ -542,6 +549,7 @@ def runtime_path(copies, states, rows_t, rows, cos_sin, spec, hb, row_active, de
         "compact_prefill_between_retrievals_us": round(held_us, 2),
         "cycle_us_retrieval_every_4": round((retrieval_us + prefill_us + 3 * held_us) / 4, 2),
         "held_tasks_per_copy": held_tasks,
+        "roots_advance_per_cycle": "0-4 tokens per row (seeded)",
     }
 
 

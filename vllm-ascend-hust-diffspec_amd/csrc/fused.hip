@@ -419,9 +419,9 @@ __device__ __forceinline__ void redo_skipped(const FusedArgs& f, const int* task
   for (int b = 0; b < f.p.batch; ++b) {
     const int tasks = task_prefix[b + 1] - task_prefix[b];
     const uint32_t* st = f.state + static_cast<int64_t>(b) * f.task_cap;
-    bool have_plan = false;
+    bool have_plan = false, failed = false;  // a plan that never came is waited for once per row
     PlanView v{};
-    for (int t0 = static_cast<int>(threadIdx.x >> 6) * 64; t0 < tasks; t0 += kThreads) {
+    for (int t0 = static_cast<int>(threadIdx.x >> 6) * 64; t0 < tasks && !failed; t0 += kThreads) {
       const int t = t0 + lane;
       const uint32_t s = t < tasks ? coherent_load(st + t) : 0u;
       uint64_t skipped = __ballot(s == (tag | kSkipped));
@@ -437,6 +437,7 @@ __device__ __forceinline__ void redo_skipped(const FusedArgs& f, const int* task
                 __hip_atomic_fetch_or(f.status_out, kStatusTasks, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
               }
             }
+            failed = true;
             break;
           }
         }

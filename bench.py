@@ -325,7 +325,7 @@ def run(args):
     # a second small kernel merges them; such a step always runs the chain.
     free_descs = []
     for inp, st in zip(copies, states):
-        st["lse_partials"] = torch.zeros((total_rows, spec["hq"], max_chunks, 2), dtype=torch.float32, device=device)
+        st["lse_partials"] = torch.zeros((total_rows, max_chunks, spec["hq"], 2), dtype=torch.float32, device=device)
         st["lse_out"] = torch.zeros((total_rows, spec["hq"]), dtype=torch.float32, device=device)
         desc, _ = step.build_step_desc(
             snapshot=step.VerifierSnapshot(inp["query"], None, inp["key_cache"], inp["table"], inp["scale"]),

@@ -244,7 +244,7 @@ typedef struct ds_step_desc {
   /* scoring without a supplied LSE (lse == NULL): the pass computes each
    * query head's LSE over the row's scored tokens (the reference's
    * chunk_attention_scores with softmax_lse=None, diffspec/runtime.py:321-322) */
-  float* lse_partials;               /* [batch_rows, Hq, max_chunks, 2] fp32 scratch; required when lse == NULL */
+  float* lse_partials;               /* [batch_rows, max_chunks, Hq, 2] fp32 scratch; required when lse == NULL */
   float* lse_out;                    /* [batch_rows, Hq] natural-log LSE of each scored row; required when lse == NULL */
   int64_t lse_out_stride;            /* elements between rows of lse_out */
   int flags;                         /* DS_STEP_* bits; 0 for normal use */

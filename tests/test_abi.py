@@ -153,7 +153,7 @@ def test_lse_free_validation_without_gpu():
     desc.max_chunks, desc.scores, desc.score_partials = 4, fake, fake
     desc.num_kv_heads, desc.num_q_heads = 2, 8
     assert lib.ds_retrieval_step(None, desc) == _lib.DS_ERR_INVALID
-    msg = ("without a softmax LSE the step needs lse_partials ([batch_rows, Hq, max_chunks, 2] fp32) and "
+    msg = ("without a softmax LSE the step needs lse_partials ([batch_rows, max_chunks, Hq, 2] fp32) and "
            "lse_out ([batch_rows, Hq] fp32)")
     assert lib.ds_last_error().decode() == msg
     desc.lse_partials = fake  # the LSE output is required too

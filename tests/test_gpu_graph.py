@@ -140,7 +140,7 @@ def test_retrieval_step_replayed_from_a_graph(cuda, path):
         if path == "fused":
             st["workspace"] = step.new_workspace(rows, max_chunks, 4, 2048, cuda)
         if path == "lse-free":
-            st["lse_partials"] = torch.zeros((rows, 32, max_chunks, 2), dtype=torch.float32, device=cuda)
+            st["lse_partials"] = torch.zeros((rows, max_chunks, 32, 2), dtype=torch.float32, device=cuda)
             st["lse_out"] = torch.full((rows, 32), float("nan"), dtype=torch.float32, device=cuda)
         return st
 

@@ -186,13 +186,16 @@ def test_lse_free_large_logits_stay_finite(cuda):
     assert_scores_close(actual, expected)
 
 
-def test_lse_free_long_rows_take_wider_slices(cuda):
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (12, 2), (16, 1), (6, 6)])
+def test_lse_free_long_rows_take_wider_slices(cuda, hq, hkv):
     """Rows of up to 2500 chunks: a (row, KV head) finalizes in at most 8 workgroups, so each
-    takes slices wider than its 256 threads (chunks t and t + 256 of the slice)."""
+    takes slices wider than its 256 threads (chunks t and t + 256 of the slice).  Past 1024
+    chunks per row the LSE merge loads two heads' pairs at once: groups of 4 and 16 heads
+    (2 and 8 lane phases), 6 (3 phases, one block of lanes each) and 1 (one head per load)."""
     g = gen(13)
     lengths = [40000, 23000, 17, 4097, 16 * 1024 + 1]
-    query = randn((len(lengths), 8, 64), torch.bfloat16, g)
-    key_cache, table = paged_keys(lengths, 2, 64, 256, torch.bfloat16, g)
+    query = randn((len(lengths), hq, 64), torch.bfloat16, g)
+    key_cache, table = paged_keys(lengths, hkv, 64, 256, torch.bfloat16, g)
     scale = default_scale(64)
     actual = _gpu_scores(query, key_cache, None, table, lengths, 16, scale, cuda)
     expected = O.paged_chunk_attention_scores(query, key_cache, None, table, torch.tensor(lengths), chunk_size=16,

@@ -82,7 +82,7 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="cha
         )
         state["work_v"] = torch.full_like(state["work_k"], float("nan"))
     if lse_free and "lse_partials" not in state:
-        state["lse_partials"] = torch.zeros((rows, case["hq"], max_chunks, 2), dtype=torch.float32, device=device)
+        state["lse_partials"] = torch.zeros((rows, max_chunks, case["hq"], 2), dtype=torch.float32, device=device)
         state["lse_out"] = torch.full((rows, case["hq"]), float("nan"), dtype=torch.float32, device=device)
     fused = path == "fused" and (stages is None or stages in (step.ALL, step.SCORE | step.SELECT | step.PREFIX))
     if fused and "workspace" not in state:

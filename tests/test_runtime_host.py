@@ -146,7 +146,7 @@ def test_snapshot_without_lse(launches):
     cache.accept_target_queries(torch.ones(2), is_prefill=False)
     call = launches[-1]
     assert call["snapshot"].lse is None
-    assert call["lse_partials"].shape == (2, 2, cache.max_chunks, 2)
+    assert call["lse_partials"].shape == (2, cache.max_chunks, 2, 2)
     assert call["lse_out"].shape == (2, 2) and cache.scored_lse.shape == (cache.max_batch_rows, 2)
     # A supplied LSE is still used when there is one; no pair buffers are passed.
     cache.begin_target_forward(["a", "b"])

@@ -52,7 +52,7 @@ def _run_static(case, device, *, lse_free):
     st["work_v"] = torch.full_like(st["work_k"], float("nan"))
     # build_step_desc validates caller scratch; the static entry point does not use it.
     dummy_partials = torch.empty((rows, max_chunks, case["hkv"]), dtype=torch.float32, device=device)
-    dummy_pairs = torch.empty((rows, case["hq"], max_chunks, 2), dtype=torch.float32, device=device)
+    dummy_pairs = torch.empty((rows, max_chunks, case["hq"], 2), dtype=torch.float32, device=device)
     keep = dict(query=case["query"].to(device), lse=case["lse"].to(device), key_cache=case["key_cache"].to(device),
                 table=case["table"].to(device), raw_k=case["raw_k"].to(device), raw_v=case["raw_v"].to(device),
                 cos_sin=case["cos_sin"].to(device), counts=i32(case["counts"]), starts=i32(case["starts"]),

@@ -103,10 +103,10 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(const float* __restr
 // workgroup per (row, KV head, slice of finalize_slice(max_chunks) chunks:
 // 128, more when a row would need more than kMaxSlices slices).
 //   - Each query head of the group merges all of the row's (max, sum) pairs
-//     into its LSE.  A head's pairs are contiguous: tph threads per head
-//     stream them with kLseLoads loads in flight and merge by lane shuffles
-//     (and LDS when a head spans several waves).  The slice-0 workgroup
-//     writes the LSEs (natural log) to lse_out.
+//     into its LSE.  A chunk's pairs are contiguous ([row, chunk, Hq]): tph
+//     threads per head stream them with kLseLoads loads in flight and merge
+//     by lane shuffles (and LDS when a head spans several waves).  The
+//     slice-0 workgroup writes the LSEs (natural log) to lse_out.
 //   - Then the KV head's partial of every chunk of the slice, sum over the
 //     group's heads of z * 2^(m - lse), which selection and the drop-in
 //     finalize read as with a supplied LSE.  The exponent uses the LSE as
@@ -117,6 +117,7 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(const float* __restr
 constexpr int kLseLoads = 16;
 constexpr int kFinalizeSlice = 128;  // chunks per workgroup, at least
 constexpr int kMaxSlices = 8;        // workgroups per (row, KV head), at most
+constexpr int kWideFinalizeChunks = 1024;  // 16-byte pair loads above this many chunks per row
 __host__ __device__ inline int finalize_slice(int max_chunks) {
   const int even = (max_chunks + kMaxSlices - 1) / kMaxSlices;
   return even > kFinalizeSlice ? even : kFinalizeSlice;
@@ -124,8 +125,8 @@ __host__ __device__ inline int finalize_slice(int max_chunks) {
 __global__ __launch_bounds__(kThreads) void lse_finalize_kernel(const float* __restrict__ mz, RowSource src,
                                                                 int max_chunks, int hq, int hkv, int chunk,
                                                                 float* __restrict__ lse_out, int64_t lse_stride,
-                                                                float* __restrict__ partial) {
-  __shared__ float s_m[kThreads], s_z[kThreads];
+                                                                float* __restrict__ partial, int wide) {
+  __shared__ float s_m[2][kThreads], s_z[2][kThreads];
   __shared__ float s_lse2[kMaxGroup];
   const int slice = finalize_slice(max_chunks);
   const int slices = (max_chunks + slice - 1) / slice;
@@ -140,33 +141,80 @@ __global__ __launch_bounds__(kThreads) void lse_finalize_kernel(const float* __r
   const int c_end = min(chunks, c_begin + slice);
   const int G = hq / hkv;
   const int t = threadIdx.x;
-  const float2* pairs = reinterpret_cast<const float2*>(mz) + (static_cast<int64_t>(b) * hq + g * G) * max_chunks;
+  // Pairs [row, chunk, Hq]: head h of this group's chunk c at pairs[c * hq + h].
+  const float2* pairs = reinterpret_cast<const float2*>(mz) + static_cast<int64_t>(b) * max_chunks * hq + g * G;
 
-  int tph = 1;  // threads per head: a power of two, tph * G <= kThreads
-  while (tph * 2 * G <= kThreads) tph *= 2;
-  const int hl = t / tph, j = t % tph;
-  float m = -INFINITY, z = 0.f;
-  if (hl < G) {
-    const float2* p = pairs + static_cast<int64_t>(hl) * max_chunks;
-    for (int c0 = j; c0 < chunks; c0 += kLseLoads * tph) {
-      float2 v[kLseLoads];
+  // P phases cover a chunk's G pairs, hp heads each: one 16-byte load of two
+  // adjacent heads (hp = 2: `wide`, G even) or one 8-byte load.  The host
+  // asks for wide loads on rows of thousands of chunks, where they halve the
+  // load rounds of the merge (17.6 against 20.4 us on 4 x 128k tokens in
+  // 32-token chunks); on shorter rows the extra lane merges of a second head
+  // cost more than they save (7.2 against 6.3 us on 16 x 40k in 64-token
+  // chunks).  With P a power of two consecutive lanes take consecutive phases,
+  // so a wave reads whole runs of the chunk's pairs; otherwise each phase
+  // takes tpp adjacent lanes.  tpp = threads per phase (a power of two,
+  // tpp * P <= kThreads), lstep = lane distance between threads of one
+  // phase, lanes = how many of them one wave holds.
+  const int hp = wide && G % 2 == 0 ? 2 : 1;
+  const int P = G / hp;
+  const bool inter = (P & (P - 1)) == 0;
+  int tpp = 1;
+  while (tpp * 2 * P <= kThreads) tpp *= 2;
+  const int ph = inter ? (t & (P - 1)) : t / tpp;
+  const int j = inter ? t / P : t % tpp;
+  const int lstep = inter ? P : 1;
+  const int lanes = inter ? 64 / P : (tpp < 64 ? tpp : 64);
+  float m0 = -INFINITY, z0 = 0.f, m1 = -INFINITY, z1 = 0.f;
+  if (ph < P) {
+    if (hp == 2) {  // workgroup-uniform
+      const float4* p = reinterpret_cast<const float4*>(pairs + 2 * ph);
+      const int64_t cs = hq / 2;
+      for (int c0 = j; c0 < chunks; c0 += kLseLoads * tpp) {
+        float4 v[kLseLoads];
 #pragma unroll
-      for (int u = 0; u < kLseLoads; ++u) {
-        const int c = c0 + u * tph;
-        v[u] = c < chunks ? p[c] : make_float2(-INFINITY, 0.f);
+        for (int u = 0; u < kLseLoads; ++u) {
+          const int c = c0 + u * tpp;
+          v[u] = c < chunks ? p[static_cast<int64_t>(c) * cs] : make_float4(-INFINITY, 0.f, -INFINITY, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < kLseLoads; ++u) {
+          merge_mz(m0, z0, v[u].x, v[u].y);
+          merge_mz(m1, z1, v[u].z, v[u].w);
+        }
       }
+    } else {
+      const float2* p = pairs + ph;
+      for (int c0 = j; c0 < chunks; c0 += kLseLoads * tpp) {
+        float2 v[kLseLoads];
 #pragma unroll
-      for (int u = 0; u < kLseLoads; ++u) merge_mz(m, z, v[u].x, v[u].y);
+        for (int u = 0; u < kLseLoads; ++u) {
+          const int c = c0 + u * tpp;
+          v[u] = c < chunks ? p[static_cast<int64_t>(c) * hq] : make_float2(-INFINITY, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < kLseLoads; ++u) merge_mz(m0, z0, v[u].x, v[u].y);
+      }
     }
   }
-  const int span = tph < 64 ? tph : 64;
-  for (int off = 1; off < span; off <<= 1) merge_mz(m, z, __shfl_xor(m, off, 64), __shfl_xor(z, off, 64));
-  s_m[t] = m;
-  s_z[t] = z;
+  for (int off = lstep; off < lstep * lanes; off <<= 1) {
+    merge_mz(m0, z0, __shfl_xor(m0, off, 64), __shfl_xor(z0, off, 64));
+    if (hp == 2) merge_mz(m1, z1, __shfl_xor(m1, off, 64), __shfl_xor(z1, off, 64));
+  }
+  s_m[0][t] = m0;
+  s_z[0][t] = z0;
+  s_m[1][t] = m1;
+  s_z[1][t] = z1;
   __syncthreads();
   if (t < G) {
+    // Head t is half t % hp of phase t / hp; one merged pair per wave of the
+    // phase: lane (phase) of every wave, or the first lane of each 64-lane
+    // block of the phase's tpp lanes.
+    const int q = t / hp, half = t % hp;
     float mh = -INFINITY, zh = 0.f;
-    for (int k = 0; k < tph; k += 64) merge_mz(mh, zh, s_m[t * tph + k], s_z[t * tph + k]);
+    for (int k = 0; k < tpp; k += lanes) {
+      const int at = inter ? (k / lanes) * 64 + q : q * tpp + k;
+      merge_mz(mh, zh, s_m[half][at], s_z[half][at]);
+    }
     const float lse2 = zh > 0.f ? mh + __log2f(zh) : -INFINITY;
     const float lse = lse2 * 0.69314718055994530942f;
     if (s == 0) lse_out[static_cast<int64_t>(b) * lse_stride + g * G + t] = lse;
@@ -176,9 +224,17 @@ __global__ __launch_bounds__(kThreads) void lse_finalize_kernel(const float* __r
 
   for (int c = c_begin + t; c < c_end; c += kThreads) {
     float2 v[kMaxGroup];
+    const float2* at = pairs + static_cast<int64_t>(c) * hq;
+    if (hp == 2) {
 #pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h) {
-      v[h] = h < G ? pairs[static_cast<int64_t>(h) * max_chunks + c] : make_float2(-INFINITY, 0.f);
+      for (int h = 0; h < kMaxGroup; h += 2) {
+        const float4 w = h < G ? *reinterpret_cast<const float4*>(at + h) : make_float4(-INFINITY, 0.f, -INFINITY, 0.f);
+        v[h] = make_float2(w.x, w.y);
+        v[h + 1] = make_float2(w.z, w.w);
+      }
+    } else {
+#pragma unroll
+      for (int h = 0; h < kMaxGroup; ++h) v[h] = h < G ? at[h] : make_float2(-INFINITY, 0.f);
     }
     float sum = 0.f;
 #pragma unroll
@@ -362,7 +418,8 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
   int rc2 = check_launch("ds_chunk_scores");
   if (rc2 != DS_OK || !lse_free) return rc2;
   lse_finalize_kernel<<<static_cast<unsigned>(partial_grid), kThreads, 0, stream>>>(
-      a.mz, a.src, max_chunks, num_q_heads, num_kv_heads, chunk_size, lse_out, lse_out_stride, partial);
+      a.mz, a.src, max_chunks, num_q_heads, num_kv_heads, chunk_size, lse_out, lse_out_stride, partial,
+      (reinterpret_cast<uintptr_t>(a.mz) & 15u) == 0 && max_chunks > kWideFinalizeChunks ? 1 : 0);
   return check_launch("ds_chunk_scores lse");
 }
 

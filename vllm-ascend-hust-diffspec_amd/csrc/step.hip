@@ -91,7 +91,7 @@ int retrieval_step(hipStream_t stream, const ds_step_desc* d, uint32_t* status_o
   }
   if (score) {
     DS_REQUIRE(d->lse != nullptr || (d->lse_partials != nullptr && d->lse_out != nullptr),
-               "without a softmax LSE the step needs lse_partials ([batch_rows, Hq, max_chunks, 2] fp32) and "
+               "without a softmax LSE the step needs lse_partials ([batch_rows, max_chunks, Hq, 2] fp32) and "
                "lse_out ([batch_rows, Hq] fp32)");
   }
   src.max_len = static_cast<int>(std::min<int64_t>(static_cast<int64_t>(d->max_chunks) * d->chunk_size, INT32_MAX));

@@ -233,7 +233,7 @@ class DiffSpecDraftCache:
         self.scores = torch.zeros((rows, self.max_chunks), dtype=torch.float32, device=self.device)
         self._score_partials: torch.Tensor | None = None  # [rows, max_chunks, target KV heads], on first use
         self.lse_free_scoring = lse_free_scoring
-        # Without a snapshot LSE: (max, sum) pairs [rows, Hq, max_chunks, 2]
+        # Without a snapshot LSE: (max, sum) pairs [rows, max_chunks, Hq, 2]
         # and the computed natural-log LSE [rows, Hq], on first use.
         self._lse_partials: torch.Tensor | None = None
         self.scored_lse: torch.Tensor | None = None
@@ -852,8 +852,8 @@ class DiffSpecDraftCache:
         lse_partials = lse_out = None
         if stages & _step.SCORE and snapshot.lse is None:
             q_heads = snapshot.query.shape[1]
-            if self._lse_partials is None or self._lse_partials.shape[1] != q_heads:
-                self._lse_partials = torch.zeros((self.max_batch_rows, q_heads, self.max_chunks, 2),
+            if self._lse_partials is None or self._lse_partials.shape[2] != q_heads:
+                self._lse_partials = torch.zeros((self.max_batch_rows, self.max_chunks, q_heads, 2),
                                                  dtype=torch.float32, device=self.device)
                 self.scored_lse = torch.zeros((self.max_batch_rows, q_heads), dtype=torch.float32,
                                               device=self.device)

@@ -180,8 +180,8 @@ def build_step_desc(
     gathers.  ``workspace`` (from ``new_workspace``) lets a full step run as
     one launch when its shapes allow it; the results are the same.
 
-    Without a snapshot LSE, SCORE needs ``lse_partials`` (``[batch_rows, Hq,
-    max_chunks, 2]`` fp32 scratch: each chunk's (max, sum) per query head)
+    Without a snapshot LSE, SCORE needs ``lse_partials`` (``[batch_rows,
+    max_chunks, Hq, 2]`` fp32 scratch: each chunk's (max, sum) per query head)
     and ``lse_out`` (``[batch_rows, Hq]`` fp32, where each scored row's
     natural-log LSE is written); such a step runs as the kernel chain.
 
@@ -275,9 +275,9 @@ def build_step_desc(
         if lse is None and stages & SCORE:
             hq = q.shape[1]
             if (lse_partials is None or lse_partials.dtype != torch.float32 or not lse_partials.is_contiguous()
-                    or lse_partials.shape != (batch_rows, hq, scores.shape[1], 2)):
+                    or lse_partials.shape != (batch_rows, scores.shape[1], hq, 2)):
                 raise ValueError("without a softmax LSE, lse_partials must be a contiguous fp32 "
-                                 "[batch_rows, query_heads, max_chunks, 2] buffer")
+                                 "[batch_rows, max_chunks, query_heads, 2] buffer")
             if lse_out is None or (lse_out.dtype != torch.float32 or lse_out.ndim != 2
                                    or lse_out.shape != (batch_rows, hq) or lse_out.stride(1) != 1):
                 raise ValueError("without a softmax LSE, lse_out must be fp32 [batch_rows, query_heads] "

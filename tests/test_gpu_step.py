@@ -264,12 +264,14 @@ def test_stage_split_equals_full_chain(cuda, path):
         assert torch.equal(torch.nan_to_num(split[key]), torch.nan_to_num(full[key])), key
 
 
-@pytest.mark.parametrize("seed,hq,hkv,head_dim,chunk,block_size", [(4, 32, 4, 128, 64, 128), (6, 16, 2, 64, 32, 64)])
+@pytest.mark.parametrize("seed,hq,hkv,head_dim,chunk,block_size", [(4, 32, 4, 128, 64, 128), (6, 16, 2, 64, 32, 64),
+                                                                   (7, 12, 2, 64, 64, 128), (8, 64, 8, 64, 128, 128)])
 def test_lse_free_step_equals_supplied_lse(cuda, path, seed, hq, hkv, head_dim, chunk, block_size):
     """Without a snapshot LSE the step computes each committed query's LSE over its
     scored tokens: the same normaliser the verifier's attention returns, so
     scores, selection, plans and working cache match the oracle with the exact
-    LSE, and lse_out equals that LSE."""
+    LSE, and lse_out equals that LSE (groups of 8, 8, 6 and 8 query heads; 64 heads
+    over 8 KV heads in the last case)."""
     g = gen(seed)
     lens = [int(x) for x in torch.randint(3000, 30000, (12,), generator=g)]
     counts = [int(x) for x in torch.randint(0, 6, (12,), generator=g)]

@@ -10,6 +10,7 @@ diffspec/runtime.py:1211-1276), the LSE orientations
 (diffspec/runtime.py:1737-1765).  No GPU is used: every launch is recorded.
 """
 
+from dataclasses import dataclass
 from types import SimpleNamespace
 
 import pytest
@@ -26,14 +27,27 @@ class _Rotary:
         self.cos_sin_cache = torch.zeros((positions, 2))
 
 
-def _cache(**overrides):
+@dataclass(frozen=True)
+class _ReferenceShapedSettings:
+    """The reference proposer's settings type: exactly the 7 fields of diffspec/runtime.py:18-27, no recent_window."""
+
+    chunk_size: int
+    token_budget: int
+    retrieval_interval: int
+    max_tree_nodes: int
+    max_tree_depth: int
+    tree_threshold: float
+    adaptive_profile: bool
+
+
+def _cache(settings_type=runtime.DiffSpecSettings, **overrides):
     settings = dict(chunk_size=2, token_budget=8, retrieval_interval=2, max_tree_nodes=4, max_tree_depth=2,
                     tree_threshold=0.7, adaptive_profile=False)
     settings.update(overrides.pop("settings", {}))
     kwargs = dict(max_num_reqs=4, max_model_len=16, num_kv_heads=1, head_dim=2, target_num_layers=2,
                   dtype=torch.float32, device=torch.device("cpu"), rotary_embedding=_Rotary())
     kwargs.update(overrides)
-    return runtime.DiffSpecDraftCache(runtime.DiffSpecSettings(**settings), **kwargs)
+    return runtime.DiffSpecDraftCache(settings_type(**settings), **kwargs)
 
 
 @pytest.fixture
@@ -297,7 +311,9 @@ def capture_calls(monkeypatch):
     return calls
 
 
-def test_linear_call_sequence_of_the_plugin(launches, attention_calls, capture_calls):
+@pytest.mark.parametrize("settings_type", [runtime.DiffSpecSettings, _ReferenceShapedSettings],
+                         ids=["ds355-settings", "reference-7-field-settings"])
+def test_linear_call_sequence_of_the_plugin(launches, attention_calls, capture_calls, settings_type):
     """The hooks the unchanged plugin calls on one linear verify + draft cycle, in its order:
     the runner's prepare_target_batch (ascend_patch.py:274) and begin_target_forward (:301),
     the attention patch's is_target_retrieval_layer / capture_target_attention (:198, :233)
@@ -305,7 +321,9 @@ def test_linear_call_sequence_of_the_plugin(launches, attention_calls, capture_c
     (proposer.py:357), accept_target_queries (:216), prepare_inputs_padded's
     target_tree_active read (:224), begin_cycle (:103), populate_prefill (:266),
     prepare_compact_prefill (:303), the draft layer's capture + attention, end_cycle (:119)."""
-    cache = _cache(settings=dict(retrieval_interval=1, token_budget=16), max_model_len=32, target_num_layers=3)
+    cache = _cache(settings_type, settings=dict(retrieval_interval=1, token_budget=16), max_model_len=32,
+                   target_num_layers=3)
+    assert cache.recent_window == 2  # the reference's settings carry no window: one chunk
     ids = ["a", "b"]
     # Verifier step: the runner activates the batch (linear: no proposed tree).
     cache.prepare_target_batch(ids, {"a": [5, 6, 7], "b": [1, 2, 3]})
@@ -456,3 +474,135 @@ def test_gather_records_follow_the_slot_map(launches):
     assert gen.tolist() == cache.sel_gen.tolist() and records.shape == cache.gather_records.shape
     assert runtime.RETRIEVAL_STAGES == step.SCORE | step.SELECT
     assert _cache(prefix_at_retrieval=True).retrieval_stages == step.SCORE | step.SELECT | step.PREFIX
+
+
+def _speculative_config(**overrides):
+    fields = dict(diffspec_chunk_size=32, diffspec_token_budget=2048, diffspec_retrieval_interval=4,
+                  diffspec_max_tree_nodes=50, num_speculative_tokens=4, diffspec_tree_threshold=0.7,
+                  diffspec_adaptive_profile=False, enabled=True)
+    fields.update(overrides)
+    spec = SimpleNamespace(**fields)
+    spec.use_diffspec = lambda: spec.enabled
+    return SimpleNamespace(speculative_config=spec)
+
+
+def test_settings_from_vllm_config_follow_the_reference_mapping():
+    """diffspec/runtime.py:28-41: max_tree_depth comes from num_speculative_tokens; a disabled policy raises."""
+    settings = runtime.DiffSpecSettings.from_vllm_config(_speculative_config())
+    assert settings == runtime.DiffSpecSettings(chunk_size=32, token_budget=2048, retrieval_interval=4,
+                                                max_tree_nodes=50, max_tree_depth=4, tree_threshold=0.7,
+                                                adaptive_profile=False, recent_window=None)
+    windowed = runtime.DiffSpecSettings.from_vllm_config(_speculative_config(diffspec_recent_window=256))
+    assert windowed.recent_window == 256
+    with pytest.raises(ValueError, match="enabled DiffSpec policy"):
+        runtime.DiffSpecSettings.from_vllm_config(_speculative_config(enabled=False))
+    with pytest.raises(ValueError, match="enabled DiffSpec policy"):
+        runtime.DiffSpecSettings.from_vllm_config(SimpleNamespace(speculative_config=None))
+    cache = _cache(settings=dict(chunk_size=2, token_budget=8), recent_window=6)
+    assert cache.recent_window == 6  # the constructor argument wins over the settings
+
+
+def test_reference_settings_construct_the_cache_with_the_proposer_arguments():
+    """The proposer's constructor call (proposer.py:52-65) on the reference's 7-field settings."""
+    settings = _ReferenceShapedSettings(chunk_size=2, token_budget=8, retrieval_interval=4, max_tree_nodes=4,
+                                        max_tree_depth=2, tree_threshold=0.7, adaptive_profile=True)
+    cache = runtime.DiffSpecDraftCache(
+        settings, max_num_reqs=4, max_model_len=16, num_kv_heads=1, head_dim=2, target_num_layers=2,
+        dtype=torch.float32, device=torch.device("cpu"), rotary_embedding=_Rotary(), target_cos_sin_cache=None,
+        target_tensor_parallel_size=1)
+    assert cache.history_budget == 4 and cache.recent_window == 2
+    assert cache.retrieval_interval == 4 and cache.controller.adaptive
+    assert cache.controller.profile == runtime.DiffSpecTreeProfile(50, 10)  # proposer.py:411 reads it
+    with pytest.raises(ValueError, match="too small for tree tokens"):
+        runtime.DiffSpecDraftCache(
+            _ReferenceShapedSettings(2, 3, 4, 4, 2, 0.7, False), max_num_reqs=4, max_model_len=16, num_kv_heads=1,
+            head_dim=2, target_num_layers=2, dtype=torch.float32, device=torch.device("cpu"),
+            rotary_embedding=_Rotary())
+
+
+class _SelectingRecorder:
+    """Stands in for the step: each scored row (count > 0) stores the selection the test scripted for its slot."""
+
+    def __init__(self):
+        self.next = {}
+        self.calls = 0
+
+    def __call__(self, **kw):
+        self.calls += 1
+        counts = kw["rows"].counts[: kw["rows"].batch_size].tolist()
+        for row, slot in enumerate(kw["slots"].tolist()):
+            if counts[row] > 0 and slot in self.next:
+                ids = self.next[slot]
+                kw["sel_ids"][slot, : len(ids)] = torch.tensor(ids, dtype=torch.int32)
+                kw["sel_count"][slot] = len(ids)
+
+
+def _verify(cache, counts, lens=(20, 12)):
+    cache.begin_target_forward(["a", "b"])
+    cache.capture_target_attention(torch.zeros((2, 2, 2)), torch.zeros((2, 2)), torch.zeros((4, 8, 1, 2)),
+                                   _metadata([1, 2], list(lens), prefill=False), 0.5)
+    cache.accept_target_queries(torch.tensor(counts), is_prefill=False)
+
+
+def test_adaptive_cadence_doubles_on_stable_selections(monkeypatch):
+    """runtime.py:575-593 fed at :1309-1331: intersection over union >= 0.9 and no acceptance drop double the
+    interval (capped at 32); a changed selection or a >10% acceptance drop returns it to the base."""
+    recorder = _SelectingRecorder()
+    monkeypatch.setattr(step, "retrieval_step", recorder)
+    cache = _cache(settings=dict(retrieval_interval=1, adaptive_profile=True, token_budget=16), max_model_len=32)
+    slot_a = 0
+    expected_calls = 0
+
+    def cycle(counts, selection_a, interval_after):
+        nonlocal expected_calls
+        recorder.next = {slot_a: selection_a, 1: [9]}
+        before = recorder.calls
+        _verify(cache, counts)
+        if recorder.calls > before:
+            expected_calls += 1
+        # The observation is applied at the next call, before the interval is read.
+        cache._observe_previous_retrieval()
+        assert cache.retrieval_interval == interval_after
+
+    cycle([3, 1], [0, 1, 2], 1)  # cycle 1: first selection, no previous chunks, overlap 0 -> base
+    cycle([3, 1], [0, 1, 2], 2)  # cycle 2: same chunks, same acceptance (2) -> doubled
+    cycle([3, 1], [0, 1, 3], 2)  # cycle 3: 3 % 2, skipped: nothing observed, whatever the scores
+    cycle([3, 1], [0, 1, 2], 4)  # cycle 4 retrieves: doubled again
+    for _ in range(3):
+        cycle([3, 1], [0, 1, 2], 4)  # cycles 5-7 skipped
+    cycle([3, 1], [0, 1, 3], 1)  # cycle 8: overlap 2/4 -> base
+    cycle([3, 1], [0, 1, 3], 2)  # cycle 9: stable -> 2
+    cycle([2, 1], [0, 1, 3], 1)  # cycle 10: acceptance 1 < 0.9 * 2 -> base, though stable
+    cycle([2, 1], [0, 1, 3], 2)  # cycle 11: acceptance 1 again -> 2
+    # Cycle 12: row 0 committed nothing, so the first scored row is row 1 (slot 1, selection [9] before and
+    # after: stable), with acceptance 0 < 0.9 * 1 -> base.
+    cycle([0, 1], [5], 1)
+    assert cache._adaptive_ids[1, slot_a, :3].tolist() == [0, 1, 3]  # row 0 kept its selection
+    cycle([2, 1], [0, 1, 3], 2)  # cycle 13
+    cycle([2, 1], [0, 1, 3], 4)  # cycle 14
+    cycle([2, 1], [0, 1, 3], 4)  # 15 skipped
+    cycle([2, 1], [0, 1, 3], 8)  # 16
+    for _ in range(7):
+        cycle([2, 1], [0, 1, 3], 8)  # 17-23 skipped
+    cycle([2, 1], [0, 1, 3], 16)  # 24
+    for _ in range(7):
+        cycle([2, 1], [0, 1, 3], 16)  # 25-31 skipped
+    cycle([2, 1], [0, 1, 3], 32)  # 32
+    for _ in range(31):
+        cycle([2, 1], [0, 1, 3], 32)  # 33-63 skipped
+    cycle([2, 1], [0, 1, 3], 32)  # 64: capped at 32
+    assert expected_calls == recorder.calls == 14  # cycles 1, 2, 4, 8-14, 16, 24, 32 and 64
+    status = cache.retrieval_status()
+    assert status["retrieval_count"] == 14 and status["retrieval_skipped_interval"] == 64 - 14
+
+
+def test_adaptive_cadence_off_keeps_the_interval(monkeypatch):
+    """adaptive_profile=False: the base interval always, and no host copies are made."""
+    recorder = _SelectingRecorder()
+    monkeypatch.setattr(step, "retrieval_step", recorder)
+    cache = _cache(settings=dict(retrieval_interval=2, token_budget=16), max_model_len=32)
+    for _ in range(8):
+        recorder.next = {0: [0, 1, 2], 1: [9]}
+        _verify(cache, [3, 1])
+        assert cache.retrieval_interval == 2 and cache._adaptive_pending is None
+    assert recorder.calls == 4

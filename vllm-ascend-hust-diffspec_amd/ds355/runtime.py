@@ -13,8 +13,9 @@ small ring of pinned staging buffers with non-blocking copies.
 Linear draft attention over the working cache (``forward_attention``) runs
 as one launch of ``ds355.attention``; the raw pre-RoPE K/V capture of draft
 tokens and the graph-safe RoPE input (``capture_raw_kv``,
-``graph_safe_rope_positions``) as one launch of ``ds355.capture``.  Tree
-drafting and the adaptive controller are outside this module.
+``graph_safe_rope_positions``) as one launch of ``ds355.capture``.  The
+adaptive retrieval cadence (``DiffSpecAdaptiveController``) is kept; tree
+drafting is outside this module.
 """
 
 from __future__ import annotations
@@ -36,7 +37,12 @@ from .plan import plan_width as _plan_width
 
 @dataclass(frozen=True)
 class DiffSpecSettings:
-    """Field order and meaning of diffspec/runtime.py:18-41."""
+    """Field order and meaning of diffspec/runtime.py:18-41.
+
+    ``recent_window`` is the only field the reference's settings lack; the
+    cache reads it with ``getattr``, so the reference's own 7-field settings
+    object works unchanged.
+    """
 
     chunk_size: int
     token_budget: int
@@ -46,6 +52,86 @@ class DiffSpecSettings:
     tree_threshold: float
     adaptive_profile: bool
     recent_window: int | None = None  # None: one chunk, the reference's tail
+
+    @classmethod
+    def from_vllm_config(cls, vllm_config: Any) -> "DiffSpecSettings":
+        """The speculative config's DiffSpec fields, mapped as diffspec/runtime.py:28-41 does.
+
+        An optional ``diffspec_recent_window`` on the speculative config sets
+        the rolling window; without it the window is one chunk.
+        """
+        spec = vllm_config.speculative_config
+        if spec is None or not spec.use_diffspec():
+            raise ValueError("DiffSpec settings require an enabled DiffSpec policy")
+        return cls(
+            chunk_size=spec.diffspec_chunk_size,
+            token_budget=spec.diffspec_token_budget,
+            retrieval_interval=spec.diffspec_retrieval_interval,
+            max_tree_nodes=spec.diffspec_max_tree_nodes,
+            max_tree_depth=spec.num_speculative_tokens,
+            tree_threshold=spec.diffspec_tree_threshold,
+            adaptive_profile=spec.diffspec_adaptive_profile,
+            recent_window=getattr(spec, "diffspec_recent_window", None),
+        )
+
+
+@dataclass(frozen=True)
+class DiffSpecTreeProfile:
+    """A draft-tree size (diffspec/runtime.py:52-55)."""
+
+    max_nodes: int
+    max_depth: int
+
+
+class DiffSpecAdaptiveController:
+    """Retrieval cadence of diffspec/runtime.py:530-593.
+
+    With ``adaptive`` set, every retrieval compares the first scored row's
+    chunk selection with the one it replaced.  An overlap (intersection over
+    union) of at least 0.9, with the accepted length not below 90% of the
+    previous retrieval's, doubles the interval up to 32 cycles; anything else
+    returns it to the configured base.  Tree profiles (``profile``,
+    ``observe_cycle``) serve the reference's tree drafting, which this cache
+    never proposes; they are kept so the proposer's reads see the same values.
+    """
+
+    PROFILES = (DiffSpecTreeProfile(16, 5), DiffSpecTreeProfile(32, 7), DiffSpecTreeProfile(50, 10))
+    MAX_INTERVAL = 32
+
+    def __init__(self, base_retrieval_interval: int, adaptive: bool) -> None:
+        self.base_retrieval_interval = base_retrieval_interval
+        self.retrieval_interval = base_retrieval_interval
+        self.adaptive = adaptive
+        self.profile = self.PROFILES[-1]
+        self._throughput_ewma: dict[DiffSpecTreeProfile, float] = {}
+        self._last_acceptance: float | None = None
+
+    def observe_cycle(self, profile: DiffSpecTreeProfile, emitted_tokens: int, latency_seconds: float) -> None:
+        """Throughput per tree profile; adaptive mode measures each, then keeps the best by 5%."""
+        if latency_seconds <= 0:
+            raise ValueError("latency_seconds must be positive")
+        rate = emitted_tokens / latency_seconds
+        self._throughput_ewma[profile] = 0.8 * self._throughput_ewma.get(profile, rate) + 0.2 * rate
+        if not self.adaptive:
+            return
+        for candidate in self.PROFILES:
+            if candidate not in self._throughput_ewma:
+                self.profile = candidate
+                return
+        best = max(self._throughput_ewma, key=self._throughput_ewma.__getitem__)
+        if self._throughput_ewma[best] > self._throughput_ewma.get(self.profile, 0.0) * 1.05:
+            self.profile = best
+
+    def observe_retrieval(self, previous_chunks: set[int], selected_chunks: set[int],
+                          acceptance_length: float) -> None:
+        union = previous_chunks | selected_chunks
+        overlap = len(previous_chunks & selected_chunks) / len(union) if union else 1.0
+        dropped = self._last_acceptance is not None and acceptance_length < 0.9 * self._last_acceptance
+        if self.adaptive and overlap >= 0.9 and not dropped:
+            self.retrieval_interval = min(2 * self.retrieval_interval, self.MAX_INTERVAL)
+        else:
+            self.retrieval_interval = self.base_retrieval_interval
+        self._last_acceptance = acceptance_length
 
 
 @dataclass
@@ -181,6 +267,7 @@ class DiffSpecDraftCache:
         max_batch_rows: int | None = None,
         lse_free_scoring: bool = False,
         prefix_at_retrieval: bool = False,
+        recent_window: int | None = None,
     ) -> None:
         if target_tensor_parallel_size < 1:
             raise ValueError("Target tensor parallel size must be positive")
@@ -196,7 +283,11 @@ class DiffSpecDraftCache:
         self.rotary_embedding = rotary_embedding
         self.target_cos_sin_cache = target_cos_sin_cache
         self.history_budget = _history_budget(settings.token_budget, settings.max_tree_depth, settings.chunk_size)
-        self.recent_window = settings.chunk_size if settings.recent_window is None else settings.recent_window
+        # The rolling window: this argument, else the settings' field (the
+        # reference's settings have none), else one chunk, the reference's tail.
+        if recent_window is None:
+            recent_window = getattr(settings, "recent_window", None)
+        self.recent_window = settings.chunk_size if recent_window is None else int(recent_window)
 
         cache_shape = (max_num_reqs, max_model_len, num_kv_heads, head_dim)
         self.raw_key = torch.empty(cache_shape, dtype=dtype, device=self.device)
@@ -247,7 +338,22 @@ class DiffSpecDraftCache:
         self._slot_map = _Staging(1, max_num_reqs, self.device)
         self._slot_map_list: list[int] | None = None
 
-        self.retrieval_interval = settings.retrieval_interval
+        self.controller = DiffSpecAdaptiveController(settings.retrieval_interval, settings.adaptive_profile)
+        # Adaptive cadence compares a slot's selection before and after a
+        # retrieval.  Both, and the committed counts, are copied to pinned
+        # host memory on the stream; the comparison runs at the next
+        # retrieval call, before the interval is read, which is the first
+        # time the reference reads what it changes.  No synchronisation is
+        # added to the retrieval itself.
+        self._adaptive_pending: tuple | None = None
+        self._adaptive_ids: torch.Tensor | None = None  # [before/after, slots, capacity]
+        self._adaptive_sel_count: torch.Tensor | None = None  # [before/after, slots]
+        self._adaptive_counts: torch.Tensor | None = None  # [rows]
+        if settings.adaptive_profile:
+            pin = self.device.type == "cuda"
+            self._adaptive_ids = torch.zeros((2, max_num_reqs, capacity), dtype=torch.int32, pin_memory=pin)
+            self._adaptive_sel_count = torch.zeros((2, max_num_reqs), dtype=torch.int32, pin_memory=pin)
+            self._adaptive_counts = torch.zeros((self.max_batch_rows,), dtype=torch.int32, pin_memory=pin)
         self.metrics = DiffSpecRuntimeMetrics()
         self._request_slots: dict[str, int] = {}
         self._active_slots: list[int] = []
@@ -289,6 +395,11 @@ class DiffSpecDraftCache:
         self.proposed_parent_indices: torch.Tensor | None = None
         self.proposed_depths: torch.Tensor | None = None
         self.proposed_depths_cpu: list[int] = []
+
+    @property
+    def retrieval_interval(self) -> int:
+        """Verifier cycles between retrievals (the controller's, diffspec/runtime.py:1206)."""
+        return self.controller.retrieval_interval
 
     def _view(self, name: str, rows: int, make) -> torch.Tensor:
         """A slice of one of the cache's buffers, made once per batch size."""
@@ -467,7 +578,37 @@ class DiffSpecDraftCache:
             target_tensor_parallel_size=self.target_tensor_parallel_size,
         )
 
+    def _observe_previous_retrieval(self) -> None:
+        """Feed the last retrieval's first scored row to the cadence controller (runtime.py:1309-1331).
+
+        That row is the first with a positive committed count; its selection
+        before the retrieval (none or empty: no chunks) and after it are
+        compared as chunk sets, with its accepted length ``count - 1``.  A
+        retrieval with no committed row observes nothing, as the reference
+        returns before scoring then.
+        """
+        pending, self._adaptive_pending = self._adaptive_pending, None
+        if pending is None:
+            return
+        slots, batch_size, done = pending
+        if done is not None:
+            done.synchronize()  # recorded a verifier cycle ago: normally complete
+        counts = self._adaptive_counts[:batch_size].tolist()
+        first = next((i for i, c in enumerate(counts) if c > 0), None)
+        if first is None:
+            return
+        slot = slots[first]
+        chunks = [set(self._adaptive_ids[k, slot, : max(0, int(self._adaptive_sel_count[k, slot]))].tolist())
+                  for k in (0, 1)]
+        self.controller.observe_retrieval(chunks[0], chunks[1], float(max(0, counts[first] - 1)))
+
+    def _copy_selection_state(self, which: int) -> None:
+        """Every slot's selection (ids, then the count) into pinned host memory, on the stream."""
+        self._adaptive_ids[which].copy_(self.sel_ids, non_blocking=True)
+        self._adaptive_sel_count[which].copy_(self.sel_count, non_blocking=True)
+
     def _accept_target_queries(self, valid_sampled_token_count: torch.Tensor, *, is_prefill: bool) -> None:
+        self._observe_previous_retrieval()
         if self._target_query is None or self._target_key_cache is None or self._target_block_tables is None:
             self.metrics.retrieval_skipped_no_snapshot += 1
             return
@@ -525,6 +666,8 @@ class DiffSpecDraftCache:
             counts = self._view("counts", batch_size, lambda: staged[4, :batch_size])
             counts.copy_(valid_sampled_token_count.reshape(-1)[:batch_size])  # device-side cast, no sync
         started = time.perf_counter()
+        if self.controller.adaptive:
+            self._copy_selection_state(0)
         q, lse, kc, bt = self._target_query, self._target_lse, self._target_key_cache, self._target_block_tables
         stages = self.retrieval_stages
         if key is None:
@@ -547,6 +690,14 @@ class DiffSpecDraftCache:
             snapshot = _step.VerifierSnapshot(query=q, lse=lse, key_cache=kc, block_table=bt, scale=self._target_scale)
             self._launch(stages, batch_size, snapshot=snapshot, rows=rows,
                          slots=self._view("rs", batch_size, lambda: staged[3, :batch_size]), committed=None)
+        if self.controller.adaptive:
+            self._copy_selection_state(1)
+            self._adaptive_counts[:batch_size].copy_(counts.reshape(-1)[:batch_size], non_blocking=True)
+            done = None
+            if self.device.type == "cuda":
+                done = torch.cuda.Event()
+                done.record(torch.cuda.current_stream(self.device))
+            self._adaptive_pending = (list(self._active_slots), batch_size, done)
         self.metrics.observe_retrieval(time.perf_counter() - started)
 
     # -- rebuild (runtime.py:1349-1371, 1683-1765) ------------------------------------------------

@@ -296,6 +296,8 @@ size_t ds_step_workspace_bytes(int batch_rows, int max_chunks, int num_kv_heads,
  * called.
  *
  * Limits, rejected with DS_ERR_INVALID and a message:
+ *   DS_STAGE_SELECT only together with DS_STAGE_SCORE (the selection reads
+ *   partials that only the same call's scoring writes into the array);
  *   batch_rows x max_chunks x num_kv_heads x 4 bytes <= DS_STATIC_PARTIALS_BYTES;
  *   without an LSE, batch_rows x num_q_heads x max_chunks x 8 bytes <= DS_STATIC_PAIRS_BYTES.
  * A full step runs as the single launch when ds_step_workspace_bytes() of its

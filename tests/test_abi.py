@@ -376,3 +376,52 @@ def test_static_scratch_step_rejects_what_does_not_fit():
     desc.score_partials = 64  # caller scratch is refused: it lives in the static array
     assert lib.ds_retrieval_step_static(None, desc, None) == _lib.DS_ERR_INVALID
     assert b"takes no score_partials" in lib.ds_last_error()
+    desc.score_partials, desc.lse = None, 1
+    for stages in (_lib.DS_STAGE_SELECT, _lib.DS_STAGE_SELECT | _lib.DS_STAGE_PLAN,
+                   _lib.DS_STAGE_SELECT | _lib.DS_STAGE_PREFIX):
+        # A selection without this call's scoring would rank whatever partials an earlier call left.
+        desc.stages = stages
+        assert lib.ds_retrieval_step_static(None, desc, None) == _lib.DS_ERR_INVALID
+        assert b"selects only after scoring in the same call" in lib.ds_last_error()
+
+
+def test_static_scratch_single_launch_cases_fit_the_fused_region():
+    """The static-scratch GPU test's single-launch batches fit DS_STATIC_FUSED_BYTES, so the static entry hands
+    the single launch its workspace (csrc/step_static.hip) rather than falling back to the chain."""
+    from ds355 import _lib
+
+    lib = _lib.load()
+    fused_region = 8 << 20
+    for rows, tokens in ((12 + 2, 20000), (9 + 2, 6000)):  # batch rows include the 2 padding rows
+        chunks = (tokens + 63) // 64
+        need = lib.ds_step_workspace_bytes(rows, chunks, 4, 2048)
+        assert 0 < need <= fused_region, (rows, chunks, need)
+
+
+def test_hip_runtime_lookup_falls_back(monkeypatch):
+    """hip_runtime() finds the HIP runtime torch already loaded, by soname or by its mapped path, and returns None
+    (callers then use torch's copies and events) when neither finds it; it never loads a second copy."""
+    import ctypes
+    import os
+
+    from ds355 import _lib
+
+    assert any("libamdhip64.so" in p for p in _lib._loaded_hip_paths())  # torch's runtime is mapped
+    monkeypatch.setattr(_lib, "_hip", None)
+    monkeypatch.setattr(_lib, "_hip_looked_up", False)
+    tried = []
+    real_cdll = ctypes.CDLL
+
+    def only_by_path(name, mode=0):
+        tried.append(name)
+        if not name.startswith("/"):
+            raise OSError(f"{name}: not found")  # as with a torch built for another ROCm major
+        assert mode & os.RTLD_NOLOAD
+        return real_cdll(name, mode=mode)
+
+    monkeypatch.setattr(ctypes, "CDLL", only_by_path)
+    assert _lib.hip_runtime() is not None and tried[:2] == ["libamdhip64.so.7", "libamdhip64.so"]
+    monkeypatch.setattr(_lib, "_hip", None)
+    monkeypatch.setattr(_lib, "_hip_looked_up", False)
+    monkeypatch.setattr(ctypes, "CDLL", lambda name, mode=0: (_ for _ in ()).throw(OSError(name)))
+    assert _lib.hip_runtime() is None

@@ -31,8 +31,14 @@ def _case(seed, rows, lo, hi):
                       num_slots=rows)
 
 
-def _run_static(case, device, *, lse_free):
-    """The same buffers run_gpu makes, through ds_retrieval_step_static."""
+def _run_static(case, device, *, lse_free, check_free_memory):
+    """The same buffers run_gpu makes, through ds_retrieval_step_static.
+
+    With ``check_free_memory`` the device's free memory (hipMemGetInfo) must
+    be the same before the call and after it has run: the entry point
+    allocates nothing.  The first call of a process loads the code object
+    that holds the static array, so only later calls are checked.
+    """
     from ds355 import step
 
     i32 = lambda xs: torch.tensor(xs, dtype=torch.int32, device=device)  # noqa: E731
@@ -70,8 +76,13 @@ def _run_static(case, device, *, lse_free):
         lse_partials=dummy_pairs if lse_free else None, lse_out=st["lse_out"] if lse_free else None,
     )
     status = torch.zeros((1,), dtype=torch.int32, device=device)
+    torch.cuda.synchronize()
+    free_before = torch.cuda.mem_get_info(device)[0]
     step.launch_static(desc, dev, status)
     torch.cuda.synchronize()
+    free_after = torch.cuda.mem_get_info(device)[0]
+    if check_free_memory:
+        assert free_after == free_before, f"free device memory moved by {free_before - free_after} bytes"
     assert int(status.item()) == 0
     return st
 
@@ -98,5 +109,5 @@ def test_static_scratch_step_equals_caller_buffers(cuda, kind, first, second):
         case = _case(31 + 7 * call + len(kind), rows, lo, hi)
         expected = run_gpu(case, cuda, path=path, lse_free=lse_free,
                            single_launch=None if path == "fused" else False)
-        got = _run_static(case, cuda, lse_free=lse_free)
+        got = _run_static(case, cuda, lse_free=lse_free, check_free_memory=call > 0)
         _same(expected, got, KEYS + (("lse_out",) if lse_free else ()))

@@ -18,7 +18,8 @@
 //                     only grows, so it starts valid from zero and needs no
 //                     clearing between calls.
 //   [8, 12 MiB)       per-KV-head score partials of the kernel chain, written
-//                     before they are read within each call.
+//                     before they are read within each call (so SELECT is
+//                     refused without SCORE).
 //   [12, 24 MiB)      (max, sum) pairs of scoring without a supplied LSE,
 //                     written before they are read within each call.
 // Calls that overlap on one GPU (two streams, or two threads) race on these
@@ -79,6 +80,12 @@ extern "C" int ds_retrieval_step_static(ds_stream_t stream, const ds_step_desc* 
              "static scratch)");
   const bool score = (d->stages & DS_STAGE_SCORE) != 0;
   const bool select = (d->stages & DS_STAGE_SELECT) != 0;
+  // Selection reads the per-KV-head partials, which here live in the static
+  // array: only a SCORE stage of the same call writes them for this layout.
+  DS_REQUIRE(score || !select,
+             "the static-scratch step selects only after scoring in the same call (DS_STAGE_SELECT needs "
+             "DS_STAGE_SCORE): its score partials live in the static scratch; use ds_retrieval_step with caller "
+             "score_partials for a separate selection");
   const int64_t rows = std::max(d->batch_rows, 0);
   const int64_t chunks = std::max(d->max_chunks, 0);
   const int64_t hkv = std::max(d->num_kv_heads, 0);

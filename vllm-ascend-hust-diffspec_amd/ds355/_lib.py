@@ -171,29 +171,56 @@ def ptr(t: torch.Tensor | None) -> int | None:
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 _hip: ctypes.CDLL | None = None
+_hip_looked_up = False
 HIP_MEMCPY_HOST_TO_DEVICE = 1
 HIP_EVENT_DISABLE_TIMING = 2
 
 
-def hip_runtime() -> ctypes.CDLL:
+def _loaded_hip_paths() -> list[str]:
+    """Paths of HIP runtimes already mapped into this process (torch's), by /proc/self/maps."""
+    paths: list[str] = []
+    try:
+        with open("/proc/self/maps") as maps:
+            for line in maps:
+                path = line.rstrip("\n").split(maxsplit=5)[-1]
+                if "/libamdhip64.so" in path and path not in paths:
+                    paths.append(path)
+    except OSError:
+        pass
+    return paths
+
+
+def hip_runtime() -> ctypes.CDLL | None:
     """The HIP runtime already loaded in the process (torch's, which the
     library's kernels and streams share), for small host-side copies and
-    events without torch's dispatch cost.  Never loads a second copy."""
-    global _hip
-    if _hip is None:
-        hip = ctypes.CDLL("libamdhip64.so.7", mode=os.RTLD_NOLOAD | os.RTLD_LAZY)
-        hip.hipMemcpyAsync.restype = ctypes.c_int
-        hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
-                                       ctypes.c_void_p]
-        hip.hipEventCreateWithFlags.restype = ctypes.c_int
-        hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
-        hip.hipEventRecord.restype = ctypes.c_int
-        hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
-        hip.hipEventSynchronize.restype = ctypes.c_int
-        hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
-        hip.hipEventDestroy.restype = ctypes.c_int
-        hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
-        _hip = hip
+    events without torch's dispatch cost.  Never loads a second copy: it is
+    looked up by soname, then by the path mapped into the process, with
+    RTLD_NOLOAD.  None when neither finds it; callers then use torch's
+    copies and events."""
+    global _hip, _hip_looked_up
+    if _hip_looked_up:
+        return _hip
+    _hip_looked_up = True
+    hip = None
+    for name in ("libamdhip64.so.7", "libamdhip64.so", *_loaded_hip_paths()):
+        try:
+            hip = ctypes.CDLL(name, mode=os.RTLD_NOLOAD | os.RTLD_LAZY)
+            break
+        except OSError:
+            continue
+    if hip is None:
+        return None
+    hip.hipMemcpyAsync.restype = ctypes.c_int
+    hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p]
+    hip.hipEventCreateWithFlags.restype = ctypes.c_int
+    hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+    hip.hipEventRecord.restype = ctypes.c_int
+    hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipEventSynchronize.restype = ctypes.c_int
+    hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+    hip.hipEventDestroy.restype = ctypes.c_int
+    hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    _hip = hip
     return _hip
 
 

@@ -166,18 +166,21 @@ class _Staging:
     """Ring of pinned host buffers for small int32 row arrays (non-blocking H2D).
 
     On a GPU the copy and the ring's events go straight to the HIP runtime
-    (a few microseconds less per upload than torch's copy and Event).  The
-    ring is cut into groups of ``group`` buffers with one event each,
-    recorded after the group's last copy: the first buffer of a group is
-    refilled only once the group's copies of the previous lap have run, so
-    one upload in ``group`` records an event and the others record none.
-    Uploads go to one device buffer, so consumers are ordered by the stream.
+    (a few microseconds less per upload than torch's copy and Event), or
+    through torch's non-blocking copy and Event when the process's HIP
+    runtime cannot be found by name.  The ring is cut into groups of
+    ``group`` buffers with one event each, recorded after the group's last
+    copy: the first buffer of a group is refilled only once the group's
+    copies of the previous lap have run, so one upload in ``group`` records
+    an event and the others record none.  Uploads go to one device buffer,
+    so consumers are ordered by the stream.
     """
 
     def __init__(self, fields: int, rows: int, device: torch.device, depth: int = 32, group: int = 8) -> None:
         if depth % group:
             raise ValueError("the ring depth must be a multiple of the group size")
         pin = device.type == "cuda"
+        self.pinned = pin
         self.host = [torch.zeros((fields, rows), dtype=torch.int32, pin_memory=pin) for _ in range(depth)]
         self.host_np = [h.numpy() for h in self.host]  # list -> pinned buffer without a temporary tensor
         self.group = group
@@ -185,15 +188,18 @@ class _Staging:
         self.device = torch.zeros((fields, rows), dtype=torch.int32, device=device)
         self.index = 0
         self.hip = None
+        self.events: list = []
         if pin:
-            self.hip = _lib.hip_runtime()
             self.torch_device = device if device.index is not None else torch.device("cuda", torch.cuda.current_device())
-            self.events = []
-            for _ in range(depth // group):
-                ev = ctypes.c_void_p()
-                _lib.hip_check(self.hip.hipEventCreateWithFlags(ctypes.byref(ev), _lib.HIP_EVENT_DISABLE_TIMING),
-                               "hipEventCreateWithFlags")
-                self.events.append(ev)
+            self.hip = _lib.hip_runtime()
+            if self.hip is None:
+                self.events = [torch.cuda.Event() for _ in range(depth // group)]
+            else:
+                for _ in range(depth // group):
+                    ev = ctypes.c_void_p()
+                    _lib.hip_check(self.hip.hipEventCreateWithFlags(ctypes.byref(ev), _lib.HIP_EVENT_DISABLE_TIMING),
+                                   "hipEventCreateWithFlags")
+                    self.events.append(ev)
             self.nbytes = fields * rows * 4
             self.host_ptr = [h.data_ptr() for h in self.host]
             self.device_ptr = self.device.data_ptr()
@@ -204,20 +210,41 @@ class _Staging:
             for ev in self.events:
                 hip.hipEventDestroy(ev)
 
+    def _wait(self, g: int) -> None:
+        if self.hip is not None:
+            _lib.hip_check(self.hip.hipEventSynchronize(self.events[g]), "hipEventSynchronize")
+        else:
+            self.events[g].synchronize()
+
+    def drain(self) -> None:
+        """Wait until every copy issued from the ring has run, so its host buffers may be released.
+
+        Copies after a group's last recorded event are covered by a stream
+        synchronisation; the ring is drained only when it is replaced.
+        """
+        if self.pinned:
+            torch.cuda.current_stream(self.torch_device).synchronize()
+
     def upload(self, columns: list[list[int]]) -> torch.Tensor:
         i = self.index
         self.index = (i + 1) % len(self.host)
         g, k = divmod(i, self.group)
-        hip = self.hip
-        if hip is not None and k == 0 and self.recorded[g]:
-            # Only waits if the GPU is a full ring behind.
-            _lib.hip_check(hip.hipEventSynchronize(self.events[g]), "hipEventSynchronize")
+        if self.pinned and k == 0 and self.recorded[g]:
+            self._wait(g)  # only waits if the GPU is a full ring behind
         buf = self.host_np[i]
         for f, values in enumerate(columns):
             if len(values):
                 buf[f, : len(values)] = values
-        if hip is None:
+        if not self.pinned:
             self.device.copy_(self.host[i])
+            return self.device
+        hip = self.hip
+        if hip is None:
+            stream = torch.cuda.current_stream(self.torch_device)
+            self.device.copy_(self.host[i], non_blocking=True)
+            if k == self.group - 1:
+                self.events[g].record(stream)
+                self.recorded[g] = True
             return self.device
         stream = _lib.stream_handle(self.torch_device)
         _lib.hip_check(hip.hipMemcpyAsync(self.device_ptr, self.host_ptr[i], self.nbytes,
@@ -759,6 +786,10 @@ class DiffSpecDraftCache:
         staging = self._token_staging
         if staging is None or staging.device.shape[1] < num_tokens:
             capacity = max(num_tokens, 8 * self.max_batch_rows)
+            if staging is not None:
+                # Raw copies from the old ring's pinned buffers may still be
+                # queued, and torch's host allocator does not know of them.
+                staging.drain()
             staging = self._token_staging = _Staging(1, capacity, self.device)
         slots = staging.upload([token_slots])[0, :num_tokens]
         positions = absolute_positions.reshape(-1)[:num_tokens]

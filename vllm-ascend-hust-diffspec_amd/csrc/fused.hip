@@ -66,7 +66,7 @@
 
 namespace ds355 {
 
-int make_score_args(score::ScoreArgs& a, int64_t& upper_units, bool& uniform_page, int dtype, const void* query,
+int make_score_args(score::ScoreArgs& a, int64_t& upper_units, int& page_mode, int dtype, const void* query,
                     int64_t q_stride, const void* key_cache, int64_t k_block_stride, int64_t k_token_stride,
                     int64_t k_head_stride, const float* lse, int64_t lse_row_stride, int64_t lse_head_stride,
                     const int32_t* block_table, int64_t bt_stride, const RowSource& src, int batch, int num_q_heads,
@@ -454,7 +454,7 @@ struct WorkShared {
   int scratch[4];
 };
 
-template <int DT, int STEPS, bool NEOX>
+template <int DT, int STEPS, bool NEOX, int PAGE>
 __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
   constexpr int KB = STEPS <= 2 ? 4 : 2;  // the chunk-score batch shape for head_dim <= 128
   __shared__ union {
@@ -510,7 +510,7 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
     const int gw = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x) * kWaves +
                                                   static_cast<int>(threadIdx.x >> 6));
     const int tw = first_selector * kWaves;
-    score::score_stream<DT, STEPS, KB, false, true, true>(sa, w.unit_prefix, w.len, w.qrow, w.unit_prefix[rows], gw,
+    score::score_stream<DT, STEPS, KB, false, PAGE, true>(sa, w.unit_prefix, w.len, w.qrow, w.unit_prefix[rows], gw,
                                                           tw, tag);
     gather_owned<DT, NEOX>(f, s_task_prefix, s_slot, gw, tw, tag);
   }
@@ -581,15 +581,24 @@ int launch_fused(hipStream_t stream, const FusedArgs& f, int64_t upper_units, in
   return rc;
 }
 
-template <int DT>
-int launch_dt(hipStream_t stream, const FusedArgs& f, int steps, bool neox, int64_t upper_units,
-              int64_t upper_tasks, bool& launched) {
+template <int DT, int PAGE>
+int launch_page(hipStream_t stream, const FusedArgs& f, int steps, bool neox, int64_t upper_units,
+                int64_t upper_tasks, bool& launched) {
   if (steps == 4) {
-    if (neox) return launch_fused<fused_step_kernel<DT, 4, true>>(stream, f, upper_units, upper_tasks, launched);
-    return launch_fused<fused_step_kernel<DT, 4, false>>(stream, f, upper_units, upper_tasks, launched);
+    if (neox) return launch_fused<fused_step_kernel<DT, 4, true, PAGE>>(stream, f, upper_units, upper_tasks, launched);
+    return launch_fused<fused_step_kernel<DT, 4, false, PAGE>>(stream, f, upper_units, upper_tasks, launched);
   }
-  if (neox) return launch_fused<fused_step_kernel<DT, 2, true>>(stream, f, upper_units, upper_tasks, launched);
-  return launch_fused<fused_step_kernel<DT, 2, false>>(stream, f, upper_units, upper_tasks, launched);
+  if (neox) return launch_fused<fused_step_kernel<DT, 2, true, PAGE>>(stream, f, upper_units, upper_tasks, launched);
+  return launch_fused<fused_step_kernel<DT, 2, false, PAGE>>(stream, f, upper_units, upper_tasks, launched);
+}
+
+template <int DT>
+int launch_dt(hipStream_t stream, const FusedArgs& f, int steps, bool neox, int page_mode, int64_t upper_units,
+              int64_t upper_tasks, bool& launched) {
+  if (page_mode == score::PAGE_POW2) {
+    return launch_page<DT, score::PAGE_POW2>(stream, f, steps, neox, upper_units, upper_tasks, launched);
+  }
+  return launch_page<DT, score::PAGE_UNIFORM>(stream, f, steps, neox, upper_units, upper_tasks, launched);
 }
 
 }  // namespace
@@ -616,8 +625,8 @@ int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource
 
   FusedArgs f{};
   int64_t upper_units = 0;
-  bool uniform_page = false;
-  int rc = make_score_args(f.s, upper_units, uniform_page, d->dtype, d->query, d->q_stride, d->key_cache,
+  int page_mode = score::PAGE_LANE;
+  int rc = make_score_args(f.s, upper_units, page_mode, d->dtype, d->query, d->q_stride, d->key_cache,
                            d->k_block_stride, d->k_token_stride, d->k_head_stride, d->lse, d->lse_token_stride,
                            d->lse_head_stride, d->block_table, d->bt_stride, src, d->batch_rows, d->num_q_heads,
                            d->num_kv_heads, d->head_dim, d->block_size, d->chunk_size, d->max_chunks, d->scale,
@@ -641,7 +650,7 @@ int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource
   const int steps = d->head_dim / 32;
   const bool fits = d->dtype == d->kv_dtype && (d->dtype == DS_BF16 || d->dtype == DS_FP16) &&
                     (d->head_dim == 64 || d->head_dim == 128) && d->num_kv_heads <= kMaxHkv &&
-                    d->batch_rows >= kMinFusedRows && d->batch_rows <= kFusedRows && uniform_page && vec &&
+                    d->batch_rows >= kMinFusedRows && d->batch_rows <= kFusedRows && page_mode != score::PAGE_LANE && vec &&
                     scalar_grid > 0 && d->slots != nullptr && d->plan_width <= kPlanCols &&
                     64 / f.g.lanes_per_row >= kMinTaskPositions &&
                     (d->gather_rec == nullptr || d->plan_width < kGenCol + 1);
@@ -670,8 +679,8 @@ int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource
   const int ppw = 64 / f.g.lanes_per_row;
   const int64_t upper_tasks = static_cast<int64_t>(d->batch_rows) * ((f.g.pos_limit + ppw - 1) / ppw);
   const bool neox = d->is_neox_style != 0;
-  if (d->dtype == DS_BF16) return launch_dt<DS_BF16>(stream, f, steps, neox, upper_units, upper_tasks, launched);
-  return launch_dt<DS_FP16>(stream, f, steps, neox, upper_units, upper_tasks, launched);
+  if (d->dtype == DS_BF16) return launch_dt<DS_BF16>(stream, f, steps, neox, page_mode, upper_units, upper_tasks, launched);
+  return launch_dt<DS_FP16>(stream, f, steps, neox, page_mode, upper_units, upper_tasks, launched);
 }
 
 }  // namespace ds355

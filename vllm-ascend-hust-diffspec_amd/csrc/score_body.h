@@ -108,25 +108,46 @@ __device__ __forceinline__ f32x4_t mfma16x16x32(const Raw16& a, const Raw16& b, 
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
-// x / d and x % d for x >= 0, by shifts when d is a power of two (lg >= 0).
-__device__ __forceinline__ int udiv(int x, int d, int lg) { return lg >= 0 ? (x >> lg) : x / d; }
-__device__ __forceinline__ int umod(int x, int d, int lg) { return lg >= 0 ? (x & (d - 1)) : x % d; }
+// Raw buffer loads from a wave-uniform base (a resource in scalar registers)
+// at loop-invariant per-lane byte offsets: a batch's loads need no address
+// arithmetic in vector registers (which also made the compiler wait for
+// loads in flight before reusing the registers).
+typedef __amdgpu_buffer_rsrc_t SRsrc;
+__device__ __forceinline__ SRsrc srsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ Raw16 bload16(SRsrc r, int voff) {
+  return __builtin_bit_cast(Raw16, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
+__device__ __forceinline__ float bload4(SRsrc r, int voff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0));
+}
 
 
-// Where a batch sits in the wave's stream.  All fields are wave-uniform.
+
+// Where a batch sits in the wave's stream.  All fields are wave-uniform and
+// 32-bit (the element offsets they imply are worked out where they are used,
+// so two batches and a unit in flight fit the scalar registers).
 struct BatchCtx {
   int valid;
-  int b;
+  int b;     // row
+  int qrow;  // query / LSE row
   int t0;    // first token of the unit
   int len;   // row's scored length
-  int qrow;  // query / LSE row
   int g;     // KV head
   int tg0;   // first 16-token group of the batch within the unit
   int last;  // last batch of the unit
   int c0;    // first chunk of the unit
-  int64_t qbase;  // element offset of (qrow, first query head of g) in q
-  int64_t lbase;  // element offset of (qrow, first query head of g) in lse
+  int chunks_row;  // chunks of the row, ceil(len / chunk)
 };
+
+// How a 16-token group finds its keys.  PAGE_LANE: per-lane block-table
+// lookups (blocks not 16-token aligned).  PAGE_UNIFORM: one scalar lookup per
+// group.  PAGE_POW2: the same with power-of-two block size and KV-head count,
+// so the per-unit and per-group index maths are shifts and masks.
+constexpr int PAGE_LANE = 0;
+constexpr int PAGE_UNIFORM = 1;
+constexpr int PAGE_POW2 = 2;
 
 template <int KB, int STEPS>
 struct Batch {
@@ -175,42 +196,69 @@ __device__ __forceinline__ void flush_pairs(const ScoreArgs& a, const BatchCtx& 
 // per-KV-head chunk sums (partial, or tagged with `tag` when TAGGED); head
 // max stores final chunk scores.  LSEFREE (head mean only): no LSE is read;
 // each chunk's (max, sum) per query head goes to a.mz instead.
-template <int DT, int STEPS, int KB, bool HMAX, bool UNIFORM_PAGE, bool TAGGED, bool LSEFREE = false>
+template <int DT, int STEPS, int KB, bool HMAX, int PAGE, bool TAGGED, bool LSEFREE = false>
 __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_prefix, const int* s_len,
                                              const int* s_qrow, int total, int gw, int tw, uint32_t tag) {
+  constexpr bool UNIFORM_PAGE = PAGE != PAGE_LANE;
+  constexpr bool POW2 = PAGE == PAGE_POW2;
   const int lane = threadIdx.x & 63;
   const int col = lane & 15;   // A row (query head in group) / B column (token in group)
   const int kgrp = lane >> 4;  // 8-element k slice of the 32-wide MFMA step
   const int bph = (a.ntu + KB - 1) / KB;     // batches per KV head of a unit
   const int bpu = bph * (HMAX ? a.Hkv : 1);  // batches per unit
 
+  // The wave's cursor: unit ordinal uk (unit gw + uk * tw), batch uj within
+  // it, and for the head max the head hj and group batch tj within the
+  // span.  Everything a unit's batches share is worked out once, when the
+  // unit starts; a batch only moves its group offset.  next_ctx() hands out
+  // the batches in order, two ahead of the one being computed.  (Integer
+  // division per batch, and both arms of shift-or-divide selects, were most
+  // of the pass's scalar instructions: about 430 per 8 KB batch.)
+  int uk = 0, uj = 0, hj = 0, tj = 0;
   int row_hint = 0;
-  auto ctx_of = [&](int n) -> BatchCtx {
-    BatchCtx c{};
-    const int k = bpu == 1 ? n : n / bpu;
-    const int j = n - k * bpu;
-    const int unit = gw + k * tw;
-    if (unit >= total) return c;
-    int lo = row_hint, hi = a.batch - 1;  // unit positions grow along the stream
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_prefix[mid] <= unit) lo = mid; else hi = mid - 1;
+  BatchCtx u{};  // the current unit
+  auto next_ctx = [&]() -> BatchCtx {
+    if (uj == 0) {
+      u = BatchCtx{};
+      const int unit = gw + uk * tw;
+      if (unit < total) {
+        int lo = row_hint, hi = a.batch - 1;  // unit positions grow along the stream
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (s_prefix[mid] <= unit) lo = mid; else hi = mid - 1;
+        }
+        lo = uniform(lo);
+        row_hint = lo;
+        const int r = unit - uniform(s_prefix[lo]);
+        const int span = HMAX ? r : (POW2 ? r >> a.hkv_log2 : r / a.Hkv);
+        u.valid = 1;
+        u.b = lo;
+        u.t0 = span * a.U;
+        u.len = uniform(s_len[lo]);
+        u.g = HMAX ? 0 : r - span * a.Hkv;
+        u.c0 = span * a.cpu;
+        u.chunks_row = (u.len + a.chunk - 1) / a.chunk;
+        u.qrow = uniform(s_qrow[lo]);
+      }
+      hj = 0;
+      tj = 0;
     }
-    row_hint = lo;
-    const int r = unit - s_prefix[lo];
-    const int span = HMAX ? r : udiv(r, a.Hkv, a.hkv_log2);
-    const int head_in_unit = bph == 1 ? j : j / bph;
-    c.valid = 1;
-    c.b = lo;
-    c.t0 = span * a.U;
-    c.len = s_len[lo];
-    c.qrow = s_qrow[lo];
-    c.g = (HMAX ? 0 : r - span * a.Hkv) + head_in_unit;
-    c.tg0 = (j - head_in_unit * bph) * KB;
-    c.last = j == bpu - 1;
-    c.c0 = span * a.cpu;
-    c.qbase = static_cast<int64_t>(c.qrow) * a.q_stride + static_cast<int64_t>(c.g * a.G) * a.D;
-    c.lbase = static_cast<int64_t>(c.qrow) * a.lse_row_stride + static_cast<int64_t>(c.g * a.G) * a.lse_head_stride;
+    BatchCtx c = u;
+    if (HMAX) {  // one unit covers every KV head of its span, bph batches each
+      c.g = hj;
+      c.tg0 = tj * KB;
+      if (++tj == bph) {
+        tj = 0;
+        ++hj;
+      }
+    } else {
+      c.tg0 = uj * KB;
+    }
+    c.last = uj == bpu - 1;
+    if (++uj == bpu) {
+      uj = 0;
+      ++uk;
+    }
     return c;
   };
 
@@ -225,52 +273,60 @@ __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_pr
   // from the batch computed just before (re-loading them every batch cost
   // about 5 us of a 57 us pass on 16 x 40k-token rows).
   //
-  // kb[i] = element offset of token group i's first row for KV head g
-  // (uniform: the group lies inside one block).  Reading lanes past the row
-  // end stays inside that block.
-  auto pages_of = [&](const BatchCtx& c, int64_t (&kb)[KB]) {
+  // pages_of() only issues the block-table loads (uniform: the group lies
+  // inside one block); the page's address arithmetic waits for load(), one
+  // computed batch later, so the scalar round trip overlaps that batch's
+  // wait and maths.  Reading lanes past the row end stays inside the block.
+  auto group_tok0 = [&](const BatchCtx& c, int i) { return c.t0 + (c.tg0 + i) * 16; };
+  auto group_ok = [&](const BatchCtx& c, int i) {
+    return c.valid && c.tg0 + i < a.ntu && group_tok0(c, i) < c.len;
+  };
+  auto pages_of = [&](const BatchCtx& c, int32_t (&kb)[KB]) {
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
       kb[i] = 0;
       if (UNIFORM_PAGE) {
-        const int tg = c.tg0 + i;
-        const int tok0 = c.t0 + tg * 16;
-        const bool ok = c.valid && tg < a.ntu && tok0 < c.len;
-        const int64_t idx = ok ? static_cast<int64_t>(c.b) * a.bt_stride + uniform(udiv(tok0, a.block_size, a.bs_log2)) : 0;
-        const int64_t page = scalar_load(a.bt + idx);
-        kb[i] = ok ? page * a.k_block_stride + static_cast<int64_t>(umod(tok0, a.block_size, a.bs_log2)) * a.k_token_stride +
-                         static_cast<int64_t>(c.g) * a.k_head_stride
-                   : 0;
+        const int tok0 = group_tok0(c, i);
+        const int blk = POW2 ? tok0 >> a.bs_log2 : tok0 / a.block_size;
+        kb[i] = scalar_load(a.bt + (group_ok(c, i) ? static_cast<int64_t>(c.b) * a.bt_stride + blk : 0));
       }
     }
+  };
+  auto page_base = [&](const BatchCtx& c, int i, int32_t page) -> int64_t {
+    const int tok0 = group_tok0(c, i);
+    const int in_block = POW2 ? tok0 & (a.block_size - 1) : tok0 % a.block_size;
+    return group_ok(c, i) ? static_cast<int64_t>(page) * a.k_block_stride +
+                                static_cast<int64_t>(in_block) * a.k_token_stride +
+                                static_cast<int64_t>(c.g) * a.k_head_stride
+                          : 0;
   };
 
   const int64_t lane_k = static_cast<int64_t>(col) * a.k_token_stride + kgrp * 8;
   const int q_head = min(col, a.G - 1);  // rows >= G read a real head; masked later
 
-  int64_t last_qbase = -1, last_lbase = -1;  // q / LSE of the last loaded batch (wave-uniform)
-  auto load = [&](const BatchCtx& c, const int64_t (&kb)[KB], Batch<KB, STEPS>& out) {
+  int last_qrow = -1, last_g = -1;  // (query row, KV head) of the last loaded batch (wave-uniform)
+  auto load = [&](const BatchCtx& c, const int32_t (&kb)[KB], Batch<KB, STEPS>& out) {
     out.c = c;
-    out.fresh = c.qbase != last_qbase || c.lbase != last_lbase;
-    last_qbase = c.qbase;
-    last_lbase = c.lbase;
+    out.fresh = c.qrow != last_qrow || c.g != last_g;
+    last_qrow = c.qrow;
+    last_g = c.g;
     if (out.fresh) {  // wave-uniform; issued before the keys
-      const uint16_t* qh = a.q + c.qbase + static_cast<int64_t>(q_head) * a.D + kgrp * 8;
+      const uint16_t* qh = a.q + static_cast<int64_t>(c.qrow) * a.q_stride + static_cast<int64_t>(c.g * a.G + q_head) * a.D +
+                           kgrp * 8;
 #pragma unroll
       for (int s = 0; s < STEPS; ++s) out.q[s] = *reinterpret_cast<const Raw16*>(qh + 32 * s);
       if constexpr (!LSEFREE) {
+        const float* lh = a.lse + static_cast<int64_t>(c.qrow) * a.lse_row_stride +
+                          static_cast<int64_t>(c.g * a.G) * a.lse_head_stride;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = min(4 * kgrp + i, a.G - 1);
-          out.lse[i] = a.lse[c.lbase + static_cast<int64_t>(m) * a.lse_head_stride];
-        }
+        for (int i = 0; i < 4; ++i) out.lse[i] = lh[static_cast<int64_t>(min(4 * kgrp + i, a.G - 1)) * a.lse_head_stride];
       }
     }
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
       const uint16_t* krow;
       if (UNIFORM_PAGE) {
-        krow = a.k + kb[i] + lane_k;
+        krow = a.k + page_base(c, i, kb[i]) + lane_k;
       } else {
         const int tg = c.tg0 + i;
         const int tin = tg * 16 + col;
@@ -366,7 +422,7 @@ __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_pr
       }
     }
     if (!c.last) return;
-    const int chunks_row = (c.len + a.chunk - 1) / a.chunk;
+    const int chunks_row = c.chunks_row;
     if (HMAX) {
       for (int cc = 0; cc < a.cpu; ++cc) {
         float s = 0.f;
@@ -417,22 +473,23 @@ __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_pr
   // a half earlier), then the block-table lookups for n+2, then the maths of
   // batch n.  Scalar loads complete out of order, so the lookups are issued
   // after the loads that consume the previous ones.
-  BatchCtx cx0 = ctx_of(0), cx1 = ctx_of(1);
-  int64_t pg0[KB], pg1[KB];
+  BatchCtx cx0 = next_ctx();
+  BatchCtx cx1 = next_ctx();
+  int32_t pg0[KB], pg1[KB];
   pages_of(cx0, pg0);
   pages_of(cx1, pg1);
   Batch<KB, STEPS> d0, d1;
   load(cx0, pg0, d0);
-  for (int n = 0;; n += 2) {
+  for (;;) {
     if (!d0.c.valid) break;
     load(cx1, pg1, d1);
-    cx0 = ctx_of(n + 2);
+    cx0 = next_ctx();
     pages_of(cx0, pg0);
     compute(d0);
     inherit(d1, d0);
     if (!d1.c.valid) break;
     load(cx0, pg0, d0);
-    cx1 = ctx_of(n + 3);
+    cx1 = next_ctx();
     pages_of(cx1, pg1);
     compute(d1);
     inherit(d0, d1);

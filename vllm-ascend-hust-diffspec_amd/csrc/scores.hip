@@ -41,10 +41,11 @@ using namespace score;
 
 // STEPS = head_dim / 32.  KB = 16-token groups per batch.  WGS = workgroups
 // per CU the register budget is sized for.  HMAX = per-token head max.
-// UNIFORM_PAGE = every 16-token group lies inside one block (block_size and
-// the unit start are multiples of 16), so its block-table entry is one
-// scalar load.
-template <int DT, int STEPS, int KB, int WGS, bool HMAX, bool UNIFORM_PAGE, bool LSEFREE>
+// PAGE = how a 16-token group finds its keys (score_body.h): per-lane
+// block-table lookups, one scalar lookup per group (block_size and the unit
+// start multiples of 16), or the same with power-of-two block size and KV
+// heads.
+template <int DT, int STEPS, int KB, int WGS, bool HMAX, int PAGE, bool LSEFREE>
 __global__ __launch_bounds__(kThreads, WGS) void chunk_score_kernel(ScoreArgs a) {
   __shared__ int s_prefix[kMaxRows + 1];
   __shared__ int s_len[kMaxRows];
@@ -62,7 +63,7 @@ __global__ __launch_bounds__(kThreads, WGS) void chunk_score_kernel(ScoreArgs a)
                    [&](int r) { return (s_len[r] + a.U - 1) / a.U * units_per_span; });
   const int total = s_prefix[a.batch];
   const int gw = uniform(blockIdx.x * kWaves + (threadIdx.x >> 6));
-  score_stream<DT, STEPS, KB, HMAX, UNIFORM_PAGE, false, LSEFREE>(a, s_prefix, s_len, s_qrow, total, gw,
+  score_stream<DT, STEPS, KB, HMAX, PAGE, false, LSEFREE>(a, s_prefix, s_len, s_qrow, total, gw,
                                                                   gridDim.x * kWaves, 0u);
 
   if (a.write_tail) {
@@ -246,7 +247,7 @@ __global__ __launch_bounds__(kThreads) void lse_finalize_kernel(const float* __r
 }
 
 template <int DT, int STEPS, bool HMAX, bool LSEFREE>
-void launch_kb(hipStream_t stream, const ScoreArgs& a, int64_t upper_blocks, bool uniform_page) {
+void launch_kb(hipStream_t stream, const ScoreArgs& a, int64_t upper_blocks, int page_mode) {
   // Batch shape, measured on 16 x 40k-token rows: batches of about 8 KB of
   // keys per wave with three workgroups per CU stream faster than 16 KB
   // batches at two (5.4 vs 5.1 TB/s at head_dim 128).  Wider heads and the
@@ -256,24 +257,26 @@ void launch_kb(hipStream_t stream, const ScoreArgs& a, int64_t upper_blocks, boo
   constexpr int WGS = narrow ? 3 : 2;
   const int64_t cap = static_cast<int64_t>(device_cu_count()) * WGS;
   const int grid = static_cast<int>(std::max<int64_t>(1, std::min(upper_blocks, cap)));
-  if (uniform_page) {
-    chunk_score_kernel<DT, STEPS, KB, WGS, HMAX, true, LSEFREE><<<grid, kThreads, 0, stream>>>(a);
+  if (page_mode == PAGE_POW2) {
+    chunk_score_kernel<DT, STEPS, KB, WGS, HMAX, PAGE_POW2, LSEFREE><<<grid, kThreads, 0, stream>>>(a);
+  } else if (page_mode == PAGE_UNIFORM) {
+    chunk_score_kernel<DT, STEPS, KB, WGS, HMAX, PAGE_UNIFORM, LSEFREE><<<grid, kThreads, 0, stream>>>(a);
   } else {
-    chunk_score_kernel<DT, STEPS, KB, WGS, HMAX, false, LSEFREE><<<grid, kThreads, 0, stream>>>(a);
+    chunk_score_kernel<DT, STEPS, KB, WGS, HMAX, PAGE_LANE, LSEFREE><<<grid, kThreads, 0, stream>>>(a);
   }
 }
 
 template <int DT, bool HMAX, bool LSEFREE>
-void launch_steps(hipStream_t stream, const ScoreArgs& a, int64_t grid, bool uniform_page) {
+void launch_steps(hipStream_t stream, const ScoreArgs& a, int64_t grid, int page_mode) {
   switch (a.D / 32) {
-    case 1: launch_kb<DT, 1, HMAX, LSEFREE>(stream, a, grid, uniform_page); break;
-    case 2: launch_kb<DT, 2, HMAX, LSEFREE>(stream, a, grid, uniform_page); break;
-    case 3: launch_kb<DT, 3, HMAX, LSEFREE>(stream, a, grid, uniform_page); break;
-    case 4: launch_kb<DT, 4, HMAX, LSEFREE>(stream, a, grid, uniform_page); break;
-    case 5: launch_kb<DT, 5, HMAX, LSEFREE>(stream, a, grid, uniform_page); break;
-    case 6: launch_kb<DT, 6, HMAX, LSEFREE>(stream, a, grid, uniform_page); break;
-    case 7: launch_kb<DT, 7, HMAX, LSEFREE>(stream, a, grid, uniform_page); break;
-    default: launch_kb<DT, 8, HMAX, LSEFREE>(stream, a, grid, uniform_page); break;
+    case 1: launch_kb<DT, 1, HMAX, LSEFREE>(stream, a, grid, page_mode); break;
+    case 2: launch_kb<DT, 2, HMAX, LSEFREE>(stream, a, grid, page_mode); break;
+    case 3: launch_kb<DT, 3, HMAX, LSEFREE>(stream, a, grid, page_mode); break;
+    case 4: launch_kb<DT, 4, HMAX, LSEFREE>(stream, a, grid, page_mode); break;
+    case 5: launch_kb<DT, 5, HMAX, LSEFREE>(stream, a, grid, page_mode); break;
+    case 6: launch_kb<DT, 6, HMAX, LSEFREE>(stream, a, grid, page_mode); break;
+    case 7: launch_kb<DT, 7, HMAX, LSEFREE>(stream, a, grid, page_mode); break;
+    default: launch_kb<DT, 8, HMAX, LSEFREE>(stream, a, grid, page_mode); break;
   }
 }
 
@@ -282,7 +285,7 @@ void launch_steps(hipStream_t stream, const ScoreArgs& a, int64_t grid, bool uni
 // Shared by ds_chunk_scores and the fused step.  With head_reduce = mean the
 // kernel writes per-KV-head partials ([batch, max_chunks, Hkv] in `partial`);
 // with max it writes final scores to `out` (and zero tails if write_tail).
-int make_score_args(ScoreArgs& a, int64_t& upper_units, bool& uniform_page, int dtype, const void* query,
+int make_score_args(ScoreArgs& a, int64_t& upper_units, int& page_mode, int dtype, const void* query,
                     int64_t q_stride, const void* key_cache, int64_t k_block_stride, int64_t k_token_stride,
                     int64_t k_head_stride, const float* lse, int64_t lse_row_stride, int64_t lse_head_stride,
                     const int32_t* block_table, int64_t bt_stride, const RowSource& src, int batch, int num_q_heads,
@@ -290,6 +293,7 @@ int make_score_args(ScoreArgs& a, int64_t& upper_units, bool& uniform_page, int 
                     int head_reduce, float* partial, float* out, int64_t out_stride, int write_tail,
                     size_t partial_bytes, float* mz) {
   upper_units = 0;
+  page_mode = PAGE_LANE;
   DS_REQUIRE(dtype == DS_BF16 || dtype == DS_FP16, "chunk scores support BF16 or FP16 query/key caches");
   DS_REQUIRE(num_q_heads > 0 && num_kv_heads > 0 && num_q_heads % num_kv_heads == 0,
              "query heads must be divisible by KV heads");
@@ -306,6 +310,9 @@ int make_score_args(ScoreArgs& a, int64_t& upper_units, bool& uniform_page, int 
              "query and key strides must be multiples of 8 elements (16-byte rows)");
   DS_REQUIRE((reinterpret_cast<uintptr_t>(query) & 15u) == 0 && (reinterpret_cast<uintptr_t>(key_cache) & 15u) == 0,
              "query and key cache must be 16-byte aligned");
+  // A query group's and an LSE group's loads use 32-bit byte offsets.
+  DS_SUPPORTED(lse_head_stride >= 0 && lse_head_stride <= (static_cast<int64_t>(INT32_MAX) / 4 - 1) / kMaxGroup,
+               "softmax LSE head stride %lld is too large", static_cast<long long>(lse_head_stride));
   const bool hmax = head_reduce == DS_HEAD_MAX;
   // Unit span: whole chunks, at least 64 tokens when the chunk divides 64.
   int cpu = 1;
@@ -374,7 +381,12 @@ int make_score_args(ScoreArgs& a, int64_t& upper_units, bool& uniform_page, int 
 
   const int64_t spans = (static_cast<int64_t>(max_chunks) * chunk_size + U - 1) / U;
   upper_units = static_cast<int64_t>(batch) * spans * (hmax ? 1 : num_kv_heads);
-  uniform_page = (block_size % 16 == 0) && (U % 16 == 0);
+  // The uniform paths load a 16-token group through a buffer resource with
+  // 32-bit byte offsets: 16 key rows must span less than 2 GiB.
+  page_mode = PAGE_LANE;
+  if (block_size % 16 == 0 && U % 16 == 0 && k_token_stride <= (static_cast<int64_t>(INT32_MAX) / 32)) {
+    page_mode = a.bs_log2 >= 0 && a.hkv_log2 >= 0 ? PAGE_POW2 : PAGE_UNIFORM;
+  }
   return clear_error();
 }
 
@@ -387,8 +399,8 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
                         float* mz, float* lse_out, int64_t lse_out_stride) {
   ScoreArgs a{};
   int64_t upper_units = 0;
-  bool uniform_page = false;
-  const int rc = make_score_args(a, upper_units, uniform_page, dtype, query, q_stride, key_cache, k_block_stride,
+  int page_mode = PAGE_LANE;
+  const int rc = make_score_args(a, upper_units, page_mode, dtype, query, q_stride, key_cache, k_block_stride,
                                  k_token_stride, k_head_stride, lse, lse_row_stride, lse_head_stride, block_table,
                                  bt_stride, src, batch, num_q_heads, num_kv_heads, head_dim, block_size, chunk_size,
                                  max_chunks, scale, head_reduce, partial, out, out_stride, write_tail, partial_bytes,
@@ -407,13 +419,13 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
   }
   const int64_t upper_blocks = (upper_units + kWaves - 1) / kWaves;
   if (dtype == DS_BF16) {
-    if (hmax) launch_steps<DS_BF16, true, false>(stream, a, upper_blocks, uniform_page);
-    else if (lse_free) launch_steps<DS_BF16, false, true>(stream, a, upper_blocks, uniform_page);
-    else launch_steps<DS_BF16, false, false>(stream, a, upper_blocks, uniform_page);
+    if (hmax) launch_steps<DS_BF16, true, false>(stream, a, upper_blocks, page_mode);
+    else if (lse_free) launch_steps<DS_BF16, false, true>(stream, a, upper_blocks, page_mode);
+    else launch_steps<DS_BF16, false, false>(stream, a, upper_blocks, page_mode);
   } else {
-    if (hmax) launch_steps<DS_FP16, true, false>(stream, a, upper_blocks, uniform_page);
-    else if (lse_free) launch_steps<DS_FP16, false, true>(stream, a, upper_blocks, uniform_page);
-    else launch_steps<DS_FP16, false, false>(stream, a, upper_blocks, uniform_page);
+    if (hmax) launch_steps<DS_FP16, true, false>(stream, a, upper_blocks, page_mode);
+    else if (lse_free) launch_steps<DS_FP16, false, true>(stream, a, upper_blocks, page_mode);
+    else launch_steps<DS_FP16, false, false>(stream, a, upper_blocks, page_mode);
   }
   int rc2 = check_launch("ds_chunk_scores");
   if (rc2 != DS_OK || !lse_free) return rc2;

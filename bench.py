@@ -407,6 +407,11 @@ def run(args):
                 continue
             log(f"workload {name}")
             workloads[name] = workload_leg(name, args.seed, device, with_cpu=not args.no_cpu_baseline)
+        # The measured workload at two more seeds (other lengths, keys and page order).
+        for extra in (0, 1, 2):
+            if extra != args.seed:
+                log(f"workload {args.workload} seed {extra}")
+                workloads[f"{args.workload} seed {extra}"] = workload_leg(args.workload, extra, device, with_cpu=False)
 
     result = {
         "metric": METRIC,
@@ -655,6 +660,8 @@ def workload_leg(name, seed, device, steps=20, with_cpu=True):
                   + f", context {spec['lens']}, Hq {spec['hq']} / Hkv {hkv} x {d}, chunk {chunk}, token budget "
                     f"{token_budget}, history {hb}, window {spec.get('window', RECENT_WINDOW)}"
                   + (", half the rows keep their working rows" if spec.get("reuse_half") else ""),
+        "seed": seed,
+        "scored_tokens": sum(n for n, c in zip(inp["committed"], inp["counts"]) if c > 0),
         "path": "single launch" if single else "chain",
         "step_us": round(step_us, 2),
         "algorithmic_bytes": chain_bytes,

@@ -339,6 +339,67 @@ def test_runtime_retrieval_and_rebuild_match_oracle(cuda, lse_free):
         torch.testing.assert_close(cache.scored_lse[rows_idx].cpu(), case["lse"][q_index], rtol=1e-5, atol=1e-4)
 
 
+def test_runtime_adaptive_cadence_on_device(cuda):
+    """adaptive_profile=True on the GPU (diffspec/runtime.py:575-593, fed at :1309-1331): the slot selections
+    before and after each retrieval reach pinned host memory on the stream, equal to the device state, and the
+    next retrieval call applies the comparison before it reads the interval.  The same snapshot retrieved twice
+    keeps every chunk (interval doubled); a different query for the first committed row resets it."""
+    from types import SimpleNamespace
+
+    from ds355 import runtime
+
+    g = gen(23)
+    rows = 6
+    lens = [int(x) for x in torch.randint(6000, 16000, (rows,), generator=g)]
+    counts = [3, 1, 4, 2, 5, 1]
+    case = build_case(23, real_rows=rows, pad_rows=0, target_lens=lens, query_len=5, counts=counts, hq=32, hkv=4,
+                      head_dim=128, chunk=64, token_budget=2048, block_size=128, lmax=16000,
+                      slots=list(range(rows)), num_slots=rows)
+
+    class Rotary:
+        rotary_dim = 128
+        is_neox_style = True
+        cos_sin_cache = case["cos_sin"].to(cuda)
+
+    settings = runtime.DiffSpecSettings(chunk_size=64, token_budget=2048, retrieval_interval=1, max_tree_nodes=4,
+                                        max_tree_depth=4, tree_threshold=0.7, adaptive_profile=True)
+    cache = runtime.DiffSpecDraftCache(settings, max_num_reqs=rows, max_model_len=16000, num_kv_heads=4,
+                                       head_dim=128, target_num_layers=2, dtype=torch.bfloat16, device=cuda,
+                                       rotary_embedding=Rotary())
+    ids = [f"request-{i}" for i in range(rows)]
+    meta = SimpleNamespace(actual_seq_lengths_q=case["ends"], seq_lens_list=case["tlens"],
+                           block_tables=case["table"].to(cuda), num_prefills=0)
+    key_cache, lse = case["key_cache"].to(cuda), case["lse"].to(cuda)
+
+    def retrieve(query):
+        cache.begin_target_forward(ids)
+        cache.capture_target_attention(query, lse, key_cache, meta, case["scale"])
+        cache.accept_target_queries(torch.tensor(counts, dtype=torch.int32, device=cuda), is_prefill=False)
+
+    query = case["query"].to(cuda)
+    retrieve(query)  # cycle 1: no selection before it
+    torch.cuda.synchronize()
+    assert torch.equal(cache._adaptive_sel_count[0], torch.full((rows,), -1, dtype=torch.int32))
+    assert torch.equal(cache._adaptive_ids[1], cache.sel_ids.cpu())
+    assert torch.equal(cache._adaptive_sel_count[1], cache.sel_count.cpu())
+    first = cache.sel_ids[0, : int(cache.sel_count[0])].cpu().tolist()
+    retrieve(query)  # cycle 2 applies cycle 1 (overlap 0 -> base), then retrieves the same chunks again
+    assert cache.retrieval_interval == 1
+    cache._observe_previous_retrieval()  # what cycle 3 would apply first: overlap 1, acceptance 2 -> doubled
+    assert cache.retrieval_interval == 2
+    assert cache.sel_ids[0, : int(cache.sel_count[0])].cpu().tolist() == first
+    other = torch.randn(query.shape, generator=torch.Generator().manual_seed(5)).to(query.dtype).to(cuda)
+    cache.begin_target_forward(ids)
+    cache.capture_target_attention(other, lse, key_cache, meta, case["scale"])
+    cache.accept_target_queries(torch.tensor(counts, dtype=torch.int32, device=cuda), is_prefill=False)  # 3 % 2
+    assert cache.metrics.retrieval_skipped_interval == 1
+    retrieve(other)  # cycle 4: retrieves with the new query
+    cache._observe_previous_retrieval()
+    changed = cache.sel_ids[0, : int(cache.sel_count[0])].cpu().tolist()
+    union, inter = set(first) | set(changed), set(first) & set(changed)
+    assert len(inter) / len(union) < 0.9 and cache.retrieval_interval == 1
+
+
 def test_runtime_populate_prefill_then_compact_prefill(cuda):
     """The proposer's compact-draft-root sequence (proposer.py:256-307) on the GPU:
     accept_target_queries (score + select), begin_cycle, populate_prefill of every

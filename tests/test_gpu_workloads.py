@@ -39,7 +39,9 @@ from helpers import O, assert_scores_close
 
 pytestmark = pytest.mark.gpu
 
-SEED = 0
+# Seed 0 for every workload; the headline workload also at seeds 1 and 2
+# (its lengths, keys, queries and page order all change with the seed).
+CASES = [(name, 0) for name in sorted(bench.WORKLOADS)] + [("ragged16-40k", 1), ("ragged16-40k", 2)]
 
 
 def _state(inp, spec, device):
@@ -95,23 +97,23 @@ def _check_selection_margin(gpu_ids, oracle_scores, length, chunk, hb):
     return len(differing)
 
 
-@pytest.mark.parametrize("name", sorted(bench.WORKLOADS))
-def test_workload_step_matches_oracle(cuda, name):
+@pytest.mark.parametrize("name,seed", CASES, ids=[f"{n}-seed{s}" for n, s in CASES])
+def test_workload_step_matches_oracle(cuda, name, seed):
     from ds355 import step
     from ds355.plan import history_budget
 
-    print(f"workload {name}, seed {SEED}", flush=True)
+    print(f"workload {name}, seed {seed}", flush=True)
     spec = bench.WORKLOADS[name]
     chunk, budget, d = spec["chunk"], spec["budget"], spec["d"]
     window = spec.get("window", bench.RECENT_WINDOW)
     hb = history_budget(budget, bench.DRAFT_TOKENS, chunk)
-    inp = bench.build_inputs(spec, SEED, cuda)
+    inp = bench.build_inputs(spec, seed, cuda)
     rows, total = inp["rows"], inp["total_rows"]
     cos_sin = O.rope_cos_sin_cache(d, budget, base=bench.ROPE_THETA)
     cos_dev = cos_sin.to(cuda)
     row_active = None
     if spec.get("reuse_half"):
-        g = torch.Generator().manual_seed(SEED + 7)
+        g = torch.Generator().manual_seed(seed + 7)
         row_active = [int(x) for x in (torch.rand(total, generator=g) >= 0.5)]
 
     chain = _state(inp, spec, cuda)

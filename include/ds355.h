@@ -172,13 +172,14 @@ enum ds_stage { DS_STAGE_SCORE = 1, DS_STAGE_SELECT = 2, DS_STAGE_PLAN = 4, DS_S
 
 /*
  * DS_STAGE_PREFIX (in place of DS_STAGE_PLAN): plan rows and working_lens as
- * DS_STAGE_PLAN writes them, but only the gather tasks wholly inside each
- * row's history prefix, the positions before the rolling tail, are moved.
- * Those read raw rows well before the committed root, which the draft's
- * prefill does not rewrite, so the retrieval call can move them before
- * populate_prefill and the compact prefill then moves only the rest.  Needs
- * gather records (below) and DS_STAGE_SELECT in the same call (it reads the
- * verifier rows); committed_lens may be NULL (each row's scored length is
+ * DS_STAGE_PLAN writes them, but only the gather tasks whose raw rows all lie
+ * below the first row the draft's prefill of this step rewrites (each row's
+ * first verifier query position, target_len - query_len) are moved: the
+ * history prefix and the rolling tail up to that row.  The retrieval call can
+ * move them before populate_prefill; the compact prefill then finds them
+ * recorded and moves only the rest (the verifier's accepted positions).
+ * Needs gather records (below) and DS_STAGE_SELECT in the same call (it reads
+ * the verifier rows); committed_lens may be NULL (each row's scored length is
  * used, 0 for rows that committed nothing).  SCORE | SELECT | PREFIX with a
  * workspace runs as the single launch.
  *
@@ -187,10 +188,13 @@ enum ds_stage { DS_STAGE_SCORE = 1, DS_STAGE_SELECT = 2, DS_STAGE_PLAN = 4, DS_S
  * increments it too when a different request takes the slot), and per
  * (slot, gather task of the plan's local positions) what the working cache
  * holds: (generation << 32) | (prefix drop + 1) for a task wholly inside the
- * history prefix, else 0.  A PLAN or PREFIX gather leaves out every task
- * whose record already matches the plan, since its bytes would not change,
- * and keeps the records.  Raw rows before a request's committed root must
- * not change while the request holds its slot.  Zero-filled by the owner.
+ * history prefix, (generation << 32) | 2^31 | history end (the root
+ * position) for another task wholly inside the history, else 0.  A PLAN or
+ * PREFIX gather leaves out every task whose record already matches the plan,
+ * since its bytes would not change, and keeps the records.  Raw rows before a
+ * request's committed root must not change while the request holds its slot,
+ * and the working cache only at and past each history's end.  Zero-filled by
+ * the owner.
  */
 
 typedef struct ds_step_desc {

@@ -289,6 +289,7 @@ __device__ __forceinline__ void select_row(const FusedArgs& f, int b, uint32_t t
 // the columns, lane l holding columns l (lo) and 64 + l (hi).
 struct PlanView {
   int64_t slot, len, tail_start, prefix_len, drop;
+  int64_t hist_len;  // the plan's history length (len is it clipped to the cos/sin rows)
   uint32_t lo, hi;
   uint32_t gen;  // the slot's selection generation (with gather records)
 };
@@ -308,8 +309,8 @@ __device__ __forceinline__ bool poll_plan(const FusedArgs& f, int r, uint32_t ta
       v.lo = static_cast<uint32_t>(a);
       v.hi = static_cast<uint32_t>(b);
       v.slot = static_cast<int32_t>(__builtin_amdgcn_readlane(v.lo, 0));
-      v.len = min(static_cast<int64_t>(static_cast<int32_t>(__builtin_amdgcn_readlane(v.lo, 1))),
-                  static_cast<int64_t>(ga.pos_limit));
+      v.hist_len = static_cast<int32_t>(__builtin_amdgcn_readlane(v.lo, 1));
+      v.len = min(v.hist_len, static_cast<int64_t>(ga.pos_limit));
       v.tail_start = static_cast<int32_t>(__builtin_amdgcn_readlane(v.lo, 2));
       v.prefix_len = static_cast<int32_t>(__builtin_amdgcn_readlane(v.lo, 3));
       v.drop = static_cast<int32_t>(__builtin_amdgcn_readlane(v.lo, 4));
@@ -352,11 +353,14 @@ __device__ __forceinline__ void gather_recorded(const FusedArgs& f, const gather
                                                 int r, int t, uint64_t have) {
   const int ppw = 64 / f.g.lanes_per_row;
   const int p0 = t * ppw;
-  // Before the draft's prefill, only a row whose prefix sources (all below
-  // tail_start) precede the rows that prefill rewrites is moved.
-  const bool early_ok = !f.prefix_only || v.tail_start <= first_rewritten(f.p.src, r);
+  // Before the draft's prefill (prefix_only), only a task whose raw rows all
+  // precede the rows that prefill rewrites is moved (and recorded).
+  const bool early_ok =
+      !f.prefix_only || gather::sources_final(p0, ppw, v.tail_start, v.prefix_len, first_rewritten(f.p.src, r));
   const uint64_t want =
-      p0 + ppw <= v.len && early_ok ? gather::prefix_record(p0, ppw, v.prefix_len, v.drop, v.gen) : 0u;
+      p0 + ppw <= v.len && early_ok
+          ? gather::history_record(p0, ppw, v.hist_len, v.tail_start, v.prefix_len, v.drop, v.gen)
+          : 0u;
   bool move = !f.prefix_only || want != 0u;
   if (f.rec != nullptr && v.slot >= 0 && v.slot < f.g.num_slots) {
     have = static_cast<uint64_t>(uniform64(static_cast<int64_t>(have)));

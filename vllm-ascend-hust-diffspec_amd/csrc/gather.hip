@@ -225,12 +225,13 @@ __global__ __launch_bounds__(kThreads) void plan_gather_kernel(GatherArgs a, Pla
   const int64_t limit = min(len, static_cast<int64_t>(a.pos_limit));
   if (!active) return;
   // The wave's record (its own entry: read before it is rewritten, by this
-  // wave only), and whether its task is moved at all.
-  // A task cut by the position limit is not moved whole: no record.
-  // Before the draft's prefill, only a row whose prefix sources (all below
-  // tail_start) precede the rows that prefill rewrites is moved.
-  const bool early_ok = !ps.prefix_only || tail_start <= first_rewritten(ps.src, r);
-  const uint64_t want = p0 + ppw <= limit && early_ok ? prefix_record(p0, ppw, prefix_len, drop, gen) : 0u;
+  // wave only), and whether its task is moved at all.  A task cut by the
+  // position limit is not moved whole: no record.  Before the draft's
+  // prefill (prefix_only), only a task whose raw rows all precede the rows
+  // that prefill rewrites is moved (and recorded).
+  const bool early_ok = !ps.prefix_only || sources_final(p0, ppw, tail_start, prefix_len, first_rewritten(ps.src, r));
+  const uint64_t want =
+      p0 + ppw <= limit && early_ok ? history_record(p0, ppw, len, tail_start, prefix_len, drop, gen) : 0u;
   bool move = p0 < limit && (!ps.prefix_only || want != 0u);
   if (ps.rec != nullptr) {
     have = static_cast<uint64_t>(uniform64(static_cast<int64_t>(have)));

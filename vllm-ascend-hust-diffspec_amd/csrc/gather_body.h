@@ -380,16 +380,39 @@ __device__ __forceinline__ void gather_task(const GatherArgs& a, const GatherLan
 
 // Gather records: what the working cache holds per (slot, task of ppw local
 // positions), so a rebuild can leave out tasks whose bytes it would rewrite
-// unchanged.  A task of local positions [p0, p0 + ppw) lying wholly in the
-// plan's history prefix (p0 + ppw <= prefix_len) holds bytes that depend only
-// on the slot's chunk ids, the prefix drop and the raw rows they point to,
-// so its record is (selection generation << 32) | (drop + 1); every other
-// task's record is 0.  Raw rows before a request's committed root are not
-// rewritten while the request holds its slot (the draft only appends), and
-// a slot's generation changes with every stored selection and every change
-// of the request holding it, so an equal record means equal bytes.
-__device__ __forceinline__ uint64_t prefix_record(int p0, int ppw, int64_t prefix_len, int64_t drop, uint32_t gen) {
-  return p0 + ppw <= prefix_len ? (static_cast<uint64_t>(gen) << 32) | static_cast<uint64_t>(drop + 1) : 0u;
+// unchanged.
+//   - A task of local positions [p0, p0 + ppw) lying wholly in the plan's
+//     history prefix (p0 + ppw <= prefix_len) holds bytes that depend only
+//     on the slot's chunk ids, the prefix drop and the raw rows they point
+//     to: its record is (selection generation << 32) | (drop + 1), which
+//     stays valid from one draft cycle to the next.
+//   - Any other task wholly inside the history (p0 + ppw <= len) depends on
+//     the whole plan, which is a function of the slot's selection and the
+//     history end (the root position, tail_start + len - prefix_len): its
+//     record is (generation << 32) | 2^31 | end, valid for that root only.
+//   - A task cut by the history's end has record 0.
+// Raw rows before a request's committed root are not rewritten while the
+// request holds its slot (the draft only appends), the draft attention
+// writes the working cache only at and past the history's end, and a slot's
+// generation changes with every stored selection and every change of the
+// request holding it, so an equal record means equal bytes.  drop + 1 and
+// end are below 2^31, so the two kinds never meet.
+__device__ __forceinline__ uint64_t history_record(int p0, int ppw, int64_t len, int64_t tail_start,
+                                                   int64_t prefix_len, int64_t drop, uint32_t gen) {
+  const uint64_t g = static_cast<uint64_t>(gen) << 32;
+  if (p0 + ppw <= prefix_len) return g | static_cast<uint64_t>(drop + 1);
+  if (p0 + ppw <= len) return g | 0x80000000u | static_cast<uint64_t>(tail_start + len - prefix_len);
+  return 0u;
+}
+
+// Whether every raw row task [p0, p0 + ppw) reads lies below `first_rw`, the
+// first raw position the draft's prefill of this step rewrites: prefix rows
+// lie below tail_start, tail position p reads tail_start + p - prefix_len.
+__device__ __forceinline__ bool sources_final(int p0, int ppw, int64_t tail_start, int64_t prefix_len,
+                                              int64_t first_rw) {
+  const int64_t last = p0 + ppw - 1;
+  if (tail_start > first_rw) return false;
+  return last < prefix_len || tail_start + (last - prefix_len) < first_rw;
 }
 
 }  // namespace gather

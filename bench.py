@@ -383,19 +383,22 @@ def run(args):
             raise RuntimeError(f"single-launch status words {status} after the stage timings: results not valid")
     # The runtime's own path: its two calls (retrieval, then compact prefill),
     # with gather records as DiffSpecDraftCache keeps them.
+    from ds355.runtime import SINGLE_LAUNCH_MIN_ROWS
+
+    # The runtime's default: the final history rows move at retrieval when it runs as the single launch.
     runtime_step = runtime_path(copies, states, rows_t, rows, cos_sin, spec, hb, row_active, device, reps,
-                                prefix=True)
+                                prefix=rows >= SINGLE_LAUNCH_MIN_ROWS)
     two_call_us = runtime_step["total_us"]
     runtime_step.update({
         "what": "DiffSpecDraftCache's calls per retrieval step, kernel time, as the runtime makes them by default: "
-                "accept_target_queries (SCORE | SELECT | PREFIX: also every history row whose raw sources are "
-                "final) and prepare_compact_prefill (PLAN with gather records: the accepted positions); and a "
-                "compact prefill between retrievals",
+                "accept_target_queries (SCORE | SELECT, and PREFIX, every history row whose raw sources are final, "
+                "when the retrieval runs as the single launch) and prepare_compact_prefill (PLAN with gather "
+                "records); and a compact prefill between retrievals",
         "algorithmic_bytes": chain_bytes,
         "achieved_gbps": round(chain_bytes / (two_call_us * 1e-6) / 1e9, 1),
         "frac": round(chain_bytes / (two_call_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
-        "score_select_retrieval": runtime_path(copies, states, rows_t, rows, cos_sin, spec, hb, row_active, device,
-                                               reps),
+        "other_retrieval": runtime_path(copies, states, rows_t, rows, cos_sin, spec, hb, row_active, device,
+                                               reps, prefix=rows < SINGLE_LAUNCH_MIN_ROWS),
         "without_records": runtime_path(copies, states, rows_t, rows, cos_sin, spec, hb, row_active, device, reps,
                                         records=False),
     })
@@ -550,7 +553,7 @@ def runtime_path(copies, states, rows_t, rows, cos_sin, spec, hb, row_active, de
     held_tasks = sum(int((rec[1] != 0).sum()) for _, _, rec in pairs if rec is not None) // len(pairs)
     del pairs
     return {
-        "retrieval_path": "single launch" if single else "chain",
+        "retrieval_path": "single launch" if single else "chain", "final_rows_at_retrieval": bool(prefix),
         "retrieval_us": round(retrieval_us, 2), "compact_prefill_us": round(prefill_us, 2),
         "total_us": round(retrieval_us + prefill_us, 2),
         "compact_prefill_between_retrievals_us": round(held_us, 2),
@@ -655,8 +658,10 @@ def workload_leg(name, seed, device, steps=20, with_cpu=True):
     plan_lens = keep[0]["plan"][:, 1].tolist()
     score_bytes, gather_bytes, chain_bytes = algorithmic_bytes(spec, inp, plan_lens, active)
     gbps = chain_bytes / (step_us * 1e-6) / 1e9
+    from ds355.runtime import SINGLE_LAUNCH_MIN_ROWS
+
     rt = runtime_path(copies, keep, rows_t, rows, cos_sin, spec, hb, row_active, device, max(10, steps // 2),
-                      prefix=True)
+                      prefix=rows >= SINGLE_LAUNCH_MIN_ROWS)
     two_call = rt["total_us"]
     leg = {
         "config": f"{rows} requests" + (f" + {spec['pad']} padding rows" if spec.get("pad") else "")
@@ -675,8 +680,9 @@ def workload_leg(name, seed, device, steps=20, with_cpu=True):
                  f"of {step_bytes / 1e6:.0f} MB and {gather_bytes / 1e6:.0f} MB against the 256 MB MALL)"),
         "copies": len(copies),
         "runtime_two_calls_us": dict(rt, frac=round(chain_bytes / (two_call * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
-                                     score_select_retrieval=runtime_path(copies, keep, rows_t, rows, cos_sin, spec,
-                                                                         hb, row_active, device, max(10, steps // 2)),
+                                     other_retrieval=runtime_path(copies, keep, rows_t, rows, cos_sin, spec, hb,
+                                                                  row_active, device, max(10, steps // 2),
+                                                                  prefix=rows < SINGLE_LAUNCH_MIN_ROWS),
                                      without_records=runtime_path(copies, keep, rows_t, rows, cos_sin, spec, hb,
                                                                   row_active, device, max(10, steps // 2),
                                                                   records=False)),

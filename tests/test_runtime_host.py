@@ -115,7 +115,7 @@ def test_retrieval_skips_prefill_snapshot_and_interval(launches):
     cache.accept_target_queries(torch.tensor([1, 1]), is_prefill=False)
     assert len(launches) == 1
     call = launches[0]
-    assert call["stages"] == step.SCORE | step.SELECT | step.PREFIX  # the final history rows too
+    assert call["stages"] == step.SCORE | step.SELECT  # 2 rows: the chain, so no rows moved at retrieval
     assert _first(call["rows"].counts, call["rows"].batch_size) == [1, 1]
     assert _first(call["rows"].query_start, call["rows"].batch_size) == [0, 1]
     assert _first(call["rows"].query_len, call["rows"].batch_size) == [1, 1]
@@ -341,7 +341,7 @@ def test_linear_call_sequence_of_the_plugin(launches, attention_calls, capture_c
     cache.clear_proposed_tree()
     assert cache.proposed_token_ids is None and cache.proposed_depths_cpu == []
     cache.accept_target_queries(torch.tensor([2, 4]), is_prefill=cache.target_is_prefill)
-    assert launches[-1]["stages"] == step.SCORE | step.SELECT | step.PREFIX
+    assert launches[-1]["stages"] == step.SCORE | step.SELECT
     assert _first(launches[-1]["rows"].counts, 2) == [2, 4]
     assert not cache.target_tree_active  # prepare_inputs_padded returns its result unchanged
     with pytest.raises(RuntimeError, match="tree has not been verified"):
@@ -458,7 +458,7 @@ def test_gather_records_follow_the_slot_map(launches):
     """A request leaving its slot changes that slot's selection generation (its
     gather records describe the request that left); slots that keep their
     request keep theirs.  Every rebuild passes the cache's records, and the
-    retrieval call moves the final history rows unless prefix_at_retrieval is off."""
+    retrieval call moves the final history rows when it runs as the single launch (prefix_at_retrieval)."""
     cache = _cache()
     cache.set_active_requests(["a", "b", "c"])
     assert cache.sel_gen.tolist() == [0, 0, 0, 0]
@@ -473,8 +473,13 @@ def test_gather_records_follow_the_slot_map(launches):
     assert launches[-1]["stages"] == step.PLAN
     assert gen.tolist() == cache.sel_gen.tolist() and records.shape == cache.gather_records.shape
     assert runtime.RETRIEVAL_STAGES == step.SCORE | step.SELECT
-    assert cache.retrieval_stages == step.SCORE | step.SELECT | step.PREFIX  # the default
-    assert _cache(prefix_at_retrieval=False).retrieval_stages == step.SCORE | step.SELECT
+    lse = torch.zeros(1)
+    # By default the final history rows move at retrieval exactly when it runs as the single launch.
+    assert cache.retrieval_stages_for(8, lse) == step.SCORE | step.SELECT | step.PREFIX
+    assert cache.retrieval_stages_for(7, lse) == step.SCORE | step.SELECT
+    assert cache.retrieval_stages_for(16, None) == step.SCORE | step.SELECT
+    assert _cache(prefix_at_retrieval=False).retrieval_stages_for(16, lse) == step.SCORE | step.SELECT
+    assert _cache(prefix_at_retrieval=True).retrieval_stages_for(1, None) == step.SCORE | step.SELECT | step.PREFIX
 
 
 def _speculative_config(**overrides):

@@ -256,11 +256,14 @@ class _Staging:
 
 
 WORKING_LENS = "working_lens"  # pending positions = the slots' device working lengths
-# The retrieval call: score and select; with prefix_at_retrieval (the
-# default) also every history row whose raw sources are final, all but the
-# verifier's accepted positions (one launch for 8+ rows with a supplied LSE).
+# The retrieval call: score and select; with prefix_at_retrieval also every
+# history row whose raw sources are final, all but the verifier's accepted
+# positions.
 RETRIEVAL_STAGES = _step.SCORE | _step.SELECT
 PREFIX_RETRIEVAL_STAGES = _step.SCORE | _step.SELECT | _step.PREFIX
+# Batches from which a step with a supplied LSE and a workspace runs as the
+# single launch (the library's minimum, csrc/fused.hip kMinFusedRows).
+SINGLE_LAUNCH_MIN_ROWS = 8
 
 
 class DiffSpecDraftCache:
@@ -294,7 +297,7 @@ class DiffSpecDraftCache:
         target_tensor_parallel_size: int = 1,
         max_batch_rows: int | None = None,
         lse_free_scoring: bool = False,
-        prefix_at_retrieval: bool = True,
+        prefix_at_retrieval: bool | None = None,
         recent_window: int | None = None,
     ) -> None:
         if target_tensor_parallel_size < 1:
@@ -337,15 +340,19 @@ class DiffSpecDraftCache:
         # rows are final before the draft's prefill (the history prefix and
         # the rolling tail up to the verifier's first query position), and the
         # compact prefill after it finds them recorded and moves the accepted
-        # positions only: at 16 rows x 40k tokens 85.5 + 6.5 us against
-        # 63.0 + 31.7 us for scoring and selection, then the whole rebuild.
-        # Between retrievals the compact prefill moves the rolling tail.
+        # positions only.  That pays where the retrieval runs as the single
+        # launch (16 rows x 40k tokens: 85.8 + 6.6 us against 62.6 + 31.6 us
+        # for scoring and selection, then the whole rebuild); in the chain it
+        # adds a launch (one 8k row: 21.1 + 6.4 against 15.7 + 8.3 us).  So by
+        # default (None) it is on exactly when the retrieval is the single
+        # launch: 8+ rows and a supplied LSE.  Between retrievals the compact
+        # prefill moves the rolling tail.
         self.sel_gen = torch.zeros((max_num_reqs,), dtype=torch.int32, device=self.device)
         self.gather_records = torch.zeros((max_num_reqs, settings.token_budget), dtype=torch.int64,
                                           device=self.device)
         self._workspace: torch.Tensor | None = None  # single-launch retrieval, on first use
         self._workspace_heads = 0
-        self.retrieval_stages = PREFIX_RETRIEVAL_STAGES if prefix_at_retrieval else RETRIEVAL_STAGES
+        self.prefix_at_retrieval = prefix_at_retrieval
 
         self.max_batch_rows = max_batch_rows or max_num_reqs
         self.max_chunks = (max_model_len + settings.chunk_size - 1) // settings.chunk_size
@@ -424,6 +431,13 @@ class DiffSpecDraftCache:
         self.proposed_parent_indices: torch.Tensor | None = None
         self.proposed_depths: torch.Tensor | None = None
         self.proposed_depths_cpu: list[int] = []
+
+    def retrieval_stages_for(self, batch_size: int, lse: torch.Tensor | None) -> int:
+        """The retrieval call's stages for a batch (see prefix_at_retrieval)."""
+        prefix = self.prefix_at_retrieval
+        if prefix is None:
+            prefix = batch_size >= SINGLE_LAUNCH_MIN_ROWS and lse is not None
+        return PREFIX_RETRIEVAL_STAGES if prefix else RETRIEVAL_STAGES
 
     @property
     def retrieval_interval(self) -> int:
@@ -588,7 +602,8 @@ class DiffSpecDraftCache:
         staged = self._rows_staging.upload([
             starts, [e - s for s, e in zip(starts, ends)], seq_lens[:batch_size], self._active_slots, [],
         ])
-        key = self._step_key(self.retrieval_stages, batch_size, batch_size, self._cos_sin_cache(),
+        key = self._step_key(self.retrieval_stages_for(batch_size, self._target_lse), batch_size, batch_size,
+                             self._cos_sin_cache(),
                              self._target_query, self._target_lse, self._target_key_cache, self._target_block_tables)
         return self._active_slots, staged, key
 
@@ -698,7 +713,7 @@ class DiffSpecDraftCache:
         if self.controller.adaptive:
             self._copy_selection_state(0)
         q, lse, kc, bt = self._target_query, self._target_lse, self._target_key_cache, self._target_block_tables
-        stages = self.retrieval_stages
+        stages = self.retrieval_stages_for(batch_size, lse)
         if key is None:
             key = self._step_key(stages, batch_size, batch_size, self._cos_sin_cache(), q, lse, kc, bt)
         hit = self._step_descs.get(key)

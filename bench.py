@@ -321,8 +321,10 @@ def run(args):
         roof_kernel, roof_bytes, roof_us = "chunk_score_kernel", score_bytes, score_us
     roof_gbps = roof_bytes / (roof_us * 1e-6) / 1e9
 
-    # Scoring without a supplied LSE: the same pass keeps (max, sum) pairs and
-    # a second small kernel merges them; such a step always runs the chain.
+    # Scoring without a supplied LSE: the same pass stores each chunk's mass
+    # per query head.  The full step runs as the single launch where the
+    # supplied-LSE step does (its selectors merge the masses into the LSEs);
+    # SCORE alone is the chain's pass plus lse_finalize_kernel.
     free_descs = []
     for inp, st in zip(copies, states):
         st["lse_partials"] = torch.zeros((total_rows, max_chunks, spec["hq"], 2), dtype=torch.float32, device=device)
@@ -335,7 +337,7 @@ def run(args):
             working_lens=st["working_lens"], raw_key=inp["raw_k"], raw_value=inp["raw_v"], working_key=st["work_k"],
             working_value=st["work_v"], cos_sin_cache=cos_sin, rotary_dim=d, is_neox_style=True, chunk_size=chunk,
             history_budget=hb, recent_window=spec.get("window", RECENT_WINDOW), row_active=row_active,
-            lse_partials=st["lse_partials"], lse_out=st["lse_out"],
+            lse_partials=st["lse_partials"], lse_out=st["lse_out"], workspace=st.get("workspace"),
         )
         free_descs.append(desc)
 
@@ -356,12 +358,19 @@ def run(args):
         return statistics.mean(a.elapsed_time(b) for a, b in ev) * 1e3  # µs
 
     free_score_us = time_free(step.SCORE, reps)
+    free_epochs = [step.workspace_epoch(st["workspace"]) for st in states] if single else []
     free_step_us = time_free(step.ALL, reps)
+    free_single = single and [step.workspace_epoch(st["workspace"]) for st in states] != free_epochs
+    if free_single and any(step.workspace_status(st["workspace"]) for st in states):
+        raise RuntimeError("a single launch without an LSE reported an expired wait: results not valid")
     free_gbps = score_bytes / (free_score_us * 1e-6) / 1e9
     lse_free_leg = {
-        "what": "scores without a supplied softmax LSE: chunk_score_kernel keeps (max, sum) pairs, "
-                "lse_finalize_kernel merges them into each head's LSE and writes the per-KV-head partials",
+        "what": "scores without a supplied softmax LSE: the scoring pass stores each chunk's mass per query "
+                "head; the single launch's selectors (or, for SCORE alone and the chain, lse_finalize_kernel) "
+                "merge them into each head's LSE and the chunk scores",
         "score_us": round(free_score_us, 2), "step_us": round(free_step_us, 2),
+        "step_path": "single launch (fused_step_kernel)" if free_single else "chain",
+        "step_us_with_lse": round(chain_ms * 1e3, 2),
         "score_us_with_lse": round(score_us, 2),
         "achieved_gbps": round(free_gbps, 1), "frac": round(free_gbps / HBM_PEAK_GBPS, 4),
         "algorithmic_bytes": score_bytes,

@@ -67,8 +67,10 @@ int ds_abi_version(void);
  * workspace: caller-owned device scratch of batch * max_chunks * Hkv floats
  *           (per-KV-head partial sums; unused with DS_HEAD_MAX), plus,
  *           when lse is NULL, batch * max_chunks * Hq * 2 floats of
- *           (max, sum) pairs and batch * Hq floats of row LSEs (placed
- *           first, so an 8-byte aligned workspace aligns the pairs).  Two
+ *           mass words (one 64-bit word per chunk and query head: the
+ *           chunk's log2 mass as fp32 in its low half) and batch * Hq
+ *           floats of row LSEs (placed first; the workspace must be 8-byte
+ *           aligned).  Two
  *           kernels (four without an LSE): the streaming pass, the head
  *           LSEs, the partials and a small finalize pass.
  * Limits  : head_dim % 32 == 0 and <= 256, Hq % Hkv == 0, Hq / Hkv <= 16,
@@ -166,7 +168,7 @@ int ds_rebuild_compact_kv(ds_stream_t stream, int dtype,
  * (graph-capturable).  With all three stages and a workspace, shapes the
  * fused kernel covers (bf16/fp16 KV, head_dim 64 or 128, <= 8 KV heads,
  * 8 to 256 batch rows, 16-token-aligned pages) run as one launch with the
- * same results.
+ * same results, with a supplied LSE or without one.
  */
 enum ds_stage { DS_STAGE_SCORE = 1, DS_STAGE_SELECT = 2, DS_STAGE_PLAN = 4, DS_STAGE_ALL = 7, DS_STAGE_PREFIX = 8 };
 
@@ -247,7 +249,11 @@ typedef struct ds_step_desc {
   size_t workspace_bytes;
   /* scoring without a supplied LSE (lse == NULL): the pass computes each
    * query head's LSE over the row's scored tokens (the reference's
-   * chunk_attention_scores with softmax_lse=None, diffspec/runtime.py:321-322) */
+   * chunk_attention_scores with softmax_lse=None, diffspec/runtime.py:321-322).
+   * lse_partials holds one 64-bit word per (row, chunk, query head), 8-byte
+   * aligned; the single launch tags its words with the workspace's launch
+   * tags, so one lse_partials buffer serves one workspace (or is zeroed when
+   * it moves to another) */
   float* lse_partials;               /* [batch_rows, max_chunks, Hq, 2] fp32 scratch; required when lse == NULL */
   float* lse_out;                    /* [batch_rows, Hq] natural-log LSE of each scored row; required when lse == NULL */
   int64_t lse_out_stride;            /* elements between rows of lse_out */

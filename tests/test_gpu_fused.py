@@ -2,7 +2,8 @@
 
 Scores, selections, plans, working lengths and working caches of the fused
 kernel are compared with the three-kernel chain on the same inputs (both
-are checked against the oracle in test_gpu_step.py).  The workspace is
+are checked against the oracle in test_gpu_step.py), with a supplied LSE
+and without one (then the LSEs written to lse_out too).  The workspace is
 reused across launches and across batch shapes: its epoch advances by one
 per launch and its status word stays 0.
 """
@@ -16,10 +17,11 @@ from test_gpu_step import build_case, check_step, run_gpu
 pytestmark = pytest.mark.gpu
 
 KEYS = ("scores", "sel_ids", "sel_count", "plan", "working_lens", "work_k", "work_v")
+LSE_FREE_KEYS = KEYS + ("lse_out",)
 
 
-def _same(a, b):
-    for key in KEYS:
+def _same(a, b, keys=KEYS):
+    for key in keys:
         x, y = a[key], b[key]
         if x.dtype.is_floating_point:
             assert torch.equal(x.isnan(), y.isnan()), key
@@ -142,3 +144,71 @@ def test_expired_wait_stays_with_its_launch(cuda):
     run_gpu(case, cuda, state=state, path="fused")
     _same(chain, state)
     assert step.workspace_epoch(state["workspace"]) == 3
+
+
+@pytest.mark.parametrize("seed,rows,lo,hi,kw", [
+    (21, 12, 100, 30000, {}),
+    (22, 9, 700, 9000, dict(hq=12, hkv=2, head_dim=64)),
+    (23, 8, 20000, 40000, dict(chunk=32, token_budget=1024)),
+    (24, 10, 500, 12000, dict(hq=64, hkv=8, head_dim=64, block_size=64)),
+    (25, 9, 1000, 8000, dict(hq=16, hkv=1, head_dim=64, dtype=torch.float16)),
+])
+def test_lse_free_single_launch_equals_chain(cuda, seed, rows, lo, hi, kw):
+    """Without a supplied LSE the single launch's selectors merge each row's mass
+    words into its heads' LSEs with the chain's merge: scores, selections, plans,
+    working caches and lse_out equal the chain's bit for bit, and match the
+    oracle with the exact LSE.  Shapes: the headline's (ragged, 8 query heads per
+    KV head); groups of 6 (three phases of two heads); 1250-chunk rows in
+    32-token chunks (several load rounds per group and several chunk blocks);
+    64 query heads (two rounds of words per chunk); one KV head of 16 in fp16."""
+    from oracle import diffspec_oracle as O
+
+    case = _ragged(seed, rows, lo, hi, **kw)
+    chain = run_gpu(case, cuda, path="chain", lse_free=True)
+    fused = run_gpu(case, cuda, path="fused", lse_free=True)
+    _same(chain, fused, LSE_FREE_KEYS)
+    check_step(case, fused)
+    rows_idx, q_index, _ = O.retrieval_rows(case["counts"], case["ends"], case["tlens"], case["real_rows"])
+    torch.testing.assert_close(fused["lse_out"].cpu()[rows_idx], case["lse"][q_index], rtol=1e-5, atol=1e-4)
+
+
+def test_lse_free_single_launch_takes_only_its_own_words(cuda):
+    """The mass words carry their launch's tag.  One lse_partials buffer holds the
+    chain's untagged words, then the words of a single launch on other queries;
+    the next single launch (new queries again) waits for its own words: its
+    results equal the chain's on its inputs, bit for bit."""
+    from ds355 import step
+
+    case = _ragged(26, 10, 2000, 16000)
+    state = run_gpu(case, cuda, path="chain", lse_free=True)
+    g = gen(27)
+    for launch in range(3):
+        query = torch.randn(tuple(case["query"].shape), generator=g).to(case["query"].dtype)
+        other = dict(case, query=query)
+        ref = run_gpu(other, cuda, path="chain", lse_free=True)
+        state["query"] = query.to(cuda)
+        for key in ("work_k", "work_v", "lse_out"):
+            state[key].fill_(float("nan"))
+        state["sel_count"].fill_(-1)
+        state["scores"].zero_()
+        run_gpu(other, cuda, state=state, path="fused", lse_free=True)
+        _same(ref, state, LSE_FREE_KEYS)
+    assert step.workspace_epoch(state["workspace"]) == 3
+
+
+def test_lse_free_expired_wait_is_reported(cuda):
+    """Without a supplied LSE a launch whose selectors report an expired wait
+    (forced from the host) leaves the bit in the owner's word; the next launch
+    equals the chain."""
+    from ds355 import step
+
+    case = _ragged(28, 9, 1000, 12000)
+    chain = run_gpu(case, cuda, path="chain", lse_free=True)
+    state = run_gpu(case, cuda, path="fused", lse_free=True, flags=step.EXPIRE_WAITS, expect_status=None)
+    assert step.workspace_status(state["workspace"]) & 1
+    step.clear_workspace_status(state["workspace"])
+    for key in ("work_k", "work_v", "lse_out"):
+        state[key].fill_(float("nan"))
+    state["sel_count"].fill_(-1)
+    run_gpu(case, cuda, state=state, path="fused", lse_free=True)
+    _same(chain, state, LSE_FREE_KEYS)

@@ -104,10 +104,10 @@ def test_draft_steps_replayed_from_a_graph(cuda):
     assert attention.attention_epoch(graphed["ws"]) == 3
 
 
-@pytest.mark.parametrize("path", ["chain", "fused", "lse-free"])
+@pytest.mark.parametrize("path", ["chain", "fused", "lse-free", "lse-free fused"])
 def test_retrieval_step_replayed_from_a_graph(cuda, path):
     """One retrieval step captured once, replayed with new queries and committed counts
-    (the chain, the single launch, and the chain scoring without a supplied LSE)."""
+    (the chain and the single launch, each with and without a supplied LSE)."""
     from ds355 import step
 
     g = gen(43)
@@ -137,9 +137,10 @@ def test_retrieval_step_replayed_from_a_graph(cuda, path):
             work_k=torch.full((12, 4, 2048, 128), float("nan"), dtype=torch.bfloat16, device=cuda),
         )
         st["work_v"] = torch.full_like(st["work_k"], float("nan"))
-        if path == "fused":
+        lse_free = path.startswith("lse-free")
+        if path.endswith("fused"):
             st["workspace"] = step.new_workspace(rows, max_chunks, 4, 2048, cuda)
-        if path == "lse-free":
+        if lse_free:
             st["lse_partials"] = torch.zeros((rows, max_chunks, 32, 2), dtype=torch.float32, device=cuda)
             st["lse_out"] = torch.full((rows, 32), float("nan"), dtype=torch.float32, device=cuda)
         return st
@@ -150,7 +151,7 @@ def test_retrieval_step_replayed_from_a_graph(cuda, path):
 
     def desc_for(st):
         desc, _ = step.build_step_desc(
-            snapshot=step.VerifierSnapshot(query, None if path == "lse-free" else lse, key_cache, table,
+            snapshot=step.VerifierSnapshot(query, None if path.startswith("lse-free") else lse, key_cache, table,
                                            case["scale"]), rows=rows_t,
             scores=st["scores"], score_partials=st["partials"], sel_ids=st["sel_ids"], sel_count=st["sel_count"],
             slots=slots_t, committed_lens=committed_t, plan=st["plan"], working_lens=st["working_lens"],
@@ -172,7 +173,7 @@ def test_retrieval_step_replayed_from_a_graph(cuda, path):
     assert torch.isnan(graphed["work_k"]).all()  # capture records, it does not run
 
     outputs = ("scores", "sel_ids", "sel_count", "plan", "working_lens", "work_k", "work_v")
-    if path == "lse-free":
+    if path.startswith("lse-free"):
         outputs += ("lse_out",)
     for replay in range(3):
         if replay:
@@ -187,7 +188,7 @@ def test_retrieval_step_replayed_from_a_graph(cuda, path):
         torch.cuda.synchronize()
         for name in outputs:
             _same(graphed[name], eager[name], f"replay {replay}: {name}")
-        if path == "fused":
+        if path.endswith("fused"):
             assert step.workspace_status(graphed["workspace"]) == 0
             assert step.workspace_epoch(graphed["workspace"]) == replay + 1
         if replay == 0:  # the captured inputs: the oracle's step

@@ -109,8 +109,8 @@ def run_gpu(case, device, *, stages=None, state=None, row_active=None, path="cha
     torch.cuda.synchronize()
     if fused:  # the single launch ran (epoch + 1) or, for other shapes, the chain did
         if single_launch is None:
-            # Batches of fewer rows, and steps without a supplied LSE, run the chain.
-            single_launch = rows >= 8 and not lse_free
+            # Batches of fewer rows run the chain.
+            single_launch = rows >= 8
         assert step.workspace_epoch(state["workspace"]) == epoch + (1 if single_launch else 0)
         if expect_status is not None:
             assert step.workspace_status(state["workspace"]) == expect_status

@@ -473,13 +473,11 @@ def test_gather_records_follow_the_slot_map(launches):
     assert launches[-1]["stages"] == step.PLAN
     assert gen.tolist() == cache.sel_gen.tolist() and records.shape == cache.gather_records.shape
     assert runtime.RETRIEVAL_STAGES == step.SCORE | step.SELECT
-    lse = torch.zeros(1)
     # By default the final history rows move at retrieval exactly when it runs as the single launch.
-    assert cache.retrieval_stages_for(8, lse) == step.SCORE | step.SELECT | step.PREFIX
-    assert cache.retrieval_stages_for(7, lse) == step.SCORE | step.SELECT
-    assert cache.retrieval_stages_for(16, None) == step.SCORE | step.SELECT
-    assert _cache(prefix_at_retrieval=False).retrieval_stages_for(16, lse) == step.SCORE | step.SELECT
-    assert _cache(prefix_at_retrieval=True).retrieval_stages_for(1, None) == step.SCORE | step.SELECT | step.PREFIX
+    assert cache.retrieval_stages_for(8) == step.SCORE | step.SELECT | step.PREFIX
+    assert cache.retrieval_stages_for(7) == step.SCORE | step.SELECT
+    assert _cache(prefix_at_retrieval=False).retrieval_stages_for(16) == step.SCORE | step.SELECT
+    assert _cache(prefix_at_retrieval=True).retrieval_stages_for(1) == step.SCORE | step.SELECT | step.PREFIX
 
 
 def _speculative_config(**overrides):

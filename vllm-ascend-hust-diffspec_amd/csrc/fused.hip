@@ -10,7 +10,8 @@
 //     gather tasks, (row, ppw local positions) numbered row-major and dealt
 //     round-robin, each once its row's plan is published;
 //   - the last S workgroups select: selector s takes rows s, s + S, ... in
-//     order and publishes each row's plan.
+//     order and publishes each row's plan (without a supplied LSE, below
+//     them the group workgroups; see below).
 //
 // Hand-over is by value through device-scope (coherent) accesses, with no
 // cache write-back on either side:
@@ -19,6 +20,16 @@
 //     selector first polls one sentinel, the partial of the row's newest
 //     chunk and last KV head (written in the row's last round of units),
 //     then reads the row's partials until all carry the tag;
+//   - without a supplied LSE (the LSEFREE kernel) the scoring waves store a
+//     mass word per (chunk, query head) instead, tagged the same way, in the
+//     caller's lse_partials.  Group workgroups, one per (row slot, KV
+//     group), sit below the row selectors: each polls its group's sentinel
+//     word (newest chunk, last head of the group), merges the group's words
+//     into its heads' LSEs and stores each chunk's share of the group as the
+//     tagged partial above (lse_finalize_kernel's steps: the same bits); the
+//     row's selector then selects as with a supplied LSE.  The words carry
+//     the tags of this workspace's launches, so one lse_partials buffer
+//     serves one workspace;
 //   - a selector stores the plan row twice: as the output (plain stores) and
 //     as a tagged copy, column j as (tag << 32) | value (plan values are
 //     below 2^31).  Gathering waves poll the tagged copy itself with one
@@ -60,6 +71,7 @@
 //   uint64 plans[rows][kPlanCols]   tagged plan copies
 //   uint32 state[rows][task_cap]    gather tasks skipped by their scoring wave
 //   uint64 partials[rows, max_chunks, Hkv]
+// (and, without a supplied LSE, the tagged mass words in lse_partials).
 #include "gather_body.h"
 #include "score_body.h"
 #include "select_body.h"
@@ -72,7 +84,7 @@ int make_score_args(score::ScoreArgs& a, int64_t& upper_units, int& page_mode, i
                     const int32_t* block_table, int64_t bt_stride, const RowSource& src, int batch, int num_q_heads,
                     int num_kv_heads, int head_dim, int block_size, int chunk_size, int max_chunks, float scale,
                     int head_reduce, float* partial, float* out, int64_t out_stride, int write_tail,
-                    size_t partial_bytes, float* mz);
+                    size_t partial_bytes, uint64_t* mw);
 int make_select_args(select::SelectArgs& a, float* scores, int64_t score_stride, const float* partials,
                      int max_chunks, int hkv, int hq, const RowSource& src, int batch, int chunk, int budget,
                      int do_select, int do_plan, int32_t* ids, int64_t ids_stride, int32_t* counts,
@@ -89,6 +101,13 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kSelectors = 16;     // selecting workgroups (fewer when the batch has fewer rows)
+// Without a supplied LSE: workgroups doing the KV groups' shares, below the
+// row selectors.  Measured on 16 rows of 4k-40k tokens (one step): 32 group
+// workgroups 96.6-98.3 us; 16 of them 101.9 us; 32 with the last group's
+// workgroup also selecting (no row selectors) 107.7 us; one per row and
+// group (64), the last selecting, 103.5 us.  Workgroups that do not score
+// lengthen the scoring stream's tail.
+constexpr int kGroupSelectors = 32;
 constexpr int kFusedKeys = 8192;   // candidate keys a selector keeps in LDS
 constexpr int kFusedRows = 256;    // batch rows per fused launch
 static_assert(kFusedRows <= kThreads, "the prologue loads one row per thread");
@@ -120,7 +139,8 @@ struct FusedArgs {
   uint64_t* plans;  // [rows, kPlanCols] tagged plan copies
   uint32_t* state;  // [rows, task_cap]
   int task_cap;
-  int selectors;
+  int selectors;        // workgroups that do not score: group workgroups, then row selectors
+  int group_selectors;  // of them, LSEFREE: one per (row slot, KV group), below the row selectors
   uint32_t owner_spins;  // polls a scorer waits for a plan (0: every task goes to the selectors)
   int expire;            // test flag: every selector raises kStatusPartials as if a wait had expired
   uint32_t* status_out;  // optional caller word that also receives the launch's status bits
@@ -128,6 +148,12 @@ struct FusedArgs {
   uint64_t* rec;         // [num_slots, rec_stride] gather records (gather_body.h), or nullptr
   int64_t rec_stride;
   int prefix_only;       // gather only the tasks wholly in each row's history prefix
+  // Without a supplied LSE (the LSEFREE kernel): a selector per (row, KV
+  // group) merges the group's mass words (s.mw, tagged) into its heads'
+  // LSEs, written to lse_out, and stores the group's tagged partials.
+  float* lse_out;
+  int64_t lse_out_stride;
+  int lse_wide;  // two heads per thread and 16-byte reads (words 16-byte aligned)
 };
 // With gather records, the tagged plan copy carries the slot's selection
 // generation in its last column (plan_width < kPlanCols then).
@@ -196,6 +222,168 @@ __device__ __forceinline__ void poll_chunk_sums(const uint64_t* part, int base, 
   for (int e = 0; e < kPollLoads; ++e) {
     const int u = e / per_chunk;
     sum[u] += __uint_as_float(static_cast<uint32_t>(v[e]));
+  }
+}
+
+// Coherent reads of mass words through a buffer resource over the row's
+// words: the cache policy (sc1) of the device-scope relaxed atomic loads,
+// 16 bytes (two adjacent heads) or 8.  Each 8-byte word was stored whole, so
+// each half of a 16-byte read is one word as it was written.  Reads past the
+// resource's range return zeros (no tag), so they need no bounds test.
+constexpr int kCoherentPolicy = 16;
+template <int HP>
+struct MassRead {  // HP words, lo / hi halves
+  uint32_t w[2 * HP];
+};
+template <int HP>
+__device__ __forceinline__ MassRead<HP> coherent_words(score::SRsrc r, int word) {
+  MassRead<HP> m;
+  if constexpr (HP == 2) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, word * static_cast<int>(sizeof(uint64_t)), 0,
+                                                         kCoherentPolicy);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m.w[i] = v[i];
+  } else {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, word * static_cast<int>(sizeof(uint64_t)), 0,
+                                                        kCoherentPolicy);
+    m.w[0] = v[0];
+    m.w[1] = v[1];
+  }
+  return m;
+}
+template <int HP>
+__device__ __forceinline__ uint64_t word_of(const MassRead<HP>& m, int i) {
+  return (static_cast<uint64_t>(m.w[2 * i + 1]) << 32) | m.w[2 * i];
+}
+
+// Without a supplied LSE: KV group g of row b, what lse_finalize_kernel does
+// for it (the same merge and sums, so the same bits), from the row's mass
+// words once each carries `tag`: the group's LSEs, written to lse_out, then
+// each chunk's share of the group, stored as the row's tagged partial for
+// its selector.  Every round issues all of its reads before it waits for
+// any (reads under a per-word branch each waited for the one before).
+template <int HP>
+__device__ __forceinline__ void group_lse_pass(const FusedArgs& f, score::SRsrc r, const score::LseLayout& l,
+                                               int C, int h0, uint32_t tag, score::LseAcc& acc) {
+  using namespace score;
+  const int hq = f.s.Hq;
+  const int past = C * hq;  // a word index past the resource: its read returns zeros without a memory access
+  for (int c0 = l.j; c0 < C; c0 += kLseLoads * l.tpp) {
+    float mass[kLseLoads][HP];  // the masses of the words that carried the tag
+    uint32_t missing = 0u;      // words of this round without the tag yet
+#pragma unroll
+    for (int u = 0; u < kLseLoads; ++u) {
+#pragma unroll
+      for (int i = 0; i < HP; ++i) mass[u][i] = -INFINITY;
+      if (c0 + u * l.tpp < C) missing |= 1u << u;
+    }
+    for (uint32_t spin = 0;; ++spin) {
+      // A retry reads only the words still missing (the others read past
+      // the resource): polling groups that reread whole rounds slowed the
+      // scoring stream that shares the memory channels.
+      MassRead<HP> n[kLseLoads];
+#pragma unroll
+      for (int u = 0; u < kLseLoads; ++u) {
+        n[u] = coherent_words<HP>(r, (missing >> u) & 1u ? (c0 + u * l.tpp) * hq + h0 : past);
+      }
+#pragma unroll
+      for (int u = 0; u < kLseLoads; ++u) {
+        bool tagged = (missing >> u) & 1u;
+#pragma unroll
+        for (int i = 0; i < HP; ++i) tagged = tagged && n[u].w[2 * i + 1] == tag;
+#pragma unroll
+        for (int i = 0; i < HP; ++i) mass[u][i] = tagged ? __uint_as_float(n[u].w[2 * i]) : mass[u][i];
+        if (tagged) missing &= ~(1u << u);
+      }
+      if (missing == 0u) break;
+      if (spin >= kSpinLimit ||
+          (spin % kStatusEvery == kStatusEvery - 1 && coherent_load(f.header + kLaunchStatus) != 0u)) {
+        raise_status(f.header, kStatusPartials);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(kSleep);
+    }
+#pragma unroll
+    for (int u = 0; u < kLseLoads; ++u) {
+      add_term(acc.m0, acc.z0, mass[u][0]);
+      if constexpr (HP == 2) add_term(acc.m1, acc.z1, mass[u][HP - 1]);
+    }
+  }
+}
+
+// Each chunk's share of group g: GM >= G heads per chunk, 16 reads in
+// flight per thread (2 * kLseLoads / GM chunks per thread and round).
+template <int HP, int GM>
+__device__ __forceinline__ void group_shares(const FusedArgs& f, score::SRsrc r, int b, int g, int C, uint32_t tag,
+                                             const float* s_lse2) {
+  using namespace score;
+  constexpr int kChunks = 2 * kLseLoads / GM;
+  constexpr int kReads = GM / HP;
+  const int G = f.s.G, hq = f.s.Hq, hkv = f.s.Hkv, tid = threadIdx.x;
+  uint64_t* part = f.s.tagged + static_cast<int64_t>(b) * f.s.max_chunks * hkv + g;
+  for (int c0 = tid; c0 < C; c0 += kChunks * kThreads) {
+    MassRead<HP> v[kChunks][kReads];
+#pragma unroll
+    for (int k = 0; k < kChunks; ++k) {
+#pragma unroll
+      for (int e = 0; e < kReads; ++e) v[k][e] = coherent_words<HP>(r, (c0 + k * kThreads) * hq + g * G + e * HP);
+    }
+#pragma unroll
+    for (int k = 0; k < kChunks; ++k) {
+      const int c = c0 + k * kThreads;
+      float sum = 0.f;
+#pragma unroll
+      for (int h = 0; h < GM; ++h) {
+        sum = h < G ? add_share(sum, __uint_as_float(v[k][h / HP].w[2 * (h % HP)]), s_lse2[h]) : sum;
+      }
+      if (c < C) {
+        coherent_store(part + static_cast<int64_t>(c) * hkv, (static_cast<uint64_t>(tag) << 32) | __float_as_uint(sum));
+      }
+    }
+  }
+}
+
+template <int HP>
+__device__ __forceinline__ void group_task_hp(const FusedArgs& f, score::SRsrc r, const score::LseLayout& l, int b,
+                                              int g, int C, uint32_t tag, float (*s_m)[kThreads],
+                                              float (*s_z)[kThreads], float* s_lse2) {
+  using namespace score;
+  const int G = f.s.G, tid = threadIdx.x;
+  LseAcc acc;
+  if (l.ph < l.P) group_lse_pass<HP>(f, r, l, C, g * G + HP * l.ph, tag, acc);
+  const float lse = lse_finish(l, acc, G, s_m, s_z);
+  if (tid < G) {
+    f.lse_out[static_cast<int64_t>(b) * f.lse_out_stride + g * G + tid] = lse;
+    s_lse2[tid] = lse_base2(lse);
+  }
+  __syncthreads();
+  // Every word of the group was read with its tag above.
+  if (G <= 8) {
+    group_shares<HP, 8>(f, r, b, g, C, tag, s_lse2);
+  } else {
+    group_shares<HP, kMaxGroup>(f, r, b, g, C, tag, s_lse2);
+  }
+}
+
+// s_m / s_z: LDS lent for the merge; s_lse2: G floats.
+__device__ __forceinline__ void lse_group_task(const FusedArgs& f, int b, int g, uint32_t tag,
+                                               float (*s_m)[kThreads], float (*s_z)[kThreads], float* s_lse2) {
+  using namespace score;
+  const ScoreArgs& sa = f.s;
+  const RowDesc d = row_desc(sa.src, b);
+  const int C = d.active ? (d.len + sa.chunk - 1) / sa.chunk : 0;
+  if (C == 0) return;  // workgroup-uniform: a row with nothing scored
+  const int G = sa.G, hq = sa.Hq;
+  const uint64_t* words = sa.mw + static_cast<int64_t>(b) * sa.max_chunks * hq;
+  const SRsrc r = srsrc(words, C * hq * static_cast<int>(sizeof(uint64_t)));
+  // The group's word of the newest chunk and last head: written in the row's
+  // last round of units.
+  wait_sentinel(words + static_cast<int64_t>(C - 1) * hq + g * G + G - 1, tag, f.header);
+  const LseLayout l = lse_layout(G, f.lse_wide, threadIdx.x);
+  if (l.hp == 2) {
+    group_task_hp<2>(f, r, l, b, g, C, tag, s_m, s_z, s_lse2);
+  } else {
+    group_task_hp<1>(f, r, l, b, g, C, tag, s_m, s_z, s_lse2);
   }
 }
 
@@ -458,7 +646,7 @@ struct WorkShared {
   int scratch[4];
 };
 
-template <int DT, int STEPS, bool NEOX, int PAGE>
+template <int DT, int STEPS, bool NEOX, int PAGE, bool LSEFREE>
 __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
   constexpr int KB = STEPS <= 2 ? 4 : 2;  // the chunk-score batch shape for head_dim <= 128
   __shared__ union {
@@ -470,6 +658,7 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
   __shared__ int s_scratch[4];
   __shared__ uint32_t s_tag;
   __shared__ uint32_t s_last;
+  __shared__ float s_lse2[LSEFREE ? score::kMaxGroup : 1];  // a group's exponent bases (no LSE supplied)
 
   const int rows = f.p.batch;
   const gather::GatherArgs& ga = f.g;
@@ -501,7 +690,24 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
 
   if (selector) {
     const int s = static_cast<int>(blockIdx.x) - first_selector;
-    for (int b = s; b < rows; b += f.selectors) select_row(f, b, tag, lds.sel);
+    if constexpr (LSEFREE) {
+      // The first group_selectors workgroups do the KV groups' shares, one
+      // per (row slot, group); the row selectors above them (higher indices:
+      // every wait is on lower-indexed workgroups) select as with an LSE.
+      const int hkv = f.s.Hkv;
+      const int gs = f.group_selectors;
+      if (s < gs) {
+        float(*s_m)[kThreads] = reinterpret_cast<float(*)[kThreads]>(&lds.sel.keys[0]);
+        for (int b = s / hkv; b < rows; b += gs / hkv) {
+          lds_barrier();  // the merge borrows the key area between rows
+          lse_group_task(f, b, s % hkv, tag, s_m, s_m + 2, s_lse2);
+        }
+      } else {
+        for (int b = s - gs; b < rows; b += f.selectors - gs) select_row(f, b, tag, lds.sel);
+      }
+    } else {
+      for (int b = s; b < rows; b += f.selectors) select_row(f, b, tag, lds.sel);
+    }
   } else {
     WorkShared& w = lds.w;
     const score::ScoreArgs& sa = f.s;
@@ -514,8 +720,8 @@ __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
     const int gw = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x) * kWaves +
                                                   static_cast<int>(threadIdx.x >> 6));
     const int tw = first_selector * kWaves;
-    score::score_stream<DT, STEPS, KB, false, PAGE, true>(sa, w.unit_prefix, w.len, w.qrow, w.unit_prefix[rows], gw,
-                                                          tw, tag);
+    score::score_stream<DT, STEPS, KB, false, PAGE, true, LSEFREE>(sa, w.unit_prefix, w.len, w.qrow,
+                                                                   w.unit_prefix[rows], gw, tw, tag);
     gather_owned<DT, NEOX>(f, s_task_prefix, s_slot, gw, tw, tag);
   }
 
@@ -585,24 +791,37 @@ int launch_fused(hipStream_t stream, const FusedArgs& f, int64_t upper_units, in
   return rc;
 }
 
-template <int DT, int PAGE>
+template <int DT, int PAGE, bool LSEFREE>
 int launch_page(hipStream_t stream, const FusedArgs& f, int steps, bool neox, int64_t upper_units,
                 int64_t upper_tasks, bool& launched) {
   if (steps == 4) {
-    if (neox) return launch_fused<fused_step_kernel<DT, 4, true, PAGE>>(stream, f, upper_units, upper_tasks, launched);
-    return launch_fused<fused_step_kernel<DT, 4, false, PAGE>>(stream, f, upper_units, upper_tasks, launched);
+    if (neox) {
+      return launch_fused<fused_step_kernel<DT, 4, true, PAGE, LSEFREE>>(stream, f, upper_units, upper_tasks,
+                                                                         launched);
+    }
+    return launch_fused<fused_step_kernel<DT, 4, false, PAGE, LSEFREE>>(stream, f, upper_units, upper_tasks,
+                                                                        launched);
   }
-  if (neox) return launch_fused<fused_step_kernel<DT, 2, true, PAGE>>(stream, f, upper_units, upper_tasks, launched);
-  return launch_fused<fused_step_kernel<DT, 2, false, PAGE>>(stream, f, upper_units, upper_tasks, launched);
+  if (neox) {
+    return launch_fused<fused_step_kernel<DT, 2, true, PAGE, LSEFREE>>(stream, f, upper_units, upper_tasks, launched);
+  }
+  return launch_fused<fused_step_kernel<DT, 2, false, PAGE, LSEFREE>>(stream, f, upper_units, upper_tasks, launched);
+}
+
+template <int DT, bool LSEFREE>
+int launch_lse(hipStream_t stream, const FusedArgs& f, int steps, bool neox, int page_mode, int64_t upper_units,
+               int64_t upper_tasks, bool& launched) {
+  if (page_mode == score::PAGE_POW2) {
+    return launch_page<DT, score::PAGE_POW2, LSEFREE>(stream, f, steps, neox, upper_units, upper_tasks, launched);
+  }
+  return launch_page<DT, score::PAGE_UNIFORM, LSEFREE>(stream, f, steps, neox, upper_units, upper_tasks, launched);
 }
 
 template <int DT>
-int launch_dt(hipStream_t stream, const FusedArgs& f, int steps, bool neox, int page_mode, int64_t upper_units,
-              int64_t upper_tasks, bool& launched) {
-  if (page_mode == score::PAGE_POW2) {
-    return launch_page<DT, score::PAGE_POW2>(stream, f, steps, neox, upper_units, upper_tasks, launched);
-  }
-  return launch_page<DT, score::PAGE_UNIFORM>(stream, f, steps, neox, upper_units, upper_tasks, launched);
+int launch_dt(hipStream_t stream, const FusedArgs& f, int steps, bool neox, int page_mode, bool lse_free,
+              int64_t upper_units, int64_t upper_tasks, bool& launched) {
+  if (lse_free) return launch_lse<DT, true>(stream, f, steps, neox, page_mode, upper_units, upper_tasks, launched);
+  return launch_lse<DT, false>(stream, f, steps, neox, page_mode, upper_units, upper_tasks, launched);
 }
 
 }  // namespace
@@ -618,9 +837,20 @@ size_t fused_workspace_bytes(int rows, int max_chunks, int num_kv_heads, int tok
 int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource& src, uint32_t* status_out,
                       bool& launched) {
   launched = false;
-  // Without a supplied LSE a row's scores need all of its chunks first: the chain runs.
   const bool prefix = d->stages == (DS_STAGE_SCORE | DS_STAGE_SELECT | DS_STAGE_PREFIX);
-  if (d->workspace == nullptr || (d->stages != DS_STAGE_ALL && !prefix) || d->lse == nullptr) return clear_error();
+  if (d->workspace == nullptr || (d->stages != DS_STAGE_ALL && !prefix)) return clear_error();
+  // Without a supplied LSE the selectors merge each row's mass words, which
+  // live in the caller's lse_partials ([batch_rows, max_chunks, Hq] 64-bit
+  // words); a row's words are read through 32-bit byte offsets, which the
+  // reads of a round may overrun by kLseLoads * kThreads chunks (they return
+  // zeros).
+  const bool lse_free = d->lse == nullptr;
+  if (lse_free && (d->lse_partials == nullptr || d->lse_out == nullptr || d->lse_out_stride < d->num_q_heads ||
+                   (static_cast<int64_t>(d->max_chunks) + score::kLseLoads * kThreads) * d->num_q_heads *
+                           static_cast<int64_t>(sizeof(uint64_t)) >
+                       INT32_MAX)) {
+    return clear_error();
+  }
   const size_t need = fused_workspace_bytes(d->batch_rows, d->max_chunks, d->num_kv_heads, d->token_budget);
   DS_REQUIRE(need > 0 && d->workspace_bytes >= need,
              "step workspace too small: need %zu bytes for %d rows, %d chunks, %d KV heads, token budget %d", need,
@@ -634,7 +864,8 @@ int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource
                            d->k_block_stride, d->k_token_stride, d->k_head_stride, d->lse, d->lse_token_stride,
                            d->lse_head_stride, d->block_table, d->bt_stride, src, d->batch_rows, d->num_q_heads,
                            d->num_kv_heads, d->head_dim, d->block_size, d->chunk_size, d->max_chunks, d->scale,
-                           DS_HEAD_MEAN, d->score_partials, nullptr, 0, 0, SIZE_MAX, nullptr);
+                           DS_HEAD_MEAN, d->score_partials, nullptr, 0, 0, SIZE_MAX,
+                           lse_free ? reinterpret_cast<uint64_t*>(d->lse_partials) : nullptr);
   if (rc != DS_OK) return rc;
   rc = make_select_args(f.p, d->scores, d->max_chunks, d->score_partials, d->max_chunks, d->num_kv_heads,
                         d->num_q_heads, src, d->batch_rows, d->chunk_size, d->history_budget, 1, 1, d->sel_ids,
@@ -679,12 +910,25 @@ int launch_fused_step(hipStream_t stream, const ds_step_desc* d, const RowSource
     f.rec_stride = d->rec_stride;
   }
   f.prefix_only = prefix ? 1 : 0;
+  if (lse_free) {
+    // kGroupSelectors / Hkv row slots of Hkv group workgroups, taking rows
+    // s, s + slots, ... (rows finish roughly in order), below the row
+    // selectors.
+    f.group_selectors =
+        std::min(d->batch_rows, std::max(1, kGroupSelectors / d->num_kv_heads)) * d->num_kv_heads;
+    f.selectors += f.group_selectors;
+    f.lse_out = d->lse_out;
+    f.lse_out_stride = d->lse_out_stride;
+    f.lse_wide = score::lse_words_wide(d->lse_partials);
+  }
   if (prefix) f.p.working_lens = nullptr;  // the compact prefill sets them
   const int ppw = 64 / f.g.lanes_per_row;
   const int64_t upper_tasks = static_cast<int64_t>(d->batch_rows) * ((f.g.pos_limit + ppw - 1) / ppw);
   const bool neox = d->is_neox_style != 0;
-  if (d->dtype == DS_BF16) return launch_dt<DS_BF16>(stream, f, steps, neox, page_mode, upper_units, upper_tasks, launched);
-  return launch_dt<DS_FP16>(stream, f, steps, neox, page_mode, upper_units, upper_tasks, launched);
+  if (d->dtype == DS_BF16) {
+    return launch_dt<DS_BF16>(stream, f, steps, neox, page_mode, lse_free, upper_units, upper_tasks, launched);
+  }
+  return launch_dt<DS_FP16>(stream, f, steps, neox, page_mode, lse_free, upper_units, upper_tasks, launched);
 }
 
 }  // namespace ds355

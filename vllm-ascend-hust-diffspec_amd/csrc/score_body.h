@@ -44,10 +44,21 @@ struct ScoreArgs {
   float* out;      // [batch, out_stride] final scores (head max; tail zeros)
   int64_t out_stride;
   int write_tail;
-  // Without a supplied LSE: per (row, chunk, query head) the chunk's largest
-  // scaled logit m (log2 units) and sum z = sum_t 2^(logit_t - m), as float
-  // pairs [batch, max_chunks, Hq, 2] (a chunk's heads are contiguous).
-  float* mz;
+  // Without a supplied LSE: per (row, chunk, query head) one 64-bit word
+  // [batch, max_chunks, Hq] (a chunk's heads are contiguous).  Its low half
+  // is the chunk's mass in log2 units, M = log2(sum_t 2^(scaled logit_t)),
+  // as fp32; its high half is 0 (kernel chain) or the launch's tag (single
+  // launch, stored coherently: a reader polling the word needs no other
+  // signal).  Chain words never carry a tag, since tags are never 0.
+  uint64_t* mw;
+};
+
+// The mass M of a word (see ScoreArgs::mw) and the tag it carries.
+__device__ __forceinline__ float mass_of(uint64_t w) { return __uint_as_float(static_cast<uint32_t>(w)); }
+__device__ __forceinline__ uint32_t tag_of(uint64_t w) { return static_cast<uint32_t>(w >> 32); }
+constexpr uint64_t kNoMassWord = 0xff800000u;  // M = -inf, no tag
+struct alignas(16) WordPair {  // two adjacent heads' words, one 16-byte access
+  uint64_t a, b;
 };
 
 // (m, z) pairs with m in log2 units: the merged pair of two parts of one sum.
@@ -159,16 +170,16 @@ struct Batch {
 };
 
 // LSEFREE: merge a chunk's running pairs (one per token group slot of a
-// batch, then the 16 token lanes), store each real head's pair at
-// mz[row, chunk, head] and reset for the next chunk.  A unit's G pairs are
+// batch, then the 16 token lanes), store each real head's mass word at
+// mw[row, chunk, head] and reset for the next chunk.  A unit's G words are
 // one contiguous run, and the waves of a workgroup walk consecutive units
-// (the KV heads of one span, with 4 KV heads), so a chunk's Hq pairs are
+// (the KV heads of one span, with 4 KV heads), so a chunk's Hq words are
 // written whole by one CU.  Scattered 8-byte pieces of lines shared with
 // other XCDs (the [row, head, chunk] order) cost 4 us of a 61 us pass on
 // 16 x 40k-token rows.
-template <int KB>
-__device__ __forceinline__ void flush_pairs(const ScoreArgs& a, const BatchCtx& c, int cc, float (&m)[KB][4],
-                                            float (&z)[KB][4], int kgrp, int col) {
+template <int KB, bool TAGGED>
+__device__ __forceinline__ void flush_mass(const ScoreArgs& a, const BatchCtx& c, int cc, float (&m)[KB][4],
+                                           float (&z)[KB][4], int kgrp, int col, uint32_t tag) {
   const int ch = c.c0 + cc;
   const int chunks_row = (c.len + a.chunk - 1) / a.chunk;
 #pragma unroll
@@ -179,8 +190,14 @@ __device__ __forceinline__ void flush_pairs(const ScoreArgs& a, const BatchCtx& 
     merge_mz_row16(mt, zt);
     const int h = 4 * kgrp + e;
     if (col == 0 && h < a.G && ch < chunks_row) {
-      const int64_t at = ((static_cast<int64_t>(c.b) * a.max_chunks + ch) * a.Hq + c.g * a.G + h) * 2;
-      *reinterpret_cast<float2*>(a.mz + at) = make_float2(mt, zt);
+      const float mass = zt > 0.f ? mt + __log2f(zt) : -INFINITY;
+      const int64_t at = (static_cast<int64_t>(c.b) * a.max_chunks + ch) * a.Hq + c.g * a.G + h;
+      const uint64_t w = (static_cast<uint64_t>(TAGGED ? tag : 0u) << 32) | __float_as_uint(mass);
+      if constexpr (TAGGED) {
+        __hip_atomic_store(a.mw + at, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        a.mw[at] = w;
+      }
     }
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
@@ -195,7 +212,8 @@ __device__ __forceinline__ void flush_pairs(const ScoreArgs& a, const BatchCtx& 
 // s_qrow the rows' scored lengths and query rows.  Head mean stores
 // per-KV-head chunk sums (partial, or tagged with `tag` when TAGGED); head
 // max stores final chunk scores.  LSEFREE (head mean only): no LSE is read;
-// each chunk's (max, sum) per query head goes to a.mz instead.
+// each chunk's mass word per query head goes to a.mw instead (tagged when
+// TAGGED).
 template <int DT, int STEPS, int KB, bool HMAX, int PAGE, bool TAGGED, bool LSEFREE = false>
 __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_prefix, const int* s_len,
                                              const int* s_qrow, int total, int gw, int tw, uint32_t tag) {
@@ -404,7 +422,7 @@ __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_pr
         }
       } else if constexpr (LSEFREE) {
         if (ci != cur) {  // wave-uniform
-          flush_pairs(a, c, cur, cm, cz, kgrp, col);
+          flush_mass<KB, TAGGED>(a, c, cur, cm, cz, kgrp, col, tag);
           cur = ci;
         }
 #pragma unroll
@@ -443,7 +461,7 @@ __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_pr
 #pragma unroll
       for (int t = 0; t < kMaxNtu; ++t) tmax[t] = 0.f;
     } else if constexpr (LSEFREE) {
-      flush_pairs(a, c, cur, cm, cz, kgrp, col);
+      flush_mass<KB, TAGGED>(a, c, cur, cm, cz, kgrp, col, tag);
       cur = 0;
     } else {
 #pragma unroll
@@ -494,6 +512,96 @@ __device__ __forceinline__ void score_stream(const ScoreArgs& a, const int* s_pr
     compute(d1);
     inherit(d0, d1);
   }
+}
+
+// ---- Each query head's LSE from a row's mass words ------------------------
+// Both the kernel chain (lse_finalize_kernel) and the single launch's
+// selectors merge a row's mass words with this thread layout and these merge
+// steps, so both give the same bits.
+//
+// One KV group's G heads over the row's chunks, kThreads threads.  hp heads
+// per thread: 2 (`wide`, G even: one 16-byte read covers both) or 1.
+// P = G / hp phases, tpp threads per phase (a power of two, tpp * P <=
+// kThreads).  Thread (ph, j) adds the masses of chunks j, j + tpp, j + 2 tpp,
+// ... in that order (add_term); the lanes of one phase then merge by xor
+// shuffles (lane distances lstep .. lstep * lanes / 2), and the waves'
+// results are merged in LDS in wave order.  How the loads are batched does
+// not change any of these sums.  With P a power of two consecutive lanes
+// take consecutive phases, so a wave reads whole runs of a chunk's words;
+// otherwise each phase takes tpp adjacent lanes.
+constexpr int kLseLoads = 16;
+// The merge takes two heads per thread when the words are 16-byte aligned.
+inline int lse_words_wide(const void* mw) { return (reinterpret_cast<uintptr_t>(mw) & 15u) == 0 ? 1 : 0; }
+struct LseLayout {
+  int hp, P, tpp, ph, j, lstep, lanes;
+  bool inter;
+};
+__device__ __forceinline__ LseLayout lse_layout(int G, int wide, int t) {
+  LseLayout l;
+  l.hp = wide && G % 2 == 0 ? 2 : 1;
+  l.P = G / l.hp;
+  l.inter = (l.P & (l.P - 1)) == 0;
+  l.tpp = 1;
+  while (l.tpp * 2 * l.P <= kThreads) l.tpp *= 2;
+  l.ph = l.inter ? (t & (l.P - 1)) : t / l.tpp;
+  l.j = l.inter ? t / l.P : t % l.tpp;
+  l.lstep = l.inter ? l.P : 1;
+  l.lanes = l.inter ? 64 / l.P : (l.tpp < 64 ? l.tpp : 64);
+  return l;
+}
+
+// A thread's running sums of its hp heads, in log2 units.
+struct LseAcc {
+  float m0 = kNoMax, z0 = 0.f, m1 = kNoMax, z1 = 0.f;
+  __device__ __forceinline__ void add(uint64_t w0, uint64_t w1, int hp) {
+    add_term(m0, z0, mass_of(w0));
+    if (hp == 2) add_term(m1, z1, mass_of(w1));
+  }
+};
+
+// Ends one group's merge: the lane shuffles, then the waves' results through
+// s_m / s_z ([2][kThreads] floats of LDS the caller lends; a barrier on each
+// side).  Returns head t's natural-log LSE for t < G (-inf for a head with no
+// chunk).
+__device__ __forceinline__ float lse_finish(const LseLayout& l, LseAcc acc, int G, float (*s_m)[kThreads],
+                                            float (*s_z)[kThreads]) {
+  const int t = threadIdx.x;
+  for (int off = l.lstep; off < l.lstep * l.lanes; off <<= 1) {
+    merge_mz(acc.m0, acc.z0, __shfl_xor(acc.m0, off, 64), __shfl_xor(acc.z0, off, 64));
+    if (l.hp == 2) merge_mz(acc.m1, acc.z1, __shfl_xor(acc.m1, off, 64), __shfl_xor(acc.z1, off, 64));
+  }
+  s_m[0][t] = acc.m0;
+  s_z[0][t] = acc.z0;
+  s_m[1][t] = acc.m1;
+  s_z[1][t] = acc.z1;
+  __syncthreads();
+  float lse = -INFINITY;
+  if (t < G) {
+    // Head t is half t % hp of phase t / hp; one merged pair per wave of the
+    // phase: lane (phase) of every wave, or the first lane of each 64-lane
+    // block of the phase's tpp lanes.
+    const int q = t / l.hp, half = t % l.hp;
+    float mh = -INFINITY, zh = 0.f;
+    for (int k = 0; k < l.tpp; k += l.lanes) {
+      const int at = l.inter ? (k / l.lanes) * 64 + q : q * l.tpp + k;
+      merge_mz(mh, zh, s_m[half][at], s_z[half][at]);
+    }
+    const float lse2 = zh > 0.f ? mh + __log2f(zh) : -INFINITY;
+    lse = lse2 * 0.69314718055994530942f;
+  }
+  __syncthreads();
+  return lse;
+}
+
+// The exponent base of a head's chunk shares: its LSE as written (natural
+// log, fp32), in log2 units.
+__device__ __forceinline__ float lse_base2(float lse) { return lse * 1.44269504088896340736f; }
+
+// One head's share of a chunk's score, 2^(M - lse2), added to a KV group's
+// running sum (heads in order, from 0): nothing for a chunk or head without
+// mass.
+__device__ __forceinline__ float add_share(float sum, float mass, float lse2) {
+  return mass != -INFINITY && lse2 != -INFINITY ? sum + __builtin_amdgcn_exp2f(mass - lse2) : sum;
 }
 
 }  // namespace score

@@ -103,27 +103,25 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(const float* __restr
 // Scores without a supplied LSE, after the pass: lse_finalize_kernel, one
 // workgroup per (row, KV head, slice of finalize_slice(max_chunks) chunks:
 // 128, more when a row would need more than kMaxSlices slices).
-//   - Each query head of the group merges all of the row's (max, sum) pairs
-//     into its LSE.  A chunk's pairs are contiguous ([row, chunk, Hq]): tph
-//     threads per head stream them with kLseLoads loads in flight and merge
-//     by lane shuffles (and LDS when a head spans several waves).  The
-//     slice-0 workgroup writes the LSEs (natural log) to lse_out.
-//   - Then the KV head's partial of every chunk of the slice, sum over the
-//     group's heads of z * 2^(m - lse), which selection and the drop-in
+//   - The group's query heads merge all of the row's mass words into their
+//     LSEs (lse_layout / lse_finish, the merge the single launch's selectors
+//     run too).  The slice-0 workgroup writes the LSEs (natural log) to
+//     lse_out.
+//   - Then the KV head's partial of every chunk of the slice, the sum over
+//     the group's heads of 2^(M - lse2), which selection and the drop-in
 //     finalize read as with a supplied LSE.  The exponent uses the LSE as
 //     written (natural log, fp32) times log2(e).
-// Every slice of a row repeats the merge (its pairs come from L2 after the
+// Every slice of a row repeats the merge (its words come from L2 after the
 // first), which costs less than a second launch waiting on the first; the
-// cap on slices bounds the repeats at kMaxSlices reads of a row's pairs.
-constexpr int kLseLoads = 16;
+// cap on slices bounds the repeats at kMaxSlices reads of a row's words.
+// `wide` (16-byte aligned words): two heads per thread and 16-byte reads.
 constexpr int kFinalizeSlice = 128;  // chunks per workgroup, at least
 constexpr int kMaxSlices = 8;        // workgroups per (row, KV head), at most
-constexpr int kWideFinalizeChunks = 1024;  // 16-byte pair loads above this many chunks per row
 __host__ __device__ inline int finalize_slice(int max_chunks) {
   const int even = (max_chunks + kMaxSlices - 1) / kMaxSlices;
   return even > kFinalizeSlice ? even : kFinalizeSlice;
 }
-__global__ __launch_bounds__(kThreads) void lse_finalize_kernel(const float* __restrict__ mz, RowSource src,
+__global__ __launch_bounds__(kThreads) void lse_finalize_kernel(const uint64_t* __restrict__ mw, RowSource src,
                                                                 int max_chunks, int hq, int hkv, int chunk,
                                                                 float* __restrict__ lse_out, int64_t lse_stride,
                                                                 float* __restrict__ partial, int wide) {
@@ -142,106 +140,60 @@ __global__ __launch_bounds__(kThreads) void lse_finalize_kernel(const float* __r
   const int c_end = min(chunks, c_begin + slice);
   const int G = hq / hkv;
   const int t = threadIdx.x;
-  // Pairs [row, chunk, Hq]: head h of this group's chunk c at pairs[c * hq + h].
-  const float2* pairs = reinterpret_cast<const float2*>(mz) + static_cast<int64_t>(b) * max_chunks * hq + g * G;
+  // Words [row, chunk, Hq]: head h of this group's chunk c at words[c * hq + h].
+  const uint64_t* words = mw + static_cast<int64_t>(b) * max_chunks * hq + g * G;
 
-  // P phases cover a chunk's G pairs, hp heads each: one 16-byte load of two
-  // adjacent heads (hp = 2: `wide`, G even) or one 8-byte load.  The host
-  // asks for wide loads on rows of thousands of chunks, where they halve the
-  // load rounds of the merge (17.6 against 20.4 us on 4 x 128k tokens in
-  // 32-token chunks); on shorter rows the extra lane merges of a second head
-  // cost more than they save (7.2 against 6.3 us on 16 x 40k in 64-token
-  // chunks).  With P a power of two consecutive lanes take consecutive phases,
-  // so a wave reads whole runs of the chunk's pairs; otherwise each phase
-  // takes tpp adjacent lanes.  tpp = threads per phase (a power of two,
-  // tpp * P <= kThreads), lstep = lane distance between threads of one
-  // phase, lanes = how many of them one wave holds.
-  const int hp = wide && G % 2 == 0 ? 2 : 1;
-  const int P = G / hp;
-  const bool inter = (P & (P - 1)) == 0;
-  int tpp = 1;
-  while (tpp * 2 * P <= kThreads) tpp *= 2;
-  const int ph = inter ? (t & (P - 1)) : t / tpp;
-  const int j = inter ? t / P : t % tpp;
-  const int lstep = inter ? P : 1;
-  const int lanes = inter ? 64 / P : (tpp < 64 ? tpp : 64);
-  float m0 = -INFINITY, z0 = 0.f, m1 = -INFINITY, z1 = 0.f;
-  if (ph < P) {
-    if (hp == 2) {  // workgroup-uniform
-      const float4* p = reinterpret_cast<const float4*>(pairs + 2 * ph);
-      const int64_t cs = hq / 2;
-      for (int c0 = j; c0 < chunks; c0 += kLseLoads * tpp) {
-        float4 v[kLseLoads];
+  const LseLayout l = lse_layout(G, wide, t);
+  LseAcc acc;
+  if (l.ph < l.P) {
+    const uint64_t* p = words + l.hp * l.ph;
+    for (int c0 = l.j; c0 < chunks; c0 += kLseLoads * l.tpp) {
+      if (l.hp == 2) {  // workgroup-uniform
+        WordPair v[kLseLoads];
 #pragma unroll
         for (int u = 0; u < kLseLoads; ++u) {
-          const int c = c0 + u * tpp;
-          v[u] = c < chunks ? p[static_cast<int64_t>(c) * cs] : make_float4(-INFINITY, 0.f, -INFINITY, 0.f);
+          const int c = c0 + u * l.tpp;
+          v[u] = c < chunks ? *reinterpret_cast<const WordPair*>(p + static_cast<int64_t>(c) * hq)
+                            : WordPair{kNoMassWord, kNoMassWord};
         }
+#pragma unroll
+        for (int u = 0; u < kLseLoads; ++u) acc.add(v[u].a, v[u].b, 2);
+      } else {
+        uint64_t v[kLseLoads];
 #pragma unroll
         for (int u = 0; u < kLseLoads; ++u) {
-          merge_mz(m0, z0, v[u].x, v[u].y);
-          merge_mz(m1, z1, v[u].z, v[u].w);
-        }
-      }
-    } else {
-      const float2* p = pairs + ph;
-      for (int c0 = j; c0 < chunks; c0 += kLseLoads * tpp) {
-        float2 v[kLseLoads];
-#pragma unroll
-        for (int u = 0; u < kLseLoads; ++u) {
-          const int c = c0 + u * tpp;
-          v[u] = c < chunks ? p[static_cast<int64_t>(c) * hq] : make_float2(-INFINITY, 0.f);
+          const int c = c0 + u * l.tpp;
+          v[u] = c < chunks ? p[static_cast<int64_t>(c) * hq] : kNoMassWord;
         }
 #pragma unroll
-        for (int u = 0; u < kLseLoads; ++u) merge_mz(m0, z0, v[u].x, v[u].y);
+        for (int u = 0; u < kLseLoads; ++u) acc.add(v[u], 0u, 1);
       }
     }
   }
-  for (int off = lstep; off < lstep * lanes; off <<= 1) {
-    merge_mz(m0, z0, __shfl_xor(m0, off, 64), __shfl_xor(z0, off, 64));
-    if (hp == 2) merge_mz(m1, z1, __shfl_xor(m1, off, 64), __shfl_xor(z1, off, 64));
-  }
-  s_m[0][t] = m0;
-  s_z[0][t] = z0;
-  s_m[1][t] = m1;
-  s_z[1][t] = z1;
-  __syncthreads();
+  const float lse = lse_finish(l, acc, G, s_m, s_z);
   if (t < G) {
-    // Head t is half t % hp of phase t / hp; one merged pair per wave of the
-    // phase: lane (phase) of every wave, or the first lane of each 64-lane
-    // block of the phase's tpp lanes.
-    const int q = t / hp, half = t % hp;
-    float mh = -INFINITY, zh = 0.f;
-    for (int k = 0; k < tpp; k += lanes) {
-      const int at = inter ? (k / lanes) * 64 + q : q * tpp + k;
-      merge_mz(mh, zh, s_m[half][at], s_z[half][at]);
-    }
-    const float lse2 = zh > 0.f ? mh + __log2f(zh) : -INFINITY;
-    const float lse = lse2 * 0.69314718055994530942f;
     if (s == 0) lse_out[static_cast<int64_t>(b) * lse_stride + g * G + t] = lse;
-    s_lse2[t] = lse * 1.44269504088896340736f;
+    s_lse2[t] = lse_base2(lse);
   }
   __syncthreads();
 
   for (int c = c_begin + t; c < c_end; c += kThreads) {
-    float2 v[kMaxGroup];
-    const float2* at = pairs + static_cast<int64_t>(c) * hq;
-    if (hp == 2) {
+    uint64_t v[kMaxGroup];
+    const uint64_t* at = words + static_cast<int64_t>(c) * hq;
+    if (l.hp == 2) {
 #pragma unroll
       for (int h = 0; h < kMaxGroup; h += 2) {
-        const float4 w = h < G ? *reinterpret_cast<const float4*>(at + h) : make_float4(-INFINITY, 0.f, -INFINITY, 0.f);
-        v[h] = make_float2(w.x, w.y);
-        v[h + 1] = make_float2(w.z, w.w);
+        const WordPair w = h < G ? *reinterpret_cast<const WordPair*>(at + h) : WordPair{kNoMassWord, kNoMassWord};
+        v[h] = w.a;
+        v[h + 1] = w.b;
       }
     } else {
 #pragma unroll
-      for (int h = 0; h < kMaxGroup; ++h) v[h] = h < G ? at[h] : make_float2(-INFINITY, 0.f);
+      for (int h = 0; h < kMaxGroup; ++h) v[h] = h < G ? at[h] : kNoMassWord;
     }
     float sum = 0.f;
 #pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h) {
-      if (v[h].x != -INFINITY && s_lse2[h] != -INFINITY) sum += v[h].y * __builtin_amdgcn_exp2f(v[h].x - s_lse2[h]);
-    }
+    for (int h = 0; h < kMaxGroup; ++h) sum = h < G ? add_share(sum, mass_of(v[h]), s_lse2[h]) : sum;
     partial[(static_cast<int64_t>(b) * max_chunks + c) * hkv + g] = sum;
   }
 }
@@ -291,7 +243,7 @@ int make_score_args(ScoreArgs& a, int64_t& upper_units, int& page_mode, int dtyp
                     const int32_t* block_table, int64_t bt_stride, const RowSource& src, int batch, int num_q_heads,
                     int num_kv_heads, int head_dim, int block_size, int chunk_size, int max_chunks, float scale,
                     int head_reduce, float* partial, float* out, int64_t out_stride, int write_tail,
-                    size_t partial_bytes, float* mz) {
+                    size_t partial_bytes, uint64_t* mw) {
   upper_units = 0;
   page_mode = PAGE_LANE;
   DS_REQUIRE(dtype == DS_BF16 || dtype == DS_FP16, "chunk scores support BF16 or FP16 query/key caches");
@@ -322,9 +274,11 @@ int make_score_args(ScoreArgs& a, int64_t& upper_units, int& page_mode, int dtyp
   DS_SUPPORTED(!hmax || ntu <= kMaxNtu, "head_reduce=max supports chunks of at most %d tokens", kMaxNtu * 16);
   if (batch == 0 || max_chunks == 0) return clear_error();
   DS_REQUIRE(query && key_cache && block_table, "null tensor pointer");
-  // No LSE: the pass computes it (head mean only); the pairs need mz.
+  // No LSE: the pass computes it (head mean only); the mass words need mw.
   DS_SUPPORTED(lse || !hmax, "head_reduce=max needs a supplied softmax LSE");
-  DS_REQUIRE(lse || mz,
+  DS_REQUIRE(lse || (reinterpret_cast<uintptr_t>(mw) & 7u) == 0,
+             "the mass words without an LSE (lse_partials / workspace) must be 8-byte aligned");
+  DS_REQUIRE(lse || mw,
              "workspace too small: need %zu bytes without an LSE (batch * (max_chunks * (kv_heads + 2 * q_heads) + "
              "q_heads) * 4)",
              static_cast<size_t>(batch) *
@@ -374,7 +328,7 @@ int make_score_args(ScoreArgs& a, int64_t& upper_units, int& page_mode, int dtyp
   a.ci_shift = cpu > 1 ? log2_or_neg(chunk_size) : 31;
   a.scale = scale;
   a.partial = partial;
-  a.mz = lse ? nullptr : mz;
+  a.mw = lse ? nullptr : mw;
   a.out = out;
   a.out_stride = out_stride;
   a.write_tail = hmax ? write_tail : 0;
@@ -396,7 +350,7 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
                         int64_t bt_stride, const RowSource& src, int batch, int num_q_heads, int num_kv_heads,
                         int head_dim, int block_size, int chunk_size, int max_chunks, float scale, int head_reduce,
                         float* partial, float* out, int64_t out_stride, int write_tail, size_t partial_bytes,
-                        float* mz, float* lse_out, int64_t lse_out_stride) {
+                        uint64_t* mw, float* lse_out, int64_t lse_out_stride) {
   ScoreArgs a{};
   int64_t upper_units = 0;
   int page_mode = PAGE_LANE;
@@ -404,7 +358,7 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
                                  k_token_stride, k_head_stride, lse, lse_row_stride, lse_head_stride, block_table,
                                  bt_stride, src, batch, num_q_heads, num_kv_heads, head_dim, block_size, chunk_size,
                                  max_chunks, scale, head_reduce, partial, out, out_stride, write_tail, partial_bytes,
-                                 mz);
+                                 mw);
   if (rc != DS_OK || upper_units == 0) return rc;
   const bool hmax = head_reduce == DS_HEAD_MAX;
   const bool lse_free = lse == nullptr;
@@ -430,8 +384,8 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
   int rc2 = check_launch("ds_chunk_scores");
   if (rc2 != DS_OK || !lse_free) return rc2;
   lse_finalize_kernel<<<static_cast<unsigned>(partial_grid), kThreads, 0, stream>>>(
-      a.mz, a.src, max_chunks, num_q_heads, num_kv_heads, chunk_size, lse_out, lse_out_stride, partial,
-      (reinterpret_cast<uintptr_t>(a.mz) & 15u) == 0 && max_chunks > kWideFinalizeChunks ? 1 : 0);
+      a.mw, a.src, max_chunks, num_q_heads, num_kv_heads, chunk_size, lse_out, lse_out_stride, partial,
+      lse_words_wide(a.mw));
   return check_launch("ds_chunk_scores lse");
 }
 
@@ -449,11 +403,11 @@ extern "C" int ds_chunk_scores(ds_stream_t stream, int dtype, const void* query,
   src.seq_lens = seq_lens;
   const bool hmax = head_reduce == DS_HEAD_MAX;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  // Without an LSE the workspace holds the (max, sum) pairs first (8-byte
-  // aligned with the workspace), then each row's LSE ([batch, Hq]), then the
-  // per-KV-head partials; a workspace too small for all three is reported
-  // with the other argument checks.
-  float* mz = nullptr;
+  // Without an LSE the workspace holds the mass words first ([batch,
+  // max_chunks, Hq] 64-bit words at the workspace's start), then each row's
+  // LSE ([batch, Hq]), then the per-KV-head partials; a workspace too small
+  // for all three is reported with the other argument checks.
+  uint64_t* mw = nullptr;
   float* lse_rows = nullptr;
   float* partial = workspace;
   size_t partial_bytes = workspace_bytes;
@@ -462,7 +416,7 @@ extern "C" int ds_chunk_scores(ds_stream_t stream, int dtype, const void* query,
     const size_t lses = static_cast<size_t>(batch) * num_q_heads;
     const size_t need = (static_cast<size_t>(batch) * max_chunks * num_kv_heads + pairs + lses) * sizeof(float);
     if (workspace != nullptr && workspace_bytes >= need) {
-      mz = workspace;
+      mw = reinterpret_cast<uint64_t*>(workspace);
       lse_rows = workspace + pairs;
       partial = lse_rows + lses;
       partial_bytes = workspace_bytes - (pairs + lses) * sizeof(float);
@@ -471,7 +425,7 @@ extern "C" int ds_chunk_scores(ds_stream_t stream, int dtype, const void* query,
   int rc = launch_chunk_scores(s, dtype, query, q_stride, key_cache, k_block_stride, k_token_stride, k_head_stride,
                                lse, lse_row_stride, lse_head_stride, block_table, bt_stride, src, batch, num_q_heads,
                                num_kv_heads, head_dim, block_size, chunk_size, max_chunks, scale, head_reduce,
-                               partial, out, out_stride, 1, partial_bytes, mz, lse_rows, num_q_heads);
+                               partial, out, out_stride, 1, partial_bytes, mw, lse_rows, num_q_heads);
   if (rc != DS_OK || hmax || batch == 0 || max_chunks == 0) return rc;
   DS_REQUIRE(out != nullptr, "null score output pointer");
   const int64_t n = static_cast<int64_t>(batch) * max_chunks;

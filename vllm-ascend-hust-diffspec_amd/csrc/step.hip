@@ -16,7 +16,7 @@ int launch_chunk_scores(hipStream_t stream, int dtype, const void* query, int64_
                         int64_t bt_stride, const RowSource& src, int batch, int num_q_heads, int num_kv_heads,
                         int head_dim, int block_size, int chunk_size, int max_chunks, float scale, int head_reduce,
                         float* partial, float* out, int64_t out_stride, int write_tail, size_t partial_bytes,
-                        float* mz, float* lse_out, int64_t lse_out_stride);
+                        uint64_t* mw, float* lse_out, int64_t lse_out_stride);
 
 int launch_select_plan(hipStream_t stream, float* scores, int64_t score_stride, const float* partials,
                        int max_chunks, int hkv, int hq, const RowSource& src,
@@ -103,7 +103,7 @@ int retrieval_step(hipStream_t stream, const ds_step_desc* d, uint32_t* status_o
                              d->k_token_stride, d->k_head_stride, d->lse, d->lse_token_stride, d->lse_head_stride,
                              d->block_table, d->bt_stride, src, d->batch_rows, d->num_q_heads, d->num_kv_heads,
                              d->head_dim, d->block_size, d->chunk_size, d->max_chunks, d->scale, DS_HEAD_MEAN,
-                             d->score_partials, nullptr, 0, 0, SIZE_MAX, d->lse_partials, d->lse_out,
+                             d->score_partials, nullptr, 0, 0, SIZE_MAX, reinterpret_cast<uint64_t*>(d->lse_partials), d->lse_out,
                              d->lse_out_stride);
     if (rc != DS_OK) return rc;
   }

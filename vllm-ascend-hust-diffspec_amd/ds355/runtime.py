@@ -261,8 +261,8 @@ WORKING_LENS = "working_lens"  # pending positions = the slots' device working l
 # positions.
 RETRIEVAL_STAGES = _step.SCORE | _step.SELECT
 PREFIX_RETRIEVAL_STAGES = _step.SCORE | _step.SELECT | _step.PREFIX
-# Batches from which a step with a supplied LSE and a workspace runs as the
-# single launch (the library's minimum, csrc/fused.hip kMinFusedRows).
+# Batches from which a step with a workspace runs as the single launch (the
+# library's minimum, csrc/fused.hip kMinFusedRows), with or without an LSE.
 SINGLE_LAUNCH_MIN_ROWS = 8
 
 
@@ -345,8 +345,8 @@ class DiffSpecDraftCache:
         # for scoring and selection, then the whole rebuild); in the chain it
         # adds a launch (one 8k row: 21.1 + 6.4 against 15.7 + 8.3 us).  So by
         # default (None) it is on exactly when the retrieval is the single
-        # launch: 8+ rows and a supplied LSE.  Between retrievals the compact
-        # prefill moves the rolling tail.
+        # launch: 8+ rows.  Between retrievals the compact prefill moves the
+        # rolling tail.
         self.sel_gen = torch.zeros((max_num_reqs,), dtype=torch.int32, device=self.device)
         self.gather_records = torch.zeros((max_num_reqs, settings.token_budget), dtype=torch.int64,
                                           device=self.device)
@@ -360,8 +360,10 @@ class DiffSpecDraftCache:
         self.scores = torch.zeros((rows, self.max_chunks), dtype=torch.float32, device=self.device)
         self._score_partials: torch.Tensor | None = None  # [rows, max_chunks, target KV heads], on first use
         self.lse_free_scoring = lse_free_scoring
-        # Without a snapshot LSE: (max, sum) pairs [rows, max_chunks, Hq, 2]
-        # and the computed natural-log LSE [rows, Hq], on first use.
+        # Without a snapshot LSE: the scoring pass's mass words (the library's
+        # lse_partials, [rows, max_chunks, Hq, 2] fp32 = one 64-bit word per
+        # chunk and head) and the computed natural-log LSE [rows, Hq], on
+        # first use.
         self._lse_partials: torch.Tensor | None = None
         self.scored_lse: torch.Tensor | None = None
         self.plan = torch.zeros((rows, _plan_width(settings.token_budget, settings.chunk_size)),
@@ -432,11 +434,11 @@ class DiffSpecDraftCache:
         self.proposed_depths: torch.Tensor | None = None
         self.proposed_depths_cpu: list[int] = []
 
-    def retrieval_stages_for(self, batch_size: int, lse: torch.Tensor | None) -> int:
+    def retrieval_stages_for(self, batch_size: int) -> int:
         """The retrieval call's stages for a batch (see prefix_at_retrieval)."""
         prefix = self.prefix_at_retrieval
         if prefix is None:
-            prefix = batch_size >= SINGLE_LAUNCH_MIN_ROWS and lse is not None
+            prefix = batch_size >= SINGLE_LAUNCH_MIN_ROWS
         return PREFIX_RETRIEVAL_STAGES if prefix else RETRIEVAL_STAGES
 
     @property
@@ -602,7 +604,7 @@ class DiffSpecDraftCache:
         staged = self._rows_staging.upload([
             starts, [e - s for s, e in zip(starts, ends)], seq_lens[:batch_size], self._active_slots, [],
         ])
-        key = self._step_key(self.retrieval_stages_for(batch_size, self._target_lse), batch_size, batch_size,
+        key = self._step_key(self.retrieval_stages_for(batch_size), batch_size, batch_size,
                              self._cos_sin_cache(),
                              self._target_query, self._target_lse, self._target_key_cache, self._target_block_tables)
         return self._active_slots, staged, key
@@ -713,7 +715,7 @@ class DiffSpecDraftCache:
         if self.controller.adaptive:
             self._copy_selection_state(0)
         q, lse, kc, bt = self._target_query, self._target_lse, self._target_key_cache, self._target_block_tables
-        stages = self.retrieval_stages_for(batch_size, lse)
+        stages = self.retrieval_stages_for(batch_size)
         if key is None:
             key = self._step_key(stages, batch_size, batch_size, self._cos_sin_cache(), q, lse, kc, bt)
         hit = self._step_descs.get(key)
@@ -1061,7 +1063,7 @@ class DiffSpecDraftCache:
             lse_partials = self._view("pairs", batch_rows, lambda: self._lse_partials[:batch_rows])
             lse_out = self._view("lse_out", batch_rows, lambda: self.scored_lse[:batch_rows])
         workspace = None
-        if stages & _step.SCORE and stages & _step.PREFIX and snapshot.lse is not None:
+        if stages & _step.SCORE and stages & _step.PREFIX:
             # Score, selection and the prefix gather as one launch where the
             # batch suits it (the library picks; the workspace allows it).
             kv_heads = snapshot.key_cache.shape[2]

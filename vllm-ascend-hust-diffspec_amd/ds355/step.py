@@ -181,9 +181,11 @@ def build_step_desc(
     one launch when its shapes allow it; the results are the same.
 
     Without a snapshot LSE, SCORE needs ``lse_partials`` (``[batch_rows,
-    max_chunks, Hq, 2]`` fp32 scratch: each chunk's (max, sum) per query head)
-    and ``lse_out`` (``[batch_rows, Hq]`` fp32, where each scored row's
-    natural-log LSE is written); such a step runs as the kernel chain.
+    max_chunks, Hq, 2]`` fp32 scratch: one 64-bit word per chunk and query
+    head holding the chunk's mass) and ``lse_out`` (``[batch_rows, Hq]`` fp32,
+    where each scored row's natural-log LSE is written).  With a workspace
+    the full step still runs as the single launch; its words carry that
+    workspace's launch tags, so keep one ``lse_partials`` per workspace.
 
     ``flags`` (tests only): ``SELECTORS_GATHER`` makes the single launch's
     scoring waves leave every gather task to the last workgroup to finish

@@ -124,6 +124,7 @@ __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirs
 // arithmetic in vector registers (which also made the compiler wait for
 // loads in flight before reusing the registers).
 typedef __amdgpu_buffer_rsrc_t SRsrc;
+constexpr int kCoherentStorePolicy = 16;  // sc1: the cache policy of device-scope relaxed atomic stores
 __device__ __forceinline__ SRsrc srsrc(const void* base, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
@@ -182,27 +183,58 @@ __device__ __forceinline__ void flush_mass(const ScoreArgs& a, const BatchCtx& c
                                            float (&z)[KB][4], int kgrp, int col, uint32_t tag) {
   const int ch = c.c0 + cc;
   const int chunks_row = (c.len + a.chunk - 1) / a.chunk;
+  float mass[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     float mt = m[0][e], zt = z[0][e];
 #pragma unroll
     for (int i = 1; i < KB; ++i) merge_mz(mt, zt, m[i][e], z[i][e]);
     merge_mz_row16(mt, zt);
-    const int h = 4 * kgrp + e;
-    if (col == 0 && h < a.G && ch < chunks_row) {
-      const float mass = zt > 0.f ? mt + __log2f(zt) : -INFINITY;
-      const int64_t at = (static_cast<int64_t>(c.b) * a.max_chunks + ch) * a.Hq + c.g * a.G + h;
-      const uint64_t w = (static_cast<uint64_t>(TAGGED ? tag : 0u) << 32) | __float_as_uint(mass);
-      if constexpr (TAGGED) {
-        __hip_atomic_store(a.mw + at, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      } else {
-        a.mw[at] = w;
-      }
-    }
+    mass[e] = zt > 0.f ? mt + __log2f(zt) : -INFINITY;
 #pragma unroll
     for (int i = 0; i < KB; ++i) {
       m[i][e] = kNoMax;
       z[i][e] = 0.f;
+    }
+  }
+  // Lane (kgrp, col 0) holds heads 4 kgrp .. 4 kgrp + 3 of the group: two
+  // adjacent heads' words go out as one 16-byte store where both exist and
+  // the address allows (half the store instructions of 8-byte words; each
+  // 8-byte word is still written whole).
+  if (col == 0 && ch < chunks_row) {
+    const int64_t row_words = static_cast<int64_t>(c.b) * a.max_chunks * a.Hq;
+    const int at0 = ch * a.Hq + c.g * a.G + 4 * kgrp;  // within the row
+    const uint64_t tg = static_cast<uint64_t>(TAGGED ? tag : 0u) << 32;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int h = 4 * kgrp + 2 * p;
+      if (h < a.G) {
+        const uint64_t w0 = tg | __float_as_uint(mass[2 * p]);
+        const uint64_t w1 = tg | __float_as_uint(mass[2 * p + 1]);
+        uint64_t* dst = a.mw + row_words + at0 + 2 * p;
+        const bool pair = h + 1 < a.G && (reinterpret_cast<uintptr_t>(dst) & 15u) == 0;
+        if constexpr (TAGGED) {
+          if (pair) {
+            const SRsrc r = srsrc(a.mw + row_words, a.max_chunks * a.Hq * static_cast<int>(sizeof(uint64_t)));
+            const uint32_t v[4] = {static_cast<uint32_t>(w0), static_cast<uint32_t>(w0 >> 32),
+                                   static_cast<uint32_t>(w1), static_cast<uint32_t>(w1 >> 32)};
+            typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4_t{v[0], v[1], v[2], v[3]}, r,
+                                                   (at0 + 2 * p) * static_cast<int>(sizeof(uint64_t)), 0,
+                                                   kCoherentStorePolicy);
+          } else {
+            __hip_atomic_store(dst, w0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (h + 1 < a.G) __hip_atomic_store(dst + 1, w1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        } else {
+          if (pair) {
+            *reinterpret_cast<WordPair*>(dst) = WordPair{w0, w1};
+          } else {
+            dst[0] = w0;
+            if (h + 1 < a.G) dst[1] = w1;
+          }
+        }
+      }
     }
   }
 }

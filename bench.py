@@ -359,16 +359,29 @@ def run(args):
 
     free_score_us = time_free(step.SCORE, reps)
     free_epochs = [step.workspace_epoch(st["workspace"]) for st in states] if single else []
-    free_step_us = time_free(step.ALL, reps)
+    free_step_events_us = time_free(step.ALL, reps)
+    # The full step back to back, timed as `value` is (events only around the whole run).
+    a_ev, b_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a_ev.record()
+    for i in range(reps):
+        desc = free_descs[i % len(free_descs)]
+        desc.stages = step.ALL
+        _lib.check(lib.ds_retrieval_step(stream, desc))
+    b_ev.record()
+    torch.cuda.synchronize()
+    free_step_us = a_ev.elapsed_time(b_ev) * 1e3 / reps
     free_single = single and [step.workspace_epoch(st["workspace"]) for st in states] != free_epochs
     if free_single and any(step.workspace_status(st["workspace"]) for st in states):
         raise RuntimeError("a single launch without an LSE reported an expired wait: results not valid")
     free_gbps = score_bytes / (free_score_us * 1e-6) / 1e9
     lse_free_leg = {
         "what": "scores without a supplied softmax LSE: the scoring pass stores each chunk's mass per query "
-                "head; the single launch's selectors (or, for SCORE alone and the chain, lse_finalize_kernel) "
-                "merge them into each head's LSE and the chunk scores",
+                "head; the single launch's group workgroups (or, for SCORE alone and the chain, "
+                "lse_finalize_kernel) merge them into each head's LSE and the chunk scores.  step_us: the full "
+                "step back to back, timed as value is; score_us and step_us_events_per_launch put events "
+                "around each launch",
         "score_us": round(free_score_us, 2), "step_us": round(free_step_us, 2),
+        "step_us_events_per_launch": round(free_step_events_us, 2),
         "step_path": "single launch (fused_step_kernel)" if free_single else "chain",
         "step_us_with_lse": round(chain_ms * 1e3, 2),
         "score_us_with_lse": round(score_us, 2),

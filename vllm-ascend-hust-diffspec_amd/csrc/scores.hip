@@ -29,9 +29,11 @@
 // softmax_lse=None, diffspec/runtime.py:321-322: the LSE of each query head
 // over the row's scored tokens) the same single pass keeps, per lane, a
 // running (max, sum of 2^(logit - max)) per chunk and query head, merges the
-// 16 token lanes with DPP permutes and stores the pairs; lse_finalize_kernel
-// then merges a row's chunks into each head's LSE and writes the usual per-KV-head partials, sum over the group's heads of
-// z * 2^(m - lse), so selection and the drop-in finalize read them unchanged.
+// 16 token lanes with DPP permutes and stores each chunk's log2 mass
+// M = max + log2(sum) as one 64-bit word per query head; lse_finalize_kernel
+// then merges a row's chunks into each head's LSE and writes the usual
+// per-KV-head partials, the sum over the group's heads of 2^(M - lse), so
+// selection and the drop-in finalize read them unchanged.
 #include "score_body.h"
 
 namespace ds355 {

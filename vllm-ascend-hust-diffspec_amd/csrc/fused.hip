@@ -397,9 +397,11 @@ __device__ __forceinline__ void select_row(const FusedArgs& f, int b, uint32_t t
   const RowDesc d = row_desc(a.src, b);
   const int slot = a.slots[b];
   const bool slot_ok = slot >= 0 && slot < a.num_slots;
-  const int committed = committed_of(a.committed_lens, a.src, b);
-  const int stored_count = slot_ok ? a.counts[slot] : 0;
-  uint32_t gen = (f.rec != nullptr && slot_ok) ? static_cast<uint32_t>(f.gen[slot]) : 0u;
+  // Made scalar (waited for) here: they are used only after the selection's
+  // stores, where waiting for their loads would wait for those stores too.
+  const int committed = __builtin_amdgcn_readfirstlane(committed_of(a.committed_lens, a.src, b));
+  const int stored_count = __builtin_amdgcn_readfirstlane(slot_ok ? a.counts[slot] : 0);
+  uint32_t gen = __builtin_amdgcn_readfirstlane((f.rec != nullptr && slot_ok) ? static_cast<uint32_t>(f.gen[slot]) : 0u);
   // The previous row's plan columns are read from sh.ids up to its end.
   lds_barrier();
   if (f.expire && tid == 0) raise_status(f.header, kStatusPartials);

@@ -250,22 +250,16 @@ __device__ __forceinline__ void select_top(SelectShared<KEYS, NT>& sh, int N, in
   if (tid == 0) sh.ids[K - 1] = N;
 }
 
-// Plan row of batch row b for a valid slot, from the selection just made
-// (n_sel >= 0, ids in sh.ids) or the slot's stored one (n_sel < 0,
-// stored_count entries).  Writes plan[b] and working_lens[slot]; with a
-// tagged copy, also stores column j as (tag << 32) | value in tagged[j]
-// with a device-scope store (plan values are below 2^31).  No barriers.
-template <int KEYS, int NT>
-__device__ __forceinline__ void write_plan_row(const SelectArgs& a, int b, int slot, int committed, int n_sel,
-                                               int stored_count, SelectShared<KEYS, NT>& sh,
-                                               uint64_t* tagged = nullptr, uint32_t tag = 0) {
+// Plan row of batch row b for a valid slot with `count` chunk ids
+// (count < 0: no selection), id j read by chunk_id(j).  Writes plan[b] and
+// working_lens[slot]; with a tagged copy, also stores column j as
+// (tag << 32) | value in tagged[j] with a device-scope store (plan values
+// are below 2^31).  No barriers.
+template <int NT, typename ChunkId>
+__device__ __forceinline__ void plan_row_from(const SelectArgs& a, int b, int slot, int committed, int count,
+                                              ChunkId chunk_id, uint64_t* tagged, uint32_t tag) {
   const int tid = threadIdx.x;
   int64_t* prow = a.plan + static_cast<int64_t>(b) * a.plan_width;
-  const int64_t cap = min(static_cast<int64_t>(a.plan_width - 5), a.ids_stride);
-  const int count = n_sel >= 0 ? n_sel : static_cast<int>(min(static_cast<int64_t>(stored_count), cap));
-  const int32_t* stored = a.ids + static_cast<int64_t>(slot) * a.ids_stride;
-  auto chunk_id = [&](int j) -> int64_t { return n_sel >= 0 ? sh.ids[j] : stored[j]; };
-
   const int64_t end = max(0, committed - 1);
   const int64_t hb = a.budget;
   int64_t len, tail_start, prefix_len = 0, drop = 0;
@@ -307,6 +301,26 @@ __device__ __forceinline__ void write_plan_row(const SelectArgs& a, int b, int s
     }
   }
   if (tid == 0 && a.working_lens != nullptr) a.working_lens[slot] = static_cast<int32_t>(len);
+}
+
+// Plan row of batch row b for a valid slot, from the selection just made
+// (n_sel >= 0, ids in sh.ids) or the slot's stored one (n_sel < 0,
+// stored_count entries).  The two sources get a loop each: ids read
+// through a pointer that may be LDS or global memory compile to flat loads,
+// and each of those waited for every store in flight (the selection's own
+// ids and scores), a memory round trip per read.
+template <int KEYS, int NT>
+__device__ __forceinline__ void write_plan_row(const SelectArgs& a, int b, int slot, int committed, int n_sel,
+                                               int stored_count, SelectShared<KEYS, NT>& sh,
+                                               uint64_t* tagged = nullptr, uint32_t tag = 0) {
+  if (n_sel >= 0) {  // workgroup-uniform
+    plan_row_from<NT>(a, b, slot, committed, n_sel, [&](int j) -> int64_t { return sh.ids[j]; }, tagged, tag);
+  } else {
+    const int64_t cap = min(static_cast<int64_t>(a.plan_width - 5), a.ids_stride);
+    const int count = static_cast<int>(min(static_cast<int64_t>(stored_count), cap));
+    const int32_t* stored = a.ids + static_cast<int64_t>(slot) * a.ids_stride;
+    plan_row_from<NT>(a, b, slot, committed, count, [&](int j) -> int64_t { return stored[j]; }, tagged, tag);
+  }
 }
 
 }  // namespace select

@@ -40,9 +40,9 @@ __global__ __launch_bounds__(NT) void select_plan_kernel(SelectArgs a) {
   const RowDesc d = a.do_select ? row_desc(a.src, b) : RowDesc{0, 0, 0};
   const int slot = a.slots != nullptr ? a.slots[b] : b;
   const bool slot_ok = slot >= 0 && slot < a.num_slots;
-  const int committed = a.do_plan ? committed_of(a.committed_lens, a.src, b) : 0;
-  const int stored_count = (a.do_plan && slot_ok) ? a.counts[slot] : 0;
-  const int32_t gen0 = (a.gen != nullptr && a.do_select && slot_ok) ? a.gen[slot] : 0;
+  int committed = a.do_plan ? committed_of(a.committed_lens, a.src, b) : 0;
+  int stored_count = (a.do_plan && slot_ok) ? a.counts[slot] : 0;
+  int32_t gen0 = (a.gen != nullptr && a.do_select && slot_ok) ? a.gen[slot] : 0;
   const float* part = a.partials + static_cast<int64_t>(b) * a.max_chunks * a.hkv;
   float pre[kPre];
   if (a.do_select && a.partials != nullptr) {
@@ -52,6 +52,12 @@ __global__ __launch_bounds__(NT) void select_plan_kernel(SelectArgs a) {
       pre[u] = head_sum<HKV>(part + static_cast<int64_t>(i) * a.hkv, a.hkv);
     }
   }
+  // Made scalar (waited for) here, behind the loads above: they are used
+  // only after the selection's stores, where waiting for their loads would
+  // wait for those stores too.
+  committed = __builtin_amdgcn_readfirstlane(committed);
+  stored_count = __builtin_amdgcn_readfirstlane(stored_count);
+  gen0 = __builtin_amdgcn_readfirstlane(gen0);
   int n_sel = -1;  // selection made by this workgroup (in sh.ids), -1 if none
 
   if (a.do_select && d.active && slot_ok) {

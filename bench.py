@@ -845,6 +845,18 @@ def draft_attention_leg(spec, states, rows, hb, device, reps, seed, with_cpu):
     b.record()
     torch.cuda.synchronize()
     back_to_back_us = a.elapsed_time(b) * 1e3 / reps
+    # A draft cycle's pattern: K steps over the same working caches (67 MB at
+    # 16 rows), which stay in the 256 MB MALL between the steps.
+    one = [c for i, c in enumerate(calls) if i % ATTENTION_COPIES == 0]
+    for c in one:
+        _lib.check(lib.ds_draft_attention(*c))
+    torch.cuda.synchronize()
+    a.record()
+    for i in range(reps):
+        _lib.check(lib.ds_draft_attention(*one[i % len(one)]))
+    b.record()
+    torch.cuda.synchronize()
+    one_cache_us = a.elapsed_time(b) * 1e3 / reps
     status = [attention.attention_status(t["ws"]) for t in sets]
     if any(status):
         raise RuntimeError(f"draft attention status words {status}")
@@ -861,6 +873,7 @@ def draft_attention_leg(spec, states, rows, hb, device, reps, seed, with_cpu):
         "kernel": "draft_attention_kernel",
         "avg_us": round(back_to_back_us, 2),
         "single_launch_event_us": round(avg_us, 2),
+        "one_cache_us": round(one_cache_us, 2),
         "algorithmic_bytes": algo,
         "achieved": round(gbps, 1),
         "peak": HBM_PEAK_GBPS,

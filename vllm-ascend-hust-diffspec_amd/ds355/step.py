@@ -123,7 +123,8 @@ def launch_static(desc: _lib.StepDesc, device: torch.device, status: torch.Tenso
     """Launch a prebuilt descriptor through ``ds_retrieval_step_static``.
 
     The step's scratch (score partials, the single launch's workspace, the
-    LSE pairs) then lives in the library's static device array, so the
+    mass words scored without an LSE) then lives in the library's static
+    device array, so the
     descriptor's ``score_partials``, ``workspace`` and ``lse_partials`` are
     cleared for this call (the descriptor itself is not changed).  Nothing is
     allocated.  ``status`` (an int32 device word the caller clears) receives

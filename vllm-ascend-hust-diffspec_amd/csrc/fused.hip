@@ -650,7 +650,7 @@ struct WorkShared {
 
 template <int DT, int STEPS, bool NEOX, int PAGE, bool LSEFREE>
 __global__ __launch_bounds__(kThreads, 3) void fused_step_kernel(FusedArgs f) {
-  constexpr int KB = STEPS <= 2 ? 4 : 1;  // chunk_score_kernel's batch shape for head_dim <= 128
+  constexpr int KB = STEPS <= 2 ? 2 : 1;  // chunk_score_kernel's batch shape (4 KB) for head_dim <= 128
   __shared__ union {
     select::SelectShared<kFusedKeys> sel;
     WorkShared w;

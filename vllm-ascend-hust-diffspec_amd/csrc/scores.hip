@@ -202,17 +202,18 @@ __global__ __launch_bounds__(kThreads) void lse_finalize_kernel(const uint64_t* 
 
 template <int DT, int STEPS, bool HMAX, bool LSEFREE>
 void launch_kb(hipStream_t stream, const ScoreArgs& a, int64_t upper_blocks, int page_mode) {
-  // Batch shape, measured at head_dim 128 with three workgroups per CU:
-  // one 16-token group (4 KB of keys) per wave and batch beat two (8 KB) by
+  // Batch shape: about 4 KB of keys per wave and batch at three workgroups
+  // per CU.  At head_dim 128 one 16-token group (4 KB) beat two (8 KB) by
   // 1.3 us on 16 rows of 4k-40k tokens and 0.4-0.7 us on 16 x 40k and
-  // 4 x 128k; both beat 16 KB batches at two workgroups per CU (5.4 vs
-  // 5.1 TB/s on 16 x 40k).  Three workgroups of 4 KB batches also beat two
-  // and four.  The single launch uses the same shape (fused.hip), which
-  // keeps the two paths' results identical without a supplied LSE.  Wider
-  // heads and the head max keep two workgroups per CU: their registers do
-  // not fit three.
+  // 4 x 128k, and both beat 16 KB batches at two workgroups per CU (5.4 vs
+  // 5.1 TB/s on 16 x 40k); three workgroups also beat four.  At head_dim 64
+  // two groups (4 KB) beat four (8 KB) by 2.1-2.9 us and one (2 KB) by
+  // 1.4-3.7 us on the same rows.  The single launch uses the same shape
+  // (fused.hip), which keeps the two paths' results identical without a
+  // supplied LSE.  Wider heads and the head max keep two workgroups per CU:
+  // their registers do not fit three.
   constexpr bool narrow = !HMAX && STEPS <= 4;
-  constexpr int KB = narrow ? (STEPS <= 2 ? 4 : 1) : ((16 / STEPS) >= 4 ? 4 : ((16 / STEPS) >= 2 ? 2 : 1));
+  constexpr int KB = narrow ? (STEPS <= 2 ? 2 : 1) : ((16 / STEPS) >= 4 ? 4 : ((16 / STEPS) >= 2 ? 2 : 1));
   constexpr int WGS = narrow ? 3 : 2;
   const int64_t cap = static_cast<int64_t>(device_cu_count()) * WGS;
   const int grid = static_cast<int>(std::max<int64_t>(1, std::min(upper_blocks, cap)));

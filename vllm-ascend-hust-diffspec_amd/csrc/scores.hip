@@ -210,10 +210,13 @@ void launch_kb(hipStream_t stream, const ScoreArgs& a, int64_t upper_blocks, int
   // two groups (4 KB) beat four (8 KB) by 2.1-2.9 us and one (2 KB) by
   // 1.4-3.7 us on the same rows.  The single launch uses the same shape
   // (fused.hip), which keeps the two paths' results identical without a
-  // supplied LSE.  Wider heads and the head max keep two workgroups per CU:
-  // their registers do not fit three.
+  // supplied LSE.  Wider heads read one group per batch (8 KB at head_dim
+  // 256: 1-2 us faster than two groups on 16 rows of 4k-40k tokens) at two
+  // workgroups per CU (three measured slower); the head max keeps its wider
+  // batches at two workgroups per CU.
   constexpr bool narrow = !HMAX && STEPS <= 4;
-  constexpr int KB = narrow ? (STEPS <= 2 ? 2 : 1) : ((16 / STEPS) >= 4 ? 4 : ((16 / STEPS) >= 2 ? 2 : 1));
+  constexpr int KB = narrow ? (STEPS <= 2 ? 2 : 1)
+                            : (HMAX ? ((16 / STEPS) >= 4 ? 4 : ((16 / STEPS) >= 2 ? 2 : 1)) : 1);
   constexpr int WGS = narrow ? 3 : 2;
   const int64_t cap = static_cast<int64_t>(device_cu_count()) * WGS;
   const int grid = static_cast<int>(std::max<int64_t>(1, std::min(upper_blocks, cap)));

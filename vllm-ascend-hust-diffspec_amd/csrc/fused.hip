@@ -100,7 +100,12 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kSelectors = 16;     // selecting workgroups (fewer when the batch has fewer rows)
+// Row selectors (fewer when the batch has fewer rows).  8 against 16, events
+// around each launch, two rounds: 16 rows of 4k-40k tokens 82.5-82.7 against
+// 82.8-83.4 us (other seeds 0.3-1.4 us faster), 16 x 40k 156.2-156.4
+// against 157.1-157.6 us, 64 rows equal or faster.  A selector's rows
+// complete tens of microseconds apart, and the freed slots score.
+constexpr int kSelectors = 8;
 // Without a supplied LSE: workgroups doing the KV groups' shares, below the
 // row selectors.  Measured on 16 rows of 4k-40k tokens (one step): 32 group
 // workgroups 96.6-98.3 us; 16 of them 101.9 us; 32 with the last group's

@@ -104,7 +104,9 @@ constexpr int kWaves = kThreads / 64;
 // around each launch, two rounds: 16 rows of 4k-40k tokens 82.5-82.7 against
 // 82.8-83.4 us (other seeds 0.3-1.4 us faster), 16 x 40k 156.2-156.4
 // against 157.1-157.6 us, 64 rows equal or faster.  A selector's rows
-// complete tens of microseconds apart, and the freed slots score.
+// complete tens of microseconds apart, and the freed slots score.  4
+// selectors: 0.5-0.9 us slower on the first draw, up to 1 us faster on
+// others; 2: 25-45% slower on ragged rows (selections queue).
 constexpr int kSelectors = 8;
 // Without a supplied LSE: workgroups doing the KV groups' shares, below the
 // row selectors.  Measured on 16 rows of 4k-40k tokens (one step): 32 group

@@ -152,6 +152,8 @@ def test_expired_wait_stays_with_its_launch(cuda):
     (23, 8, 20000, 40000, dict(chunk=32, token_budget=1024)),
     (24, 10, 500, 12000, dict(hq=64, hkv=8, head_dim=64, block_size=64)),
     (25, 9, 1000, 8000, dict(hq=16, hkv=1, head_dim=64, dtype=torch.float16)),
+    (28, 9, 600, 9000, dict(hq=12, hkv=4, head_dim=64)),
+    (29, 8, 800, 7000, dict(hq=28, hkv=4)),
 ])
 def test_lse_free_single_launch_equals_chain(cuda, seed, rows, lo, hi, kw):
     """Without a supplied LSE the single launch's selectors merge each row's mass
@@ -160,7 +162,8 @@ def test_lse_free_single_launch_equals_chain(cuda, seed, rows, lo, hi, kw):
     oracle with the exact LSE.  Shapes: the headline's (ragged, 8 query heads per
     KV head); groups of 6 (three phases of two heads); 1250-chunk rows in
     32-token chunks (several load rounds per group and several chunk blocks);
-    64 query heads (two rounds of words per chunk); one KV head of 16 in fp16."""
+    64 query heads (two rounds of words per chunk); one KV head of 16 in fp16;
+    odd groups of 3 and 7 (one head per thread, 8-byte word reads)."""
     from oracle import diffspec_oracle as O
 
     case = _ragged(seed, rows, lo, hi, **kw)

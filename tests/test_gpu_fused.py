@@ -154,6 +154,7 @@ def test_expired_wait_stays_with_its_launch(cuda):
     (25, 9, 1000, 8000, dict(hq=16, hkv=1, head_dim=64, dtype=torch.float16)),
     (28, 9, 600, 9000, dict(hq=12, hkv=4, head_dim=64)),
     (29, 8, 800, 7000, dict(hq=28, hkv=4)),
+    (30, 8, 500, 6000, dict(hq=16, hkv=2, head_dim=64, chunk=48, token_budget=1536, block_size=64)),
 ])
 def test_lse_free_single_launch_equals_chain(cuda, seed, rows, lo, hi, kw):
     """Without a supplied LSE the single launch's selectors merge each row's mass
@@ -163,7 +164,8 @@ def test_lse_free_single_launch_equals_chain(cuda, seed, rows, lo, hi, kw):
     KV head); groups of 6 (three phases of two heads); 1250-chunk rows in
     32-token chunks (several load rounds per group and several chunk blocks);
     64 query heads (two rounds of words per chunk); one KV head of 16 in fp16;
-    odd groups of 3 and 7 (one head per thread, 8-byte word reads)."""
+    odd groups of 3 and 7 (one head per thread, 8-byte word reads); 48-token
+    chunks at head_dim 64 (three 16-token groups per unit, two per batch)."""
     from oracle import diffspec_oracle as O
 
     case = _ragged(seed, rows, lo, hi, **kw)

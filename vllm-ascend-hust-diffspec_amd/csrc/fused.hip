@@ -17,9 +17,8 @@
 // cache write-back on either side:
 //   - a score partial is stored as (tag << 32) | fp32 bits.  `tag` is unique
 //     to the launch, so stale values of earlier launches never match.  A
-//     selector first polls one sentinel, the partial of the row's newest
-//     chunk and last KV head (written in the row's last round of units),
-//     then reads the row's partials until all carry the tag;
+//     selector reads the row's partials, 16 per thread at a time, until all
+//     carry the tag;
 //   - without a supplied LSE (the LSEFREE kernel) the scoring waves store a
 //     mass word per (chunk, query head) instead, tagged the same way, in the
 //     caller's lse_partials.  Group workgroups, one per (row slot, KV
@@ -41,8 +40,11 @@
 // Polling is the costly part of this design: every poll is a device-scope
 // request to one memory channel, and thousands of waves polling one line
 // slow every stream that shares the channel.  So each row's tagged plan has
-// lines of its own, polls sleep between tries, and a selector reads its full
-// row only after the sentinel arrived.
+// lines of its own and polls sleep between tries.  The row selectors (at
+// most kSelectors, each on one row at a time) poll their rows' partials
+// whole: at most kSelectors rows of partials per round trip (8 KB for a
+// 16k-token row with 4 KV heads), and no round trip for a sentinel word
+// between the row's last partial and its selection.
 //
 // Forward progress does not depend on all workgroups being resident at once
 // (the launch is an ordinary one).  Workgroups are dispatched in index order
@@ -424,7 +426,6 @@ __device__ __forceinline__ void select_row(const FusedArgs& f, int b, uint32_t t
     const int N = C - 1;
     const bool in_lds = C > K && N <= kFusedKeys;
     const uint64_t* part = f.s.tagged + static_cast<int64_t>(b) * a.max_chunks * a.hkv;
-    if (C > 0) wait_sentinel(part + static_cast<int64_t>(C) * a.hkv - 1, tag, f.header);
     const int per_poll = kPollLoads / a.hkv;  // chunks per thread and poll
     uint32_t kmin = ~0u, kmax = 0u;           // bounds of this thread's candidate keys
     for (int base = 0; base < C; base += per_poll * kThreads) {

@@ -46,6 +46,15 @@ def test_fused_equals_chain_bitwise(cuda):
     _same(chain, fused)
 
 
+def test_fused_rows_longer_than_one_poll_round(cuda):
+    """Rows of 1031-1250 chunks: each selector reads its row's partials in rounds of 1024
+    chunks while the scoring waves are still writing the later ones."""
+    case = _ragged(31, 8, 33000, 40000, chunk=32, token_budget=1024)
+    chain = run_gpu(case, cuda, path="chain")
+    fused = run_gpu(case, cuda, path="fused")
+    _same(chain, fused)
+
+
 def test_fused_repeated_launches_and_reused_workspace(cuda):
     """Three launches on one workspace, then another batch shape and layout in the same bytes."""
     from ds355 import step

@@ -55,6 +55,21 @@ def test_fused_rows_longer_than_one_poll_round(cuda):
     _same(chain, fused)
 
 
+@pytest.mark.parametrize("seed,kw", [
+    (32, dict(block_size=48)),
+    (33, dict(hq=24, hkv=6, head_dim=64, block_size=80)),
+])
+def test_fused_pages_not_a_power_of_two(cuda, seed, kw):
+    """Block sizes (48, 80) or KV head counts (6) that are not powers of two: the single
+    launch's scoring resolves pages by division instead of shifts.  Oracle parity and the
+    chain's bytes."""
+    case = _ragged(seed, 10, 500, 9000, **kw)
+    fused = run_gpu(case, cuda, path="fused")
+    check_step(case, fused)
+    chain = run_gpu(case, cuda, path="chain")
+    _same(chain, fused)
+
+
 def test_fused_repeated_launches_and_reused_workspace(cuda):
     """Three launches on one workspace, then another batch shape and layout in the same bytes."""
     from ds355 import step

@@ -179,6 +179,8 @@ def test_expired_wait_stays_with_its_launch(cuda):
     (28, 9, 600, 9000, dict(hq=12, hkv=4, head_dim=64)),
     (29, 8, 800, 7000, dict(hq=28, hkv=4)),
     (30, 8, 500, 6000, dict(hq=16, hkv=2, head_dim=64, chunk=48, token_budget=1536, block_size=64)),
+    (34, 9, 600, 9000, dict(block_size=48)),
+    (35, 9, 600, 9000, dict(hq=24, hkv=6, head_dim=64, block_size=80, dtype=torch.float16)),
 ])
 def test_lse_free_single_launch_equals_chain(cuda, seed, rows, lo, hi, kw):
     """Without a supplied LSE the single launch's selectors merge each row's mass
@@ -189,7 +191,8 @@ def test_lse_free_single_launch_equals_chain(cuda, seed, rows, lo, hi, kw):
     32-token chunks (several load rounds per group and several chunk blocks);
     64 query heads (two rounds of words per chunk); one KV head of 16 in fp16;
     odd groups of 3 and 7 (one head per thread, 8-byte word reads); 48-token
-    chunks at head_dim 64 (three 16-token groups per unit, two per batch)."""
+    chunks at head_dim 64 (three 16-token groups per unit, two per batch); blocks
+    of 48 and 80 tokens and 6 KV heads in fp16 (pages resolved by division)."""
     from oracle import diffspec_oracle as O
 
     case = _ragged(seed, rows, lo, hi, **kw)

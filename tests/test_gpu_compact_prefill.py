@@ -128,6 +128,8 @@ CASES = [
     (64, 1024, 128, 2, 96, 96, True, torch.bfloat16),  # 6 lanes per position: lanes 60..63 idle
     (8, 2048, 8, 2, 64, 64, True, torch.bfloat16),     # 256 chunk ids per row: plan kernel + gather
     (64, 1024, 128, 2, 72, 72, True, torch.bfloat16),  # head_dim 72: plan kernel + scalar gather
+    (64, 1024, 128, 3, 128, 128, False, torch.float16),  # heads in pairs, then one alone
+    (32, 2048, 64, 7, 64, 64, True, torch.bfloat16),     # heads in fours, then three
 ]
 
 

@@ -29,6 +29,8 @@ def _run_batched(cache_k, cache_v, work_k, work_v, plan, cos_sin, chunk, width, 
     (4, 256, 256, True),
     (4, 256, 128, True),
     (2, 128, 64, False),
+    (3, 128, 128, True),   # heads in pairs, then one alone
+    (5, 64, 64, False),    # heads in fours, then one alone
 ])
 @pytest.mark.parametrize("slots", [[0, 1], [2, 0]])
 def test_batched_rebuild_matches_per_request_path(cuda, heads, dim, rotary_dim, neox, slots):

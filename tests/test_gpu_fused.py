@@ -104,6 +104,15 @@ def test_unsupported_shape_with_workspace_runs_chain(cuda):
     _same(chain, state)
 
 
+def test_pages_not_a_multiple_of_16_run_chain(cuda):
+    """40-token blocks: a 16-token group can straddle two blocks, so scoring looks up
+    each lane's page.  The single launch does not take such pages: the same call runs
+    the chain, leaves the epoch, and matches the oracle."""
+    case = _ragged(36, 9, 500, 6000, block_size=40)
+    state = run_gpu(case, cuda, path="fused", single_launch=False)
+    check_step(case, state)
+
+
 def test_small_batch_with_workspace_runs_chain(cuda):
     """Below 8 rows the chain is faster; the same call runs it and leaves the epoch."""
     case = _ragged(15, 3, 2000, 9000)

@@ -75,7 +75,7 @@ def test_zero_keys_give_uniform_mass(cuda):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("head_dim,chunk,block_size", [(128, 64, 128), (64, 32, 16), (128, 128, 256), (96, 48, 64),
-                                                       (64, 48, 64)])
+                                                       (64, 48, 64), (128, 64, 40), (64, 32, 8)])
 def test_ragged_batch_matches_oracle(cuda, dtype, head_dim, chunk, block_size):
     g = gen(3)
     hq, hkv = 32, 4
@@ -142,7 +142,7 @@ def test_reference_validation_messages(cuda):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("head_dim,chunk,block_size", [(128, 64, 128), (64, 32, 16), (128, 128, 256), (96, 48, 64),
-                                                       (256, 16, 1024), (64, 48, 64)])
+                                                       (256, 16, 1024), (64, 48, 64), (128, 64, 40)])
 @pytest.mark.parametrize("hq,hkv", [(32, 4), (12, 2), (16, 1), (12, 4)])
 def test_lse_free_ragged_batch_matches_oracle(cuda, dtype, head_dim, chunk, block_size, hq, hkv):
     g = gen(11)

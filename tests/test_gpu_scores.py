@@ -90,15 +90,20 @@ def test_ragged_batch_matches_oracle(cuda, dtype, head_dim, chunk, block_size):
     assert_scores_close(actual, expected)
 
 
-def test_head_reduce_max_matches_oracle(cuda):
+@pytest.mark.parametrize("head_dim,chunk,block_size,dtype", [
+    (128, 64, 64, torch.bfloat16),
+    (64, 32, 40, torch.float16),     # pages looked up per lane
+    (256, 128, 48, torch.bfloat16),  # pages by division, wide heads
+])
+def test_head_reduce_max_matches_oracle(cuda, head_dim, chunk, block_size, dtype):
     g = gen(4)
-    lengths = [3000, 777, 64]
-    query = randn((3, 32, 128), torch.bfloat16, g)
-    key_cache, table = paged_keys(lengths, 4, 128, 64, torch.bfloat16, g)
-    scale = default_scale(128)
+    lengths = [3000, 777, 64, chunk + 1]
+    query = randn((len(lengths), 32, head_dim), dtype, g)
+    key_cache, table = paged_keys(lengths, 4, head_dim, block_size, dtype, g)
+    scale = default_scale(head_dim)
     lse = lse_for(query, key_cache, table, lengths, scale)
-    actual = _gpu_scores(query, key_cache, lse, table, lengths, 64, scale, cuda, head_reduce="max")
-    expected = O.paged_chunk_attention_scores(query, key_cache, lse, table, torch.tensor(lengths), chunk_size=64,
+    actual = _gpu_scores(query, key_cache, lse, table, lengths, chunk, scale, cuda, head_reduce="max")
+    expected = O.paged_chunk_attention_scores(query, key_cache, lse, table, torch.tensor(lengths), chunk_size=chunk,
                                               max_seq_len=max(lengths), scale=scale, head_reduce="max")
     assert_scores_close(actual, expected)
 
